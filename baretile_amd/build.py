@@ -1,0 +1,39 @@
+"""Builds libbaretile_amd.so from csrc/*.hip with hipcc for gfx950, in the package directory.
+
+`python -m baretile_amd.build` or build() from Python. The library is one shared object with a C ABI
+(include/baretile_amd.h), loaded by baretile_amd._lib with ctypes.
+"""
+import glob, os, subprocess, sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "libbaretile_amd.so")
+SOURCES = sorted(glob.glob(os.path.join(HERE, "csrc", "*.hip")))
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-shared", "-fPIC",
+         # packed fp32 adds and multiplies stay out of the device code (hipcc's host pass warns that it doesn't know
+         # the feature, which is harmless)
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         "-Wno-unused-result", "-I", os.path.join(os.path.dirname(HERE), "include")]
+
+
+def hipcc():
+  for c in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
+    if c and (os.path.isabs(c) and os.path.exists(c) or not os.path.isabs(c)): return c
+  raise RuntimeError("hipcc not found")
+
+
+def build(verbose=False):
+  """Compile every source into LIB (a temporary name first, so a failed build leaves the old library)."""
+  tmp = LIB + ".tmp"
+  cmd = [hipcc(), *FLAGS, "-o", tmp, *SOURCES]
+  if verbose: print(" ".join(cmd), flush=True)
+  p = subprocess.run(cmd, capture_output=True, text=True)
+  errors = [l for l in (p.stdout + p.stderr).splitlines() if "packed-fp32-ops" not in l and l.strip()]
+  if p.returncode != 0:
+    raise RuntimeError("hipcc failed:\n" + "\n".join(errors[-60:]))
+  if verbose and errors: print("\n".join(errors[-40:]))
+  os.replace(tmp, LIB)
+  return LIB
+
+
+if __name__ == "__main__":
+  print(build(verbose="-v" in sys.argv))

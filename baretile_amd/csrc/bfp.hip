@@ -1,0 +1,267 @@
+// Block floats on the GPU: the cast into the plain planes, the exact unpacker, and the one-time repack into the
+// columns tiles that the matmul kernels read.
+//
+// Rules (restated from the reference, in code of our own):
+//   cast   models/gpt2.py:19-30, kernels.py:1074-1081 (NIBBLE), kernels.py:1108-1114 (put's bfp8 rule): round to bf16
+//          (nearest even), take the run's largest exponent field `top`, keep 7 (bfp8) or 3 (bfp4) bits of magnitude
+//          below it, rounding half up (bfp8) or to nearest with ties up (bfp4), saturating at 127 / 7. A zero keeps no
+//          sign.
+//   decode tensor.py:1093-1104 (_bf16s): normalize the magnitude, exponent (e - shift) mod 256.
+#include "common.h"
+
+namespace bt {
+
+// One thread a run: 16 values of one row sharing an exponent. Runs are numbered along rows, so neighbouring threads
+// read neighbouring 32-byte pieces of a bf16 row.
+template <int FMT>
+__global__ void __launch_bounds__(256) pack_kernel(const void *src, int src_dtype, int64_t batch, int64_t rows,
+                                                   int64_t cols, int64_t sb, int64_t sr, int64_t sc, uint8_t *exps,
+                                                   uint8_t *vals) {
+  int64_t runs = (cols + 15) / 16;
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= batch * rows * runs) return;
+  int64_t j = t % runs, r = t / runs % rows, b = t / runs / rows;
+  uint32_t bits[16];
+  uint32_t top = 0;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    int64_t c = j * 16 + i;
+    uint32_t v = 0;
+    if (c < cols) {
+      int64_t at = b * sb + r * sr + c * sc;
+      v = src_dtype == BT_BF16 ? ((const uint16_t *)src)[at] : bf16_rne(((const float *)src)[at]);
+    }
+    bits[i] = v;
+    top = max(top, (v >> 7) & 255u);
+  }
+  exps[t] = (uint8_t)top;
+  if (FMT == BT_BFP8) {
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 16; i++) w[i / 4] |= ((uint32_t)bfp_signed<8>(bits[i], top) & 255u) << (8 * (i % 4));
+    *(uint4 *)(vals + t * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    uint32_t w[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 16; i++) w[i / 8] |= ((uint32_t)bfp_signed<4>(bits[i], top) & 15u) << (4 * (i % 8));
+    *(uint2 *)(vals + t * 8) = make_uint2(w[0], w[1]);
+  }
+}
+
+// Signed q of value c in row r of matrix b of the plain planes.
+template <int FMT>
+__device__ __forceinline__ int plain_q(const uint8_t *vals, int64_t row_bytes, int64_t b_rows_r, int64_t c) {
+  if (FMT == BT_BFP8) return (int)(int8_t)vals[b_rows_r * row_bytes + c];
+  uint32_t byte = vals[b_rows_r * row_bytes + c / 2];
+  int nib = (int)((byte >> (4 * (c & 1))) & 15u);
+  return nib >= 8 ? nib - 16 : nib;
+}
+
+// One thread a value: bf16 bits exactly as the unpacker gives them.
+template <int FMT>
+__global__ void __launch_bounds__(256) unpack_kernel(const uint8_t *exps, const uint8_t *vals, int64_t batch,
+                                                     int64_t rows, int64_t cols, uint16_t *dst) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= batch * rows * cols) return;
+  int64_t c = t % cols, br = t / cols;  // br = b * rows + r
+  int64_t runs = (cols + 15) / 16, cols16 = runs * 16;
+  int q = plain_q<FMT>(vals, FMT == BT_BFP8 ? cols16 : cols16 / 2, br, c);
+  uint32_t e = exps[br * runs + c / 16];
+  dst[t] = (uint16_t)unpacked_bits(FMT == BT_BFP8 ? q : q * 16, e);
+}
+
+// Row of exponent byte p of a columns tile, and row of value j (of 8) for lane l, half h.
+__device__ __forceinline__ int tile_row_of_exp(int p) { return 32 * ((p >> 3) & 1) + 8 * (p >> 4) + (p & 7); }
+__device__ __forceinline__ int tile_row(int l, int h, int j) { return 32 * h + 8 * (l >> 4) + j; }
+
+// One block a columns tile, one thread a lane. Reads the plain planes, writes the tile.
+template <int FMT>
+__global__ void __launch_bounds__(64) columns_kernel(const uint8_t *exps, const uint8_t *vals, int64_t rows,
+                                                     int64_t cols, int64_t chunks, int64_t nruns, uint8_t *dst) {
+  constexpr int TB = FMT == BT_BFP8 ? 1088 : 576;
+  int64_t tile = blockIdx.x;  // (b * nruns + run) * chunks + chunk
+  int64_t chunk = tile % chunks, run = tile / chunks % nruns, b = tile / chunks / nruns;
+  int l = threadIdx.x;
+  int64_t runs = (cols + 15) / 16, cols16 = runs * 16;
+  uint8_t *out = dst + tile * TB;
+  {  // exponent byte l
+    int64_t k = chunk * 64 + tile_row_of_exp(l);
+    out[l] = k < rows ? exps[(b * rows + k) * runs + run] : 0;
+  }
+  int64_t n = run * 16 + (l & 15);
+  uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int h = 0; h < 2; h++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      int64_t k = chunk * 64 + tile_row(l, h, j);
+      int q = (k < rows && n < cols16) ? plain_q<FMT>(vals, FMT == BT_BFP8 ? cols16 : cols16 / 2, b * rows + k, n) : 0;
+      if (FMT == BT_BFP8) w[(h * 8 + j) / 4] |= ((uint32_t)q & 255u) << (8 * (j % 4));
+      else w[h] |= ((uint32_t)q & 15u) << (4 * j);
+    }
+  if (FMT == BT_BFP8) *(uint4 *)(out + 64 + 16 * l) = make_uint4(w[0], w[1], w[2], w[3]);
+  else *(uint2 *)(out + 64 + 8 * l) = make_uint2(w[0], w[1]);
+}
+
+__global__ void __launch_bounds__(64) bf16_columns_kernel(const uint16_t *src, int64_t rows, int64_t cols, int64_t sb,
+                                                          int64_t sr, int64_t sc, int64_t chunks, int64_t nruns,
+                                                          uint16_t *dst) {
+  int64_t tile = blockIdx.x;
+  int64_t chunk = tile % chunks, run = tile / chunks % nruns, b = tile / chunks / nruns;
+  int l = threadIdx.x;
+  int64_t n = run * 16 + (l & 15);
+  uint32_t w[8];
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    uint32_t pair = 0;
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      int h = (i + u) / 8, j = (i + u) % 8;
+      int64_t k = chunk * 64 + tile_row(l, h, j);
+      uint32_t v = (k < rows && n < cols) ? src[b * sb + k * sr + n * sc] : 0;
+      pair |= v << (16 * u);
+    }
+    w[i / 2] = pair;
+  }
+  uint4 *out = (uint4 *)(dst + tile * 1024 + 16 * l);
+  out[0] = make_uint4(w[0], w[1], w[2], w[3]);
+  out[1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
+// One thread a value of the result: finds it in its tile, decodes it exactly.
+template <int FMT>
+__global__ void __launch_bounds__(256) columns_unpack_kernel(const uint8_t *src, int64_t batch, int64_t rows,
+                                                             int64_t cols, int64_t chunks, int64_t nruns,
+                                                             uint16_t *dst) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= batch * rows * cols) return;
+  int64_t n = t % cols, k = t / cols % rows, b = t / cols / rows;
+  int64_t run = n / 16, chunk = k / 64;
+  int kk = (int)(k % 64), h = kk / 32, g = (kk % 32) / 8, j = kk % 8, l = g * 16 + (int)(n % 16);
+  int64_t tile = (b * nruns + run) * chunks + chunk;
+  if (FMT == BT_BF16) {
+    dst[t] = ((const uint16_t *)src)[tile * 1024 + 16 * l + 8 * h + j];
+    return;
+  }
+  constexpr int TB = FMT == BT_BFP8 ? 1088 : 576;
+  const uint8_t *tp = src + tile * TB;
+  uint32_t e = tp[16 * g + 8 * h + j];
+  int q;
+  if (FMT == BT_BFP8) q = (int)(int8_t)tp[64 + 16 * l + 8 * h + j];
+  else {
+    int nib = (tp[64 + 8 * l + 4 * h + j / 2] >> (4 * (j & 1))) & 15;
+    q = (nib >= 8 ? nib - 16 : nib) * 16;
+  }
+  dst[t] = (uint16_t)unpacked_bits(q, e);
+}
+
+static int check_fmt(int fmt) {
+  if (fmt != BT_BFP8 && fmt != BT_BFP4) return fail(BT_EINVAL, "block-float format must be bfp8 or bfp4, not %d", fmt);
+  return BT_OK;
+}
+
+static int check_shape(int64_t batch, int64_t rows, int64_t cols) {
+  if (batch <= 0 || rows <= 0 || cols <= 0)
+    return fail(BT_EINVAL, "shape %lld x %lld x %lld must be positive", (long long)batch, (long long)rows,
+                (long long)cols);
+  return BT_OK;
+}
+
+static unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
+
+}  // namespace bt
+
+using namespace bt;
+
+extern "C" {
+
+int bt_bfp_pack(bt_runtime *rt, int fmt, uint64_t src, int src_dtype, int64_t batch, int64_t rows, int64_t cols,
+                int64_t sb, int64_t sr, int64_t sc, uint64_t exps, uint64_t vals) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (int s = check_fmt(fmt)) return s;
+  if (int s = check_shape(batch, rows, cols)) return s;
+  if (src_dtype != BT_BF16 && src_dtype != BT_FP32) return fail(BT_EINVAL, "a block float is cast from bf16 or fp32");
+  if (vals % 16) return fail(BT_EINVAL, "the value plane must be 16-byte aligned");
+  int64_t n = batch * rows * ((cols + 15) / 16);
+  if (fmt == BT_BFP8)
+    pack_kernel<BT_BFP8><<<blocks_for(n, 256), 256, 0, r->stream>>>((const void *)src, src_dtype, batch, rows, cols,
+                                                                     sb, sr, sc, (uint8_t *)exps, (uint8_t *)vals);
+  else
+    pack_kernel<BT_BFP4><<<blocks_for(n, 256), 256, 0, r->stream>>>((const void *)src, src_dtype, batch, rows, cols,
+                                                                     sb, sr, sc, (uint8_t *)exps, (uint8_t *)vals);
+  BT_LAUNCHED("bfp_pack");
+  return BT_OK;
+}
+
+int bt_bfp_unpack(bt_runtime *rt, int fmt, uint64_t exps, uint64_t vals, int64_t batch, int64_t rows, int64_t cols,
+                  uint64_t dst) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (int s = check_fmt(fmt)) return s;
+  if (int s = check_shape(batch, rows, cols)) return s;
+  int64_t n = batch * rows * cols;
+  if (fmt == BT_BFP8)
+    unpack_kernel<BT_BFP8><<<blocks_for(n, 256), 256, 0, r->stream>>>((const uint8_t *)exps, (const uint8_t *)vals,
+                                                                       batch, rows, cols, (uint16_t *)dst);
+  else
+    unpack_kernel<BT_BFP4><<<blocks_for(n, 256), 256, 0, r->stream>>>((const uint8_t *)exps, (const uint8_t *)vals,
+                                                                       batch, rows, cols, (uint16_t *)dst);
+  BT_LAUNCHED("bfp_unpack");
+  return BT_OK;
+}
+
+int bt_bfp_columns(bt_runtime *rt, int fmt, uint64_t exps, uint64_t vals, int64_t batch, int64_t rows, int64_t cols,
+                   uint64_t dst) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (int s = check_fmt(fmt)) return s;
+  if (int s = check_shape(batch, rows, cols)) return s;
+  if (dst % 16) return fail(BT_EINVAL, "columns tiles must be 16-byte aligned");
+  int64_t chunks = (rows + 63) / 64, nruns = (cols + 15) / 16, tiles = batch * nruns * chunks;
+  if (tiles >= (1ll << 31)) return fail(BT_EINVAL, "too many tiles");
+  if (fmt == BT_BFP8)
+    columns_kernel<BT_BFP8><<<(unsigned)tiles, 64, 0, r->stream>>>((const uint8_t *)exps, (const uint8_t *)vals, rows,
+                                                                    cols, chunks, nruns, (uint8_t *)dst);
+  else
+    columns_kernel<BT_BFP4><<<(unsigned)tiles, 64, 0, r->stream>>>((const uint8_t *)exps, (const uint8_t *)vals, rows,
+                                                                    cols, chunks, nruns, (uint8_t *)dst);
+  BT_LAUNCHED("bfp_columns");
+  return BT_OK;
+}
+
+int bt_bf16_columns(bt_runtime *rt, uint64_t src, int64_t batch, int64_t rows, int64_t cols, int64_t sb, int64_t sr,
+                    int64_t sc, uint64_t dst) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (int s = check_shape(batch, rows, cols)) return s;
+  if (dst % 16) return fail(BT_EINVAL, "columns tiles must be 16-byte aligned");
+  int64_t chunks = (rows + 63) / 64, nruns = (cols + 15) / 16, tiles = batch * nruns * chunks;
+  if (tiles >= (1ll << 31)) return fail(BT_EINVAL, "too many tiles");
+  bf16_columns_kernel<<<(unsigned)tiles, 64, 0, r->stream>>>((const uint16_t *)src, rows, cols, sb, sr, sc, chunks,
+                                                              nruns, (uint16_t *)dst);
+  BT_LAUNCHED("bf16_columns");
+  return BT_OK;
+}
+
+int bt_columns_unpack(bt_runtime *rt, int fmt, uint64_t src, int64_t batch, int64_t rows, int64_t cols,
+                      uint64_t dst) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (fmt != BT_BF16 && fmt != BT_BFP8 && fmt != BT_BFP4) return fail(BT_EINVAL, "columns format %d", fmt);
+  if (int s = check_shape(batch, rows, cols)) return s;
+  int64_t chunks = (rows + 63) / 64, nruns = (cols + 15) / 16, n = batch * rows * cols;
+  if (fmt == BT_BF16)
+    columns_unpack_kernel<BT_BF16><<<blocks_for(n, 256), 256, 0, r->stream>>>((const uint8_t *)src, batch, rows, cols,
+                                                                               chunks, nruns, (uint16_t *)dst);
+  else if (fmt == BT_BFP8)
+    columns_unpack_kernel<BT_BFP8><<<blocks_for(n, 256), 256, 0, r->stream>>>((const uint8_t *)src, batch, rows, cols,
+                                                                               chunks, nruns, (uint16_t *)dst);
+  else
+    columns_unpack_kernel<BT_BFP4><<<blocks_for(n, 256), 256, 0, r->stream>>>((const uint8_t *)src, batch, rows, cols,
+                                                                               chunks, nruns, (uint16_t *)dst);
+  BT_LAUNCHED("columns_unpack");
+  return BT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,82 @@
+// Shared definitions of the baretile_amd HIP library: status codes, the per-thread error text, and the number rules
+// that every kernel applies (bf16 rounding, block-float fields). gfx950 only.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cstdio>
+#include <cstdarg>
+#include "../../include/baretile_amd.h"
+
+namespace bt {
+
+// The last error's text, per host thread. Set by fail(), read through bt_last_error().
+void set_error(const char *fmt, ...);
+// fail(BT_EINVAL, "...") records the message and returns the code, so entry points can `return fail(...)`.
+int fail(int code, const char *fmt, ...);
+
+#define BT_HIP(call)                                                                                           \
+  do {                                                                                                         \
+    hipError_t e_ = (call);                                                                                    \
+    if (e_ != hipSuccess) return ::bt::fail(e_ == hipErrorOutOfMemory ? BT_ENOMEM : BT_ESTATE, "%s: %s (%s:%d)", \
+                                            #call, hipGetErrorString(e_), __FILE__, __LINE__);                  \
+  } while (0)
+
+// A launch's own error, read right after the <<<>>> so a bad configuration names its kernel.
+#define BT_LAUNCHED(name)                                                                                      \
+  do {                                                                                                         \
+    hipError_t e_ = hipGetLastError();                                                                         \
+    if (e_ != hipSuccess) return ::bt::fail(BT_ESTATE, "launching %s: %s", name, hipGetErrorString(e_));       \
+  } while (0)
+
+struct Runtime {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipStream_t capture_origin = nullptr;  // non-null while bt_graph_begin has the stream in capture
+  int closed = 0;
+};
+
+// Checks a runtime handle and makes its device current.
+int enter(bt_runtime *rt, Runtime **out);
+
+inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+// ---- number rules (device) -------------------------------------------------------------------------------------
+
+// fp32 -> bf16 bits, round to nearest even, no NaN special case: the host upload rule and the bfp cast's first step.
+__device__ __forceinline__ uint32_t bf16_rne(float x) {
+  uint32_t b = __float_as_uint(x);
+  return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+// fp32 -> bf16 bits, round half up in magnitude: how a computed bf16 result is packed.
+__device__ __forceinline__ uint32_t bf16_packed(float x) { return (__float_as_uint(x) + 0x8000u) >> 16; }
+__device__ __forceinline__ float bf16_value(uint32_t bits) { return __uint_as_float(bits << 16); }
+// A value rounded the way a bf16 kernel rounds each result it computes.
+__device__ __forceinline__ float round_packed(float x) { return bf16_value(bf16_packed(x)); }
+
+// The block-float magnitude of one bf16 value below its run's largest exponent `top`: bfp8 keeps 7 bits rounded half
+// up, bfp4 3 bits rounded to nearest with ties up. The exponent gap saturates at 8, and the result at 127 / 7.
+template <int BITS>
+__device__ __forceinline__ int bfp_magnitude(uint32_t b, uint32_t top) {
+  uint32_t e = (b >> 7) & 255u, m = (b & 127u) | (e ? 128u : 0u);
+  uint32_t shift = min(top - e, 8u);
+  uint32_t q = BITS == 8 ? (m + (1u << shift)) >> (shift + 1) : (m + (16u << shift)) >> (shift + 5);
+  return (int)min(q, BITS == 8 ? 127u : 7u);
+}
+// The signed q of a value: the magnitude with the value's sign, and 0 without one.
+template <int BITS>
+__device__ __forceinline__ int bfp_signed(uint32_t b, uint32_t top) {
+  int q = bfp_magnitude<BITS>(b, top);
+  return (b >> 15) & 1u ? -q : q;
+}
+
+// The unpacker's exact bf16 bits for a signed magnitude q (|q| <= 127, bfp4's 3 bits already shifted up by 4) under
+// exponent byte e: the magnitude normalized, the exponent (e - shift) mod 256. q == 0 gives +0.
+__device__ __forceinline__ uint32_t unpacked_bits(int q, uint32_t e) {
+  if (q == 0) return 0;
+  uint32_t s = q < 0, mag = (uint32_t)(q < 0 ? -q : q);
+  uint32_t m = mag << 1;                       // 8 bits with the top one set once normalized
+  uint32_t shift = __clz(m) - 24;              // leading zeros within the byte
+  return s << 15 | ((e - shift) & 255u) << 7 | ((m << shift) & 0x7Eu);
+}
+
+}  // namespace bt

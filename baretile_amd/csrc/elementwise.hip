@@ -1,0 +1,217 @@
+// Fused elementwise programs, reductions, and the row gather and put that fill and read caches.
+#include "program.h"
+#include <algorithm>
+
+namespace bt {
+
+// A thread an element, in row-major order of the result.
+template <int DT>
+__global__ void __launch_bounds__(256) elementwise_kernel(const bt_program prog, int64_t batch, int64_t rows,
+                                                          int64_t cols, const bt_operand out) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t total = batch * rows * cols;
+  for (; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    int64_t c = t % cols, r = t / cols % rows, b = t / cols / rows;
+    uint32_t v = run_program<DT>(prog, b, r, c, 0);
+    store_value<DT>(out, operand_matrix(out, b) * out.sb + r * out.sr + c * out.sc, v);
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float w = __shfl_xor(v, o, 64);
+    v = (v != v || w != w) ? __builtin_nanf("") : fmaxf(v, w);
+  }
+  return v;
+}
+__device__ __forceinline__ int32_t wave_imax(int32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// A wavefront an output element. Lanes stride along the reduced axis; the wave combines their partial results.
+// Sums accumulate in fp32. With DT bf16 each program value is rounded first, as the reference's pack of the folded
+// operand is; the reduced value is rounded again when it is stored.
+template <int DT>
+__global__ void __launch_bounds__(256) reduce_kernel(const bt_program prog, int kind, int axis, int64_t batch,
+                                                     int64_t rows, int64_t cols, int64_t sweep, int64_t step,
+                                                     const bt_operand out) {
+  int lane = threadIdx.x & 63;
+  int64_t w = (int64_t)blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+  int64_t ob = axis == 0 ? batch / sweep : batch, orows = axis == 1 ? 1 : rows, ocols = axis == 2 ? 1 : cols;
+  if (w >= ob * orows * ocols) return;
+  int64_t c = w % ocols, r = w / ocols % orows, b = w / ocols / orows;
+  int64_t n = axis == 0 ? sweep : axis == 1 ? rows : cols;
+  int64_t base = axis == 0 ? (b / step) * step * sweep + b % step : 0;
+  float facc = kind == BT_REDUCE_SUM ? 0.0f : -__builtin_inff();
+  int32_t iacc = INT32_MIN;
+  for (int64_t i = lane; i < n; i += 64) {
+    int64_t bb = axis == 0 ? base + i * step : b, rr = axis == 1 ? i : r, cc = axis == 2 ? i : c;
+    uint32_t v = run_program<DT>(prog, bb, rr, cc, 0);
+    if (DT == BT_INT32) iacc = max(iacc, (int32_t)v);
+    else if (kind == BT_REDUCE_SUM) facc += __uint_as_float(v);
+    else {
+      float f = __uint_as_float(v);
+      facc = (f != f || facc != facc) ? __builtin_nanf("") : fmaxf(facc, f);
+    }
+  }
+  uint32_t res;
+  if (DT == BT_INT32) res = (uint32_t)wave_imax(iacc);
+  else res = __float_as_uint(kind == BT_REDUCE_SUM ? wave_sum(facc) : wave_max(facc));
+  if (lane == 0) {
+    if (DT == BT_BF16) res = __float_as_uint(round_packed(__uint_as_float(res)));
+    store_value<DT>(out, operand_matrix(out, b) * out.sb + r * out.sr + c * out.sc, res);
+  }
+}
+
+// A block a gathered row: 256 threads copy its 32-bit words (a bf16 row of odd width copies its last half word).
+__global__ void __launch_bounds__(256) gather_kernel(const uint8_t *table, int64_t rows, int64_t row_bytes,
+                                                     int64_t table_rstride_bytes, const int32_t *ids, uint8_t *out,
+                                                     int64_t out_rstride_bytes) {
+  int64_t i = blockIdx.x;
+  int32_t id = ids[i];
+  uint8_t *dst = out + i * out_rstride_bytes;
+  const uint8_t *src = table + (int64_t)id * table_rstride_bytes;
+  bool in = id >= 0 && id < rows;
+  for (int64_t at = threadIdx.x * 2; at < row_bytes; at += 2 * blockDim.x)
+    *(uint16_t *)(dst + at) = in ? *(const uint16_t *)(src + at) : 0;
+}
+
+// One block per (batch entry, column piece). Each block walks the n rows in order, so a later duplicate place
+// overwrites an earlier one, and no two blocks write the same element.
+__global__ void __launch_bounds__(256) put_kernel(uint8_t *dst, int64_t dst_rows, int64_t row_bytes, int64_t dst_sb,
+                                                  int64_t dst_sr, const int32_t *ids, int64_t n, const uint8_t *x,
+                                                  int64_t x_sb, int64_t x_sr, int64_t pieces) {
+  int64_t b = blockIdx.x / pieces, piece = blockIdx.x % pieces;
+  int64_t at = (piece * blockDim.x + threadIdx.x) * 2;
+  if (at >= row_bytes) return;
+  for (int64_t i = 0; i < n; i++) {
+    int32_t p = ids[i];
+    if (p < 0 || p >= dst_rows) continue;
+    *(uint16_t *)(dst + b * dst_sb + p * dst_sr + at) = *(const uint16_t *)(x + b * x_sb + i * x_sr + at);
+  }
+}
+
+static int check_program(const bt_program *prog) {
+  if (!prog) return fail(BT_EINVAL, "no program");
+  if (prog->n_inst < 0 || prog->n_inst > BT_MAX_INST)
+    return fail(BT_EINVAL, "a program has at most %d instructions, not %d", BT_MAX_INST, prog->n_inst);
+  if (prog->n_inputs < 0 || prog->n_inputs > BT_MAX_INPUTS)
+    return fail(BT_EINVAL, "a program has at most %d inputs, not %d", BT_MAX_INPUTS, prog->n_inputs);
+  if (prog->dtype != BT_BF16 && prog->dtype != BT_FP32 && prog->dtype != BT_INT32)
+    return fail(BT_EINVAL, "a program computes in bf16, fp32 or int32, not %d", prog->dtype);
+  if (prog->result < 0 || prog->result >= BT_MAX_REGS) return fail(BT_EINVAL, "result register %d", prog->result);
+  for (int i = 0; i < prog->n_inst; i++) {
+    const bt_inst &in = prog->inst[i];
+    if (in.op >= BT_OP_COUNT) return fail(BT_EINVAL, "instruction %d: unknown op %d", i, in.op);
+    if (in.dst >= BT_MAX_REGS || in.a >= BT_MAX_REGS || in.b >= BT_MAX_REGS || in.c >= BT_MAX_REGS)
+      return fail(BT_EINVAL, "instruction %d: register out of range", i);
+    if (in.op == BT_OP_LOAD && in.a >= prog->n_inputs) return fail(BT_EINVAL, "instruction %d loads input %d", i, in.a);
+  }
+  for (int i = 0; i < prog->n_inputs; i++) {
+    const bt_operand &o = prog->in[i];
+    if (!o.ptr) return fail(BT_EINVAL, "input %d has no address", i);
+    if (o.rep < 1 || o.cyc < 0) return fail(BT_EINVAL, "input %d: rep %d, cyc %d", i, o.rep, o.cyc);
+    if (o.dtype != BT_BF16 && o.dtype != BT_FP32 && o.dtype != BT_INT32)
+      return fail(BT_EINVAL, "input %d: dtype %d", i, o.dtype);
+  }
+  return BT_OK;
+}
+
+int check_out(const bt_operand *out) {
+  if (!out || !out->ptr) return fail(BT_EINVAL, "no output");
+  if (out->dtype != BT_BF16 && out->dtype != BT_FP32 && out->dtype != BT_INT32)
+    return fail(BT_EINVAL, "output dtype %d", out->dtype);
+  if (out->rep < 1 || out->cyc < 0) return fail(BT_EINVAL, "output rep %d, cyc %d", out->rep, out->cyc);
+  return BT_OK;
+}
+
+int validate_program(const bt_program *prog) { return check_program(prog); }
+
+}  // namespace bt
+
+using namespace bt;
+
+extern "C" {
+
+int bt_elementwise(bt_runtime *rt, const bt_program *prog, int64_t batch, int64_t rows, int64_t cols,
+                   const bt_operand *out) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (int s = check_program(prog)) return s;
+  if (int s = check_out(out)) return s;
+  if (batch <= 0 || rows <= 0 || cols <= 0) return fail(BT_EINVAL, "elementwise shape must be positive");
+  int64_t total = batch * rows * cols;
+  unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 1 << 20);
+  if (prog->dtype == BT_BF16) elementwise_kernel<BT_BF16><<<blocks, 256, 0, r->stream>>>(*prog, batch, rows, cols, *out);
+  else if (prog->dtype == BT_FP32)
+    elementwise_kernel<BT_FP32><<<blocks, 256, 0, r->stream>>>(*prog, batch, rows, cols, *out);
+  else elementwise_kernel<BT_INT32><<<blocks, 256, 0, r->stream>>>(*prog, batch, rows, cols, *out);
+  BT_LAUNCHED("elementwise");
+  return BT_OK;
+}
+
+int bt_reduce(bt_runtime *rt, const bt_program *prog, int kind, int axis, int64_t batch, int64_t rows, int64_t cols,
+              int64_t sweep, int64_t step, const bt_operand *out) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (int s = check_program(prog)) return s;
+  if (int s = check_out(out)) return s;
+  if (kind != BT_REDUCE_SUM && kind != BT_REDUCE_MAX) return fail(BT_EINVAL, "reduction kind %d", kind);
+  if (axis < 0 || axis > 2) return fail(BT_EINVAL, "reduction axis %d", axis);
+  if (batch <= 0 || rows <= 0 || cols <= 0) return fail(BT_EINVAL, "reduction shape must be positive");
+  if (prog->dtype == BT_INT32 && kind == BT_REDUCE_SUM) return fail(BT_EINVAL, "int32 sums go through fp32");
+  if (axis == 0) {
+    if (sweep <= 1) { sweep = batch; step = 1; }
+    if (step < 1 || batch % (sweep * step)) return fail(BT_EINVAL, "sweep %lld x step %lld doesn't fold batch %lld",
+                                                        (long long)sweep, (long long)step, (long long)batch);
+  }
+  int64_t outs = (axis == 0 ? batch / sweep : batch) * (axis == 1 ? 1 : rows) * (axis == 2 ? 1 : cols);
+  unsigned blocks = (unsigned)((outs + 3) / 4);
+  if (prog->dtype == BT_BF16)
+    reduce_kernel<BT_BF16><<<blocks, 256, 0, r->stream>>>(*prog, kind, axis, batch, rows, cols, sweep, step, *out);
+  else if (prog->dtype == BT_FP32)
+    reduce_kernel<BT_FP32><<<blocks, 256, 0, r->stream>>>(*prog, kind, axis, batch, rows, cols, sweep, step, *out);
+  else reduce_kernel<BT_INT32><<<blocks, 256, 0, r->stream>>>(*prog, kind, axis, batch, rows, cols, sweep, step, *out);
+  BT_LAUNCHED("reduce");
+  return BT_OK;
+}
+
+int bt_gather(bt_runtime *rt, int dtype, uint64_t table, int64_t rows, int64_t cols, int64_t table_rstride,
+              uint64_t ids, int64_t n, uint64_t out, int64_t out_rstride) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (dtype != BT_BF16 && dtype != BT_FP32 && dtype != BT_INT32) return fail(BT_EINVAL, "gather dtype %d", dtype);
+  if (rows <= 0 || cols <= 0 || n < 0) return fail(BT_EINVAL, "gather shape");
+  if (!n) return BT_OK;
+  int size = dtype == BT_BF16 ? 2 : 4;
+  gather_kernel<<<(unsigned)n, 256, 0, r->stream>>>((const uint8_t *)table, rows, cols * size, table_rstride * size,
+                                                    (const int32_t *)ids, (uint8_t *)out, out_rstride * size);
+  BT_LAUNCHED("gather");
+  return BT_OK;
+}
+
+int bt_put(bt_runtime *rt, int dtype, uint64_t dst, int64_t batch, int64_t dst_rows, int64_t cols, int64_t dst_sb,
+           int64_t dst_sr, uint64_t ids, int64_t n, uint64_t x, int64_t x_sb, int64_t x_sr) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (dtype != BT_BF16 && dtype != BT_FP32 && dtype != BT_INT32) return fail(BT_EINVAL, "put dtype %d", dtype);
+  if (batch <= 0 || dst_rows <= 0 || cols <= 0 || n < 0) return fail(BT_EINVAL, "put shape");
+  if (!n) return BT_OK;
+  int size = dtype == BT_BF16 ? 2 : 4;
+  int64_t row_bytes = cols * size, pieces = (row_bytes / 2 + 255) / 256;
+  put_kernel<<<(unsigned)(batch * pieces), 256, 0, r->stream>>>((uint8_t *)dst, dst_rows, row_bytes, dst_sb * size,
+                                                                dst_sr * size, (const int32_t *)ids, n,
+                                                                (const uint8_t *)x, x_sb * size, x_sr * size, pieces);
+  BT_LAUNCHED("put");
+  return BT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,162 @@
+// The per-element evaluator of a bt_program: a straight line of instructions over 16 registers of 32-bit values, in
+// one dtype. The program sits in the kernel arguments, so instruction fields are uniform across a wavefront, and the
+// register index switches below become scalar branches rather than indexed (scratch) register access.
+#pragma once
+#include "common.h"
+#include <math.h>
+
+namespace bt {
+
+__device__ __forceinline__ uint32_t reg_get(const uint32_t (&r)[BT_MAX_REGS], int i) {
+  switch (i) {
+    case 0: return r[0]; case 1: return r[1]; case 2: return r[2]; case 3: return r[3];
+    case 4: return r[4]; case 5: return r[5]; case 6: return r[6]; case 7: return r[7];
+    case 8: return r[8]; case 9: return r[9]; case 10: return r[10]; case 11: return r[11];
+    case 12: return r[12]; case 13: return r[13]; case 14: return r[14]; default: return r[15];
+  }
+}
+
+__device__ __forceinline__ void reg_set(uint32_t (&r)[BT_MAX_REGS], int i, uint32_t v) {
+  switch (i) {
+    case 0: r[0] = v; break; case 1: r[1] = v; break; case 2: r[2] = v; break; case 3: r[3] = v; break;
+    case 4: r[4] = v; break; case 5: r[5] = v; break; case 6: r[6] = v; break; case 7: r[7] = v; break;
+    case 8: r[8] = v; break; case 9: r[9] = v; break; case 10: r[10] = v; break; case 11: r[11] = v; break;
+    case 12: r[12] = v; break; case 13: r[13] = v; break; case 14: r[14] = v; break; default: r[15] = v; break;
+  }
+}
+
+// The stored matrix that batch entry b of the result reads.
+__device__ __forceinline__ int64_t operand_matrix(const bt_operand &o, int64_t b) {
+  int64_t m = b / o.rep;
+  return o.cyc ? m % o.cyc : m;
+}
+
+__device__ __forceinline__ const void *operand_at(const bt_operand &o, int64_t b, int64_t r, int64_t c) {
+  int64_t at = operand_matrix(o, b) * o.sb + r * o.sr + c * o.sc;
+  int size = o.dtype == BT_BF16 ? 2 : 4;
+  return (const void *)(o.ptr + (uint64_t)(at * size));
+}
+
+// An input value in the program's dtype, as raw bits.
+template <int DT>
+__device__ __forceinline__ uint32_t load_operand(const bt_operand &o, int64_t b, int64_t r, int64_t c) {
+  const void *p = operand_at(o, b, r, c);
+  if (o.dtype == BT_BF16) {
+    uint32_t bits = *(const uint16_t *)p;
+    if (DT == BT_INT32) return (uint32_t)(int32_t)rintf(bf16_value(bits));
+    return bits << 16;
+  }
+  uint32_t v = *(const uint32_t *)p;
+  if (o.dtype == BT_INT32 && DT != BT_INT32) {
+    float f = (float)(int32_t)v;
+    return __float_as_uint(DT == BT_BF16 ? round_packed(f) : f);
+  }
+  if (o.dtype == BT_FP32 && DT == BT_INT32) return (uint32_t)(int32_t)rintf(__uint_as_float(v));
+  if (o.dtype == BT_FP32 && DT == BT_BF16) return __float_as_uint(round_packed(__uint_as_float(v)));
+  return v;
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  return 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * x * x * x)));
+}
+
+// One instruction's float result, before the dtype's rounding.
+__device__ __forceinline__ float float_op(int op, float a, float b, float c) {
+  switch (op) {
+    case BT_OP_ADD: return a + b;
+    case BT_OP_SUB: return a - b;
+    case BT_OP_MUL: return a * b;
+    case BT_OP_DIV: return a / b;
+    case BT_OP_MAX: return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b);
+    case BT_OP_MIN: return (a != a || b != b) ? __builtin_nanf("") : fminf(a, b);
+    case BT_OP_CMPLT: return a < b ? 1.0f : 0.0f;
+    case BT_OP_CMPLE: return a <= b ? 1.0f : 0.0f;
+    case BT_OP_CMPNE: return a != b ? 1.0f : 0.0f;
+    case BT_OP_CMPEQ: return a == b ? 1.0f : 0.0f;
+    case BT_OP_NEG: return -a;
+    case BT_OP_RELU: return a > 0.0f ? a : 0.0f;
+    case BT_OP_EXP: return expf(a);
+    case BT_OP_EXP2: return exp2f(a);
+    case BT_OP_LOG: return logf(a);
+    case BT_OP_LOG2: return log2f(a);
+    case BT_OP_SQRT: return sqrtf(a);
+    case BT_OP_RECIP: return 1.0f / a;
+    case BT_OP_RSQRT: return 1.0f / sqrtf(a);
+    case BT_OP_SIN: return sinf(a);
+    case BT_OP_COS: return cosf(a);
+    case BT_OP_SIGMOID: return 1.0f / (1.0f + expf(-a));
+    case BT_OP_SILU: return a / (1.0f + expf(-a));
+    case BT_OP_GELU: return gelu_tanh(a);
+    case BT_OP_TANH: return tanhf(a);
+    case BT_OP_FTOB: return round_packed(a);
+    default: return a;
+  }
+}
+
+__device__ __forceinline__ int32_t int_op(int op, int32_t a, int32_t b) {
+  switch (op) {
+    case BT_OP_ADD: return (int32_t)((uint32_t)a + (uint32_t)b);
+    case BT_OP_SUB: return (int32_t)((uint32_t)a - (uint32_t)b);
+    case BT_OP_MUL: return (int32_t)((uint32_t)a * (uint32_t)b);
+    case BT_OP_MAX: return a > b ? a : b;
+    case BT_OP_MIN: return a < b ? a : b;
+    case BT_OP_CMPLT: return a < b;
+    case BT_OP_CMPLE: return a <= b;
+    case BT_OP_CMPNE: return a != b;
+    case BT_OP_CMPEQ: return a == b;
+    case BT_OP_NEG: return (int32_t)(0u - (uint32_t)a);
+    case BT_OP_RELU: return a > 0 ? a : 0;
+    default: return a;
+  }
+}
+
+// Runs prog at element (b, r, c). acc, if the program reads register 0 as a preloaded value (a matmul epilogue), is
+// placed there first. Returns the result register's bits.
+template <int DT>
+__device__ __forceinline__ uint32_t run_program(const bt_program &prog, int64_t b, int64_t r, int64_t c,
+                                                uint32_t acc) {
+  uint32_t regs[BT_MAX_REGS];
+#pragma unroll
+  for (int i = 0; i < BT_MAX_REGS; i++) regs[i] = 0;
+  regs[0] = acc;
+  for (int i = 0; i < prog.n_inst; i++) {
+    const bt_inst in = prog.inst[i];
+    uint32_t v;
+    if (in.op == BT_OP_LOAD) v = load_operand<DT>(prog.in[in.a], b, r, c);
+    else if (in.op == BT_OP_CONST) v = in.imm;
+    else if (in.op == BT_OP_MOV) v = reg_get(regs, in.a);
+    else if (in.op == BT_OP_WHERE) {
+      uint32_t cnd = reg_get(regs, in.a);
+      bool on = DT == BT_INT32 ? cnd != 0 : __uint_as_float(cnd) != 0.0f;
+      v = on ? reg_get(regs, in.b) : reg_get(regs, in.c);
+    } else if (DT == BT_INT32) {
+      v = (uint32_t)int_op(in.op, (int32_t)reg_get(regs, in.a), (int32_t)reg_get(regs, in.b));
+    } else {
+      float x = float_op(in.op, __uint_as_float(reg_get(regs, in.a)), __uint_as_float(reg_get(regs, in.b)), 0.0f);
+      v = __float_as_uint(DT == BT_BF16 ? round_packed(x) : x);
+    }
+    reg_set(regs, in.dst, v);
+  }
+  return reg_get(regs, prog.result);
+}
+
+// Stores a result computed in DT as out's dtype at element offset `at`.
+template <int DT>
+__device__ __forceinline__ void store_value(const bt_operand &out, int64_t at, uint32_t v) {
+  if (out.dtype == BT_BF16) {
+    float f = DT == BT_INT32 ? (float)(int32_t)v : __uint_as_float(v);
+    ((uint16_t *)out.ptr)[at] = (uint16_t)bf16_packed(f);
+  } else if (out.dtype == BT_FP32) {
+    ((float *)out.ptr)[at] = DT == BT_INT32 ? (float)(int32_t)v : __uint_as_float(v);
+  } else {
+    int32_t i;
+    if (DT == BT_INT32) i = (int32_t)v;
+    else {
+      float f = rintf(__uint_as_float(v));
+      i = f != f ? 0 : f >= 2147483648.0f ? 2147483647 : f < -2147483648.0f ? (-2147483647 - 1) : (int32_t)f;
+    }
+    ((int32_t *)out.ptr)[at] = i;
+  }
+}
+
+}  // namespace bt

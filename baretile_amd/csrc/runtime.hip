@@ -1,0 +1,253 @@
+// The runtime facade: a device, one in-order HIP stream per runtime, stream-ordered memory, host copies, a wait with a
+// timeout, timing events and graph capture. Each entry point returns a status and leaves its message for
+// bt_last_error().
+#include "common.h"
+#include <chrono>
+#include <string>
+#include <thread>
+
+namespace bt {
+
+static thread_local std::string last_error;
+
+void set_error(const char *fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  last_error = buf;
+}
+
+int fail(int code, const char *fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  last_error = buf;
+  return code;
+}
+
+int enter(bt_runtime *rt, Runtime **out) {
+  Runtime *r = reinterpret_cast<Runtime *>(rt);
+  if (!r) return fail(BT_EINVAL, "no runtime");
+  if (r->closed) return fail(BT_ESTATE, "the runtime is closed");
+  BT_HIP(hipSetDevice(r->device));
+  *out = r;
+  return BT_OK;
+}
+
+// Fills words of 32 bits. A kernel rather than hipMemsetAsync, so that a captured graph holds no memset node.
+__global__ void fill32_kernel(uint32_t *dst, uint32_t value, uint64_t words) {
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x, step = (uint64_t)gridDim.x * blockDim.x;
+  for (; i < words; i += step) dst[i] = value;
+}
+
+}  // namespace bt
+
+using namespace bt;
+
+extern "C" {
+
+const char *bt_last_error(void) { return last_error.c_str(); }
+
+int bt_version(void) { return BT_ABI_VERSION; }
+
+int bt_device_count(int *n) {
+  if (!n) return fail(BT_EINVAL, "no result pointer");
+  hipError_t e = hipGetDeviceCount(n);
+  if (e == hipErrorNoDevice) { *n = 0; return BT_OK; }
+  BT_HIP(e);
+  return BT_OK;
+}
+
+int bt_open(int device, bt_runtime **out) {
+  if (!out) return fail(BT_EINVAL, "no result pointer");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0) return fail(BT_ESTATE, "no GPU is visible: %s", hipGetErrorString(e));
+  if (device < 0 || device >= n) return fail(BT_EINVAL, "device %d outside 0..%d", device, n - 1);
+  BT_HIP(hipSetDevice(device));
+  hipDeviceProp_t p;
+  BT_HIP(hipGetDeviceProperties(&p, device));
+  if (std::string(p.gcnArchName).rfind("gfx950", 0) != 0)
+    return fail(BT_ESTATE, "this library is built for gfx950, and device %d is %s", device, p.gcnArchName);
+  Runtime *r = new Runtime;
+  r->device = device;
+  hipError_t s = hipStreamCreateWithFlags(&r->stream, hipStreamNonBlocking);
+  if (s != hipSuccess) { delete r; return fail(BT_ESTATE, "hipStreamCreate: %s", hipGetErrorString(s)); }
+  *out = reinterpret_cast<bt_runtime *>(r);
+  return BT_OK;
+}
+
+int bt_close(bt_runtime *rt) {
+  Runtime *r = reinterpret_cast<Runtime *>(rt);
+  if (!r) return fail(BT_EINVAL, "no runtime");
+  if (r->closed) return BT_OK;
+  BT_HIP(hipSetDevice(r->device));
+  if (r->capture_origin) return fail(BT_ESTATE, "close a runtime after ending its graph capture");
+  BT_HIP(hipStreamSynchronize(r->stream));
+  BT_HIP(hipStreamDestroy(r->stream));
+  r->closed = 1;
+  delete r;
+  return BT_OK;
+}
+
+int bt_alloc(bt_runtime *rt, uint64_t bytes, uint64_t *addr) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (!addr) return fail(BT_EINVAL, "no result pointer");
+  void *p = nullptr;
+  uint64_t n = bytes ? (bytes + 255) / 256 * 256 : 256;
+  // Outside a capture, stream-ordered from the device's pool, so a free only waits for the launches queued before it.
+  // Inside a capture, a plain allocation that outlives the graph: the graph keeps using it on every replay.
+  hipError_t e = r->capture_origin ? hipMalloc(&p, n) : hipMallocAsync(&p, n, r->stream);
+  if (e == hipErrorOutOfMemory) return fail(BT_ENOMEM, "out of device memory allocating %llu bytes", (unsigned long long)n);
+  if (e != hipSuccess) return fail(BT_ESTATE, "allocating %llu bytes: %s", (unsigned long long)n, hipGetErrorString(e));
+  *addr = (uint64_t)(uintptr_t)p;
+  return BT_OK;
+}
+
+int bt_free(bt_runtime *rt, uint64_t addr, int captured) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (!addr) return BT_OK;
+  if (captured) {  // made while capturing: freed only once the stream has drained
+    BT_HIP(hipStreamSynchronize(r->stream));
+    BT_HIP(hipFree((void *)(uintptr_t)addr));
+  } else {
+    BT_HIP(hipFreeAsync((void *)(uintptr_t)addr, r->stream));
+  }
+  return BT_OK;
+}
+
+int bt_upload(bt_runtime *rt, uint64_t dst, const void *src, uint64_t bytes) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (r->capture_origin) return fail(BT_ESTATE, "a graph capture can't copy host memory");
+  if (!bytes) return BT_OK;
+  BT_HIP(hipMemcpyAsync((void *)(uintptr_t)dst, src, bytes, hipMemcpyHostToDevice, r->stream));
+  BT_HIP(hipStreamSynchronize(r->stream));  // the caller's buffer may go away on return
+  return BT_OK;
+}
+
+int bt_download(bt_runtime *rt, void *dst, uint64_t src, uint64_t bytes) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (r->capture_origin) return fail(BT_ESTATE, "a graph capture can't read back to the host");
+  if (!bytes) return BT_OK;
+  BT_HIP(hipMemcpyAsync(dst, (const void *)(uintptr_t)src, bytes, hipMemcpyDeviceToHost, r->stream));
+  BT_HIP(hipStreamSynchronize(r->stream));
+  return BT_OK;
+}
+
+int bt_copy(bt_runtime *rt, uint64_t dst, uint64_t src, uint64_t bytes) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (!bytes) return BT_OK;
+  BT_HIP(hipMemcpyAsync((void *)(uintptr_t)dst, (const void *)(uintptr_t)src, bytes, hipMemcpyDeviceToDevice,
+                        r->stream));
+  return BT_OK;
+}
+
+int bt_fill32(bt_runtime *rt, uint64_t dst, uint32_t value, uint64_t words) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (!words) return BT_OK;
+  if (dst % 4) return fail(BT_EINVAL, "fill32 needs a 4-byte aligned address");
+  uint64_t blocks = (words + 255) / 256;
+  fill32_kernel<<<(unsigned)(blocks < 4096 ? blocks : 4096), 256, 0, r->stream>>>((uint32_t *)(uintptr_t)dst, value,
+                                                                                  words);
+  BT_LAUNCHED("fill32");
+  return BT_OK;
+}
+
+int bt_wait(bt_runtime *rt, double timeout_s) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (r->capture_origin) return fail(BT_ESTATE, "can't wait while a graph capture is open");
+  auto start = std::chrono::steady_clock::now();
+  for (int spins = 0;; spins++) {
+    hipError_t e = hipStreamQuery(r->stream);
+    if (e == hipSuccess) return BT_OK;
+    if (e != hipErrorNotReady) return fail(BT_ESTATE, "waiting for the stream: %s", hipGetErrorString(e));
+    double waited = std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count();
+    if (timeout_s >= 0 && waited > timeout_s)
+      return fail(BT_ETIMEOUT, "launches still running after %.1f s", timeout_s);
+    if (spins > 64) std::this_thread::sleep_for(std::chrono::microseconds(spins > 4096 ? 1000 : 20));
+  }
+}
+
+int bt_event_create(bt_runtime *rt, void **ev) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  hipEvent_t e;
+  BT_HIP(hipEventCreate(&e));
+  *ev = (void *)e;
+  return BT_OK;
+}
+
+int bt_event_record(bt_runtime *rt, void *ev) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  BT_HIP(hipEventRecord((hipEvent_t)ev, r->stream));
+  return BT_OK;
+}
+
+int bt_event_elapsed(void *start, void *end, float *ms) {
+  BT_HIP(hipEventSynchronize((hipEvent_t)end));
+  BT_HIP(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end));
+  return BT_OK;
+}
+
+int bt_event_destroy(void *ev) {
+  BT_HIP(hipEventDestroy((hipEvent_t)ev));
+  return BT_OK;
+}
+
+int bt_graph_begin(bt_runtime *rt) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (r->capture_origin) return fail(BT_ESTATE, "a graph capture is already open on this runtime");
+  BT_HIP(hipStreamBeginCapture(r->stream, hipStreamCaptureModeRelaxed));
+  r->capture_origin = r->stream;
+  return BT_OK;
+}
+
+int bt_graph_end(bt_runtime *rt, void **exec) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (!r->capture_origin) return fail(BT_ESTATE, "no graph capture is open");
+  hipGraph_t g = nullptr;
+  r->capture_origin = nullptr;
+  BT_HIP(hipStreamEndCapture(r->stream, &g));
+  hipGraphExec_t x = nullptr;
+  hipError_t e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  if (e != hipSuccess) return fail(BT_ESTATE, "instantiating the graph: %s", hipGetErrorString(e));
+  *exec = (void *)x;
+  return BT_OK;
+}
+
+int bt_graph_launch(bt_runtime *rt, void *exec) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (r->capture_origin) return fail(BT_ESTATE, "can't replay a graph while capturing");
+  BT_HIP(hipGraphLaunch((hipGraphExec_t)exec, r->stream));
+  return BT_OK;
+}
+
+int bt_graph_destroy(void *exec) {
+  if (exec) BT_HIP(hipGraphExecDestroy((hipGraphExec_t)exec));
+  return BT_OK;
+}
+
+int bt_stream(bt_runtime *rt, void **stream) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  *stream = (void *)r->stream;
+  return BT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,196 @@
+/* baretile_amd: the C ABI of the MI355X (gfx950) backend for baretile's hot path.
+ *
+ * One shared library, libbaretile_amd.so, loaded with ctypes the way baretile's pci.Sim loads its device library
+ * (baretile/pci.py:50-60). Plain pointers and sizes only: device memory is a uint64_t address, sizes and strides are
+ * int64_t element counts, and every function returns a status, with the message of the last failure on the calling
+ * thread in bt_last_error().
+ *
+ * Status -> Python exception, as baretile's API promises (docs/api.md:51-63): BT_EINVAL -> ValueError,
+ * BT_ESTATE -> RuntimeError, BT_ETIMEOUT -> TimeoutError, BT_ENOMEM -> MemoryError.
+ *
+ * Each declaration names the reference interface it replaces. In the reference those are Python functions that build
+ * a Tensix kernel image and queue it with Runtime.launch(kernel, args: tuple[u32], units, name) (runtime.py:680-695);
+ * here they are direct calls that queue HIP kernels on the runtime's stream, in order, without waiting.
+ */
+#ifndef BARETILE_AMD_H
+#define BARETILE_AMD_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BT_ABI_VERSION 1
+
+enum { BT_OK = 0, BT_EINVAL = 1, BT_ESTATE = 2, BT_ETIMEOUT = 3, BT_ENOMEM = 4 };
+
+/* Storage formats (tensix.py:14-21: ITEMSIZE and BFP). */
+enum { BT_BF16 = 0, BT_FP32 = 1, BT_INT32 = 2, BT_BFP8 = 3, BT_BFP4 = 4 };
+
+typedef struct bt_runtime bt_runtime;
+
+/* ---- runtime: replaces Runtime (runtime.py:543-880) and the device layer under it (pci.py, chip.py) ------------ */
+
+const char *bt_last_error(void);
+int bt_version(void);
+int bt_device_count(int *n);
+/* Runtime(chip) (runtime.py:543): a device and one in-order stream. */
+int bt_open(int device, bt_runtime **rt);
+/* Runtime.close (runtime.py:484-541): waits for queued work, then releases the stream. */
+int bt_close(bt_runtime *rt);
+/* Runtime.dram_alloc / dram_free (runtime.py:791-820). Frees are stream-ordered, so memory goes back once the
+ * launches queued before the free are done (runtime.py:814-820). `captured` marks memory allocated while a graph
+ * capture was open. */
+int bt_alloc(bt_runtime *rt, uint64_t bytes, uint64_t *addr);
+int bt_free(bt_runtime *rt, uint64_t addr, int captured);
+/* Tensor.frombytes / tobytes transfers (tensor.py:113-204, kernels.py:1374-1453 upload/readback_kernel). Both
+ * return once the bytes have arrived. */
+int bt_upload(bt_runtime *rt, uint64_t dst, const void *src, uint64_t bytes);
+int bt_download(bt_runtime *rt, void *dst, uint64_t src, uint64_t bytes);
+int bt_copy(bt_runtime *rt, uint64_t dst, uint64_t src, uint64_t bytes);
+/* zeros_kernel (kernels.py:1436-1453): fills 32-bit words, by a kernel (never a memset node in a graph). */
+int bt_fill32(bt_runtime *rt, uint64_t dst, uint32_t value, uint64_t words);
+/* Runtime.wait(timeout) (runtime.py:851-880): BT_ETIMEOUT if the stream is still busy after timeout_s seconds. */
+int bt_wait(bt_runtime *rt, double timeout_s);
+/* Timing for Runtime.profile (runtime.py:773-786): events on the runtime's stream. */
+int bt_event_create(bt_runtime *rt, void **ev);
+int bt_event_record(bt_runtime *rt, void *ev);
+int bt_event_elapsed(void *start, void *end, float *ms);
+int bt_event_destroy(void *ev);
+/* jit / Recording (tensor.py:1171-1293): record the launches queued between begin and end into a graph, then replay
+ * it with one call. */
+int bt_graph_begin(bt_runtime *rt);
+int bt_graph_end(bt_runtime *rt, void **graph);
+int bt_graph_launch(bt_runtime *rt, void *graph);
+int bt_graph_destroy(void *graph);
+/* The runtime's hipStream_t, for callers that time or order their own work against it. */
+int bt_stream(bt_runtime *rt, void **stream);
+
+/* ---- block floats: replaces the bfp8 packer cast (kernels.py:128-138), bfp4_kernel (kernels.py:1527-1567),
+ * storage_kernel (kernels.py:1483-1525) and columns_kernel (kernels.py:1455-1481) --------------------------------
+ *
+ * Plain layout of a block-float batch of [rows, cols] matrices: an exponent plane, one byte per run of 16 values
+ * along a row, [batch][rows][ceil(cols / 16)], then a value plane of signed magnitudes q in two's complement,
+ * [batch][rows][cols16] int8 for bfp8 or [batch][rows][cols16 / 2] bytes of two 4-bit values for bfp4 (the first in
+ * the low nibble), where cols16 rounds cols up to 16. A value is q * 2^(e - 133) (bfp8) or q * 2^(e - 129) (bfp4).
+ *
+ * Columns layout (Tensor.columns(), a matmul's B): tiles of 64 rows (K) by 16 columns (N), ordered
+ * [batch][column run][64-row chunk]. A tile is 64 exponent bytes, then its values in the order the 16x16x32 matrix
+ * instruction reads B: lane l (0..63) holds rows 32h + 8(l / 16) + j, j = 0..7, of column l % 16, for h = 0, 1.
+ * Exponent byte p = 16g + 8h + j belongs to row 32h + 8g + j. bfp8 tiles are 64 + 1024 bytes (lane l's 16 bytes at
+ * 64 + 16l), bfp4 tiles 64 + 512 (8 bytes at 64 + 8l), and bf16 tiles 2048 bytes (32 bytes at 32l, no exponents).
+ * Rows past K and columns past N are zero. */
+
+/* bf16 (round to nearest even first, as gpt2.bfp does: models/gpt2.py:19-30) or fp32 matrices -> plain planes.
+ * src strides are in elements. */
+int bt_bfp_pack(bt_runtime *rt, int fmt, uint64_t src, int src_dtype, int64_t batch, int64_t rows, int64_t cols,
+                int64_t src_bstride, int64_t src_rstride, int64_t src_cstride, uint64_t exps, uint64_t vals);
+/* plain planes -> bf16 row-major [batch][rows][cols], bit for bit what the unpacker gives (tensor.py:1093-1104). */
+int bt_bfp_unpack(bt_runtime *rt, int fmt, uint64_t exps, uint64_t vals, int64_t batch, int64_t rows, int64_t cols,
+                  uint64_t dst);
+/* plain planes -> columns tiles (Tensor.columns, tensor.py:597-611). */
+int bt_bfp_columns(bt_runtime *rt, int fmt, uint64_t exps, uint64_t vals, int64_t batch, int64_t rows, int64_t cols,
+                   uint64_t dst);
+/* bf16 matrices with any strides -> bf16 columns tiles (a matmul's B read as it is, or transposed by strides). */
+int bt_bf16_columns(bt_runtime *rt, uint64_t src, int64_t batch, int64_t rows, int64_t cols, int64_t sb, int64_t sr,
+                    int64_t sc, uint64_t dst);
+/* columns tiles of any format -> bf16 row-major [batch][rows][cols] (readback of a tensor by columns). */
+int bt_columns_unpack(bt_runtime *rt, int fmt, uint64_t src, int64_t batch, int64_t rows, int64_t cols, uint64_t dst);
+
+/* ---- fused expressions: replaces fused_kernel's elementwise and reduction kernels (kernels.py:41-727) ----------
+ *
+ * A program is a straight line of instructions over up to 16 registers, evaluated per element in one dtype: bf16
+ * rounds every result half up as the packer does (so fused and unfused give the same bits, test_kernels.py:987-1004),
+ * fp32 keeps it, int32 is integer arithmetic that wraps. Inputs are read with element strides; a stride of 0
+ * broadcasts. Batch index b of the result reads stored matrix (b / rep) % cyc of an input (cyc 0: no wrap), as a
+ * repeat or a spread view does (tensor.py:265-279, 414-424). */
+#define BT_MAX_INPUTS 8
+#define BT_MAX_INST 48
+#define BT_MAX_REGS 16
+
+enum {
+  BT_OP_LOAD = 0,  /* dst = input a, converted to the program's dtype */
+  BT_OP_CONST,     /* dst = imm (bits in the program's dtype) */
+  BT_OP_MOV,
+  BT_OP_ADD, BT_OP_SUB, BT_OP_MUL, BT_OP_DIV, BT_OP_MAX, BT_OP_MIN,
+  BT_OP_CMPLT, BT_OP_CMPLE, BT_OP_CMPNE, BT_OP_CMPEQ, /* 1 or 0 */
+  BT_OP_WHERE,     /* dst = a != 0 ? b : c, keeping the selected value's bits */
+  BT_OP_NEG, BT_OP_RELU, BT_OP_EXP, BT_OP_EXP2, BT_OP_LOG, BT_OP_LOG2, BT_OP_SQRT, BT_OP_RECIP, BT_OP_RSQRT,
+  BT_OP_SIN, BT_OP_COS, BT_OP_SIGMOID, BT_OP_SILU, BT_OP_GELU, BT_OP_TANH,
+  BT_OP_FTOB,      /* round an fp32 value to bf16 (half up, as the bf16 cast does) and back */
+  BT_OP_COUNT
+};
+
+typedef struct {
+  uint64_t ptr;      /* address of element (0, 0, 0) */
+  int64_t sb, sr, sc; /* element strides of batch, row and column */
+  int32_t dtype;     /* BT_BF16, BT_FP32 or BT_INT32 */
+  int32_t rep;       /* >= 1 */
+  int32_t cyc;       /* 0, or the number of stored matrices the batch index wraps at */
+  int32_t pad_;
+} bt_operand;
+
+typedef struct {
+  uint8_t op, dst, a, b, c, pad_[3];
+  uint32_t imm;
+} bt_inst;
+
+typedef struct {
+  int32_t n_inst;
+  int32_t n_inputs;
+  int32_t dtype;   /* the dtype the program computes in */
+  int32_t result;  /* the register holding the result */
+  bt_inst inst[BT_MAX_INST];
+  bt_operand in[BT_MAX_INPUTS];
+} bt_program;
+
+/* A fused elementwise kernel over [batch, rows, cols], written to out in out->dtype (a cast at the root converts:
+ * to bf16 rounds half up, to int32 rounds to nearest, from int32 converts exactly where it can). */
+int bt_elementwise(bt_runtime *rt, const bt_program *prog, int64_t batch, int64_t rows, int64_t cols,
+                   const bt_operand *out);
+/* A reduction (sum or max) along axis 0 (batch), 1 (rows) or 2 (columns) of the program's value over [batch, rows,
+ * cols], accumulated in fp32 (int32 for an int32 max), written to out, whose extent along axis is 1. With sweep > 1,
+ * axis 0 folds `sweep` matrices a `step` apart, as a reduction over a middle leading dimension does
+ * (tensor.py:657-676). */
+enum { BT_REDUCE_SUM = 0, BT_REDUCE_MAX = 1 };
+int bt_reduce(bt_runtime *rt, const bt_program *prog, int kind, int axis, int64_t batch, int64_t rows, int64_t cols,
+              int64_t sweep, int64_t step, const bt_operand *out);
+
+/* ---- matmul: replaces fused_kernel's matmul schedules (kernels.py:41-727, 216-555) ------------------------------
+ *
+ * out[b, m, n] = epilogue(sum_k A[b, m, k] * B[b', k, n]), with exact bf16 products summed in fp32 by the matrix
+ * instructions (fidelity 4, tensor.py:12, 756-757). A is bf16 with element strides. B is in columns layout (any of
+ * bf16, bfp8, bfp4) with b' = b when b_batch > 1, else 0. The epilogue program, if any, reads the matmul's value
+ * from register 0 (rounded to the program's dtype first) and may read other inputs at the same [b, m, n]. Without
+ * one, the value is written to out as bf16 (rounded half up) or fp32. */
+int bt_matmul(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_t b, int64_t b_batch, int64_t batch, int64_t m,
+              int64_t k, int64_t n, const bt_program *epilogue, const bt_operand *out);
+
+/* ---- attention: replaces attention_kernel and its division/combine launches (kernels.py:794-1005,
+ * tensor.py:797-841) -------------------------------------------------------------------------------------------
+ *
+ * out[e, r, :] = softmax(q[e, r, :] . k[e / rep, j, :] + mask) @ v[e / rep, j, :] over keys j < keys, where the mask
+ * hides j > places[r] and, with window > 0, j <= places[r] - window. Scores, maxima and sums are fp32; out is bf16.
+ * q, k, v, out are bf16 with element strides (head, row); places is int32 with a head stride of 0 or rows. No scale
+ * is applied: baretile's RoPE pre-scales q (llama.py:210-216). */
+typedef struct {
+  uint64_t q, k, v, out, places;
+  int64_t q_sh, q_sr, k_sh, k_sr, v_sh, v_sr, o_sh, o_sr, places_sh;
+  int32_t heads, rep, rows, keys, head_dim, window;
+} bt_attention_args;
+int bt_attention(bt_runtime *rt, const bt_attention_args *args);
+
+/* ---- rows in and out of a cache: replaces gather_kernel (kernels.py:1007-1049) and put_kernel
+ * (kernels.py:1083-1168) ------------------------------------------------------------------------------------------ */
+/* out[i, :] = table[ids[i], :] for i < n. An id outside [0, rows) gives a row of zeros. */
+int bt_gather(bt_runtime *rt, int dtype, uint64_t table, int64_t rows, int64_t cols, int64_t table_rstride,
+              uint64_t ids, int64_t n, uint64_t out, int64_t out_rstride);
+/* dst[b, ids[i], :] = x[b, i, :] for i < n, in order, so a later duplicate wins. Places outside [0, dst_rows) are
+ * skipped. dst and x share dtype (bf16, fp32, int32). */
+int bt_put(bt_runtime *rt, int dtype, uint64_t dst, int64_t batch, int64_t dst_rows, int64_t cols, int64_t dst_sb,
+           int64_t dst_sr, uint64_t ids, int64_t n, uint64_t x, int64_t x_sb, int64_t x_sr);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
