@@ -58,7 +58,7 @@ SIGNATURES = {
   "bt_wait": [RT, c_double], "bt_event_create": [RT, POINTER(c_void_p)], "bt_event_record": [RT, c_void_p],
   "bt_event_elapsed": [c_void_p, c_void_p, POINTER(c_float)], "bt_event_destroy": [c_void_p],
   "bt_graph_begin": [RT], "bt_graph_end": [RT, POINTER(c_void_p)], "bt_graph_launch": [RT, c_void_p],
-  "bt_graph_destroy": [c_void_p], "bt_stream": [RT, POINTER(c_void_p)],
+  "bt_graph_destroy": [c_void_p], "bt_stream": [RT, POINTER(c_void_p)], "bt_stream_read": [RT, U64, U64, U64],
   "bt_bfp_pack": [RT, c_int, U64, c_int, I64, I64, I64, I64, I64, I64, U64, U64],
   "bt_bfp_unpack": [RT, c_int, U64, U64, I64, I64, I64, U64],
   "bt_bfp_columns": [RT, c_int, U64, U64, I64, I64, I64, U64],

@@ -74,6 +74,14 @@ __global__ void __launch_bounds__(256) unpack_kernel(const uint8_t *exps, const 
 __device__ __forceinline__ int tile_row_of_exp(int p) { return 32 * ((p >> 3) & 1) + 8 * (p >> 4) + (p & 7); }
 __device__ __forceinline__ int tile_row(int l, int h, int j) { return 32 * h + 8 * (l >> 4) + j; }
 
+// A columns tile keeps each run's exponent as d = (e - bias) mod 256, read by the matmul as a signed byte: the
+// power of two it applies to the integer magnitude (bfp8: q * 2^d) or to q * 2^-9, what a bfp4 value's fp8 form
+// converts to (bfp4: q * 2^-9 * 2^d). The map is a bijection, so readback recovers e exactly.
+template <int FMT> __device__ __forceinline__ uint32_t exp_bias() { return FMT == BT_BFP8 ? 133u : 120u; }
+
+// A bfp4 value in a columns tile: sign << 3 | magnitude (the low nibble of its fp8 e4m3 subnormal form).
+__device__ __forceinline__ uint32_t nibble_sm(int q) { return q < 0 ? 8u | (uint32_t)(-q) : (uint32_t)q; }
+
 // One block a columns tile, one thread a lane. Reads the plain planes, writes the tile.
 template <int FMT>
 __global__ void __launch_bounds__(64) columns_kernel(const uint8_t *exps, const uint8_t *vals, int64_t rows,
@@ -86,7 +94,8 @@ __global__ void __launch_bounds__(64) columns_kernel(const uint8_t *exps, const 
   uint8_t *out = dst + tile * TB;
   {  // exponent byte l
     int64_t k = chunk * 64 + tile_row_of_exp(l);
-    out[l] = k < rows ? exps[(b * rows + k) * runs + run] : 0;
+    uint32_t e = k < rows ? exps[(b * rows + k) * runs + run] : 0;
+    out[l] = (uint8_t)((e - exp_bias<FMT>()) & 255u);
   }
   int64_t n = run * 16 + (l & 15);
   uint32_t w[4] = {0, 0, 0, 0};
@@ -97,7 +106,7 @@ __global__ void __launch_bounds__(64) columns_kernel(const uint8_t *exps, const 
       int64_t k = chunk * 64 + tile_row(l, h, j);
       int q = (k < rows && n < cols16) ? plain_q<FMT>(vals, FMT == BT_BFP8 ? cols16 : cols16 / 2, b * rows + k, n) : 0;
       if (FMT == BT_BFP8) w[(h * 8 + j) / 4] |= ((uint32_t)q & 255u) << (8 * (j % 4));
-      else w[h] |= ((uint32_t)q & 15u) << (4 * j);
+      else w[h] |= nibble_sm(q) << (8 * (j % 4) + 4 * (j / 4));  // values j and j + 4 share byte j % 4
     }
   if (FMT == BT_BFP8) *(uint4 *)(out + 64 + 16 * l) = make_uint4(w[0], w[1], w[2], w[3]);
   else *(uint2 *)(out + 64 + 8 * l) = make_uint2(w[0], w[1]);
@@ -145,12 +154,12 @@ __global__ void __launch_bounds__(256) columns_unpack_kernel(const uint8_t *src,
   }
   constexpr int TB = FMT == BT_BFP8 ? 1088 : 576;
   const uint8_t *tp = src + tile * TB;
-  uint32_t e = tp[16 * g + 8 * h + j];
+  uint32_t e = (tp[16 * g + 8 * h + j] + exp_bias<FMT>()) & 255u;
   int q;
   if (FMT == BT_BFP8) q = (int)(int8_t)tp[64 + 16 * l + 8 * h + j];
   else {
-    int nib = (tp[64 + 8 * l + 4 * h + j / 2] >> (4 * (j & 1))) & 15;
-    q = (nib >= 8 ? nib - 16 : nib) * 16;
+    int nib = (tp[64 + 8 * l + 4 * h + (j & 3)] >> (4 * (j >> 2))) & 15;
+    q = (nib & 8 ? -(nib & 7) : nib) * 16;
   }
   dst[t] = (uint16_t)unpacked_bits(q, e);
 }

@@ -27,6 +27,7 @@ __device__ __forceinline__ void reg_set(uint32_t (&r)[BT_MAX_REGS], int i, uint3
 
 // The stored matrix that batch entry b of the result reads.
 __device__ __forceinline__ int64_t operand_matrix(const bt_operand &o, int64_t b) {
+  if (o.rep == 1 && o.cyc == 0) return b;  // the common case, without a division
   int64_t m = b / o.rep;
   return o.cyc ? m % o.cyc : m;
 }

@@ -29,12 +29,17 @@ def step_bytes(fmt, rows):
   return int(K_DIM * N_DIM * bpv + rows * K_DIM * 2 + rows * N_DIM * 2)
 
 
+def weight_bytes(fmt):  # the packed weight alone: 64 x 16 tiles of 1088 (bfp8) or 576 (bfp4) bytes
+  return (N_DIM // 16) * (K_DIM // 64) * (1088 if fmt == "bfp8" else 576)
+
+
 def log(*a):
   print(*a, file=sys.stderr, flush=True)
 
 
 def gpu_leg(fmt, rows, steps, warmup):
-  """Times `steps` GEMV launches on one GPU; returns (us per step, kernel name)."""
+  """Times `steps` GEMV launches on one GPU, then a plain streaming read of the same weight bytes. Returns
+  (us per GEMV, its result, x, w, us per streaming read)."""
   from baretile_amd import _lib
   from baretile_amd.runtime import Runtime
   rt = Runtime()
@@ -69,29 +74,37 @@ def gpu_leg(fmt, rows, steps, warmup):
     def launch(i):
       _lib.call("matmul", rt.handle, byref(a), code, pool[i % copies], 1, 1, rows, K_DIM, N_DIM, None, byref(o))
 
-    for i in range(3): launch(i)  # first launches load the code object
-    rt.wait()
-    graph = c_void_p()
-    _lib.call("graph_begin", rt.handle)
-    for i in range(steps): launch(i)
-    _lib.call("graph_end", rt.handle, byref(graph))
-    for _ in range(max(1, warmup // max(1, steps)) if warmup else 0): _lib.call("graph_launch", rt.handle, graph)
-    rt.wait()
-    start, end = c_void_p(), c_void_p()
-    _lib.call("event_create", rt.handle, byref(start))
-    _lib.call("event_create", rt.handle, byref(end))
-    _lib.call("event_record", rt.handle, start)
-    _lib.call("graph_launch", rt.handle, graph)
-    _lib.call("event_record", rt.handle, end)
-    ms = c_float()
-    _lib.call("event_elapsed", start, end, byref(ms))
-    rt.wait()
+    def timed(fn, warm):
+      """us per launch of fn(i) for i < steps, captured into one graph and replayed between two events."""
+      for i in range(3): fn(i)  # the first launches load the code object
+      rt.wait()
+      graph = c_void_p()
+      _lib.call("graph_begin", rt.handle)
+      for i in range(steps): fn(i)
+      _lib.call("graph_end", rt.handle, byref(graph))
+      for _ in range(max(1, warm // max(1, steps)) if warm else 0): _lib.call("graph_launch", rt.handle, graph)
+      rt.wait()
+      start, end = c_void_p(), c_void_p()
+      _lib.call("event_create", rt.handle, byref(start))
+      _lib.call("event_create", rt.handle, byref(end))
+      _lib.call("event_record", rt.handle, start)
+      _lib.call("graph_launch", rt.handle, graph)
+      _lib.call("event_record", rt.handle, end)
+      ms = c_float()
+      _lib.call("event_elapsed", start, end, byref(ms))
+      rt.wait()
+      _lib.call("graph_destroy", graph)
+      _lib.call("event_destroy", start)
+      _lib.call("event_destroy", end)
+      return ms.value * 1000 / steps
+
+    us = timed(launch, warmup)
     # the result is checked against the oracle's values on a few columns, so a fast wrong kernel can't report
     got = np.frombuffer(bytes(rt.download(out, rows * N_DIM * 2)), np.uint16).reshape(rows, N_DIM)
-    _lib.call("graph_destroy", graph)
-    _lib.call("event_destroy", start)
-    _lib.call("event_destroy", end)
-    return ms.value * 1000 / steps, got, x, w
+    # the same weight bytes read by a plain streaming kernel, from the same pool: what one launch of this size can get
+    word = rt.dram_alloc(256)
+    read_us = timed(lambda i: _lib.call("stream_read", rt.handle, pool[i % copies], wbytes // 16 * 16, word), steps)
+    return us, got, x, w, read_us
   finally:
     rt.close()
 
@@ -103,6 +116,16 @@ def check(got, x, w, fmt):
   want, bound = ops.matmul(xw, wq), ops.matmul_bound(xw, wq)
   val = (got[:, cols].astype(np.uint32) << 16).view(np.float32)
   return bool(np.all(np.abs(val - want) <= bound))
+
+
+def measured_traffic():
+  """HBM bytes per launch of the headline kernel, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+  (profiles/gemv_bfp4_B1_lmhead_traffic.json: per-dispatch counters scaled by a streaming read of known size)."""
+  path = os.path.join(ROOT, "profiles", "gemv_bfp4_B1_lmhead_traffic.json")
+  try:
+    with open(path) as f: return json.load(f)["traffic_bytes_per_launch"]
+  except (OSError, KeyError, ValueError):
+    return None
 
 
 def cpu_leg(fmt, rows, seconds=10.0):
@@ -138,6 +161,7 @@ def main():
   ap.add_argument("--warmup", type=int, default=400)
   ap.add_argument("--cpu-seconds", type=float, default=10.0)
   ap.add_argument("--no-cpu", action="store_true")
+  ap.add_argument("--only", default=None, help="time one configuration, e.g. bfp4_B1 (for profiling runs)")
   args = ap.parse_args()
   if args.gpus != 1:
     print(f"bench.py runs on one GPU: this build has no multi-GPU path, and --gpus {args.gpus} is not supported",
@@ -146,15 +170,19 @@ def main():
   configs = {}
   for fmt in ("bfp4", "bfp8"):
     for rows in (1, 4, 16):
+      if args.only and args.only != f"{fmt}_B{rows}": continue
       steps = args.steps if (fmt, rows) == ("bfp4", 1) else max(50, args.steps // 4)
-      us, got, x, w = gpu_leg(fmt, rows, steps, args.warmup if (fmt, rows) == ("bfp4", 1) else steps)
+      us, got, x, w, read_us = gpu_leg(fmt, rows, steps, args.warmup if (fmt, rows) == ("bfp4", 1) else steps)
       ok = check(got, x, w, fmt)
       gbs = step_bytes(fmt, rows) / us / 1e3
+      wb = weight_bytes(fmt)
       configs[f"{fmt}_B{rows}"] = {"us_per_step": round(us, 3), "GB/s": round(gbs, 1),
                                    "frac_hbm_peak": round(gbs / PEAK_GBS, 4), "bytes": step_bytes(fmt, rows),
-                                   "steps": steps, "parity": ok}
+                                   "steps": steps, "parity": ok,
+                                   "stream_read_us": round(read_us, 3), "stream_read_GB/s": round(wb / read_us / 1e3, 1),
+                                   "frac_of_stream_read": round(read_us / us, 4)}
       log(fmt, rows, configs[f"{fmt}_B{rows}"])
-  head = configs["bfp4_B1"]
+  head = configs.get("bfp4_B1") or next(iter(configs.values()))
   cpu = None
   if not args.no_cpu:
     us_cpu, n = cpu_leg("bfp4", 1, args.cpu_seconds)
@@ -170,7 +198,7 @@ def main():
     "config": {"workload": "decode GEMV x[1,576] @ W[576,49152] bfp4 (BASELINE config 2, B=1)", "batch_rows": 1,
                "K": K_DIM, "N": N_DIM, "weight_pool_bytes": POOL_BYTES},
     "roofline": {"bound": "hbm", "achieved": head["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
-                 "frac": head["frac_hbm_peak"], "traffic": None},
+                 "frac": head["frac_hbm_peak"], "traffic": measured_traffic()},
     "cpu_baseline": cpu,
     "configs": configs,
   }

@@ -52,6 +52,11 @@ int bt_copy(bt_runtime *rt, uint64_t dst, uint64_t src, uint64_t bytes);
 int bt_fill32(bt_runtime *rt, uint64_t dst, uint32_t value, uint64_t words);
 /* Runtime.wait(timeout) (runtime.py:851-880): BT_ETIMEOUT if the stream is still busy after timeout_s seconds. */
 int bt_wait(bt_runtime *rt, double timeout_s);
+/* No counterpart in the reference (a measurement aid, like probe.py's DRAM probes, probe.py:81): reads `bytes` once
+ * with 16-byte loads and folds them into a word written to scratch_word only for one unlikely value. The plain
+ * streaming read that bench.py sets beside a kernel of the same size, and the known-size read that calibrates the
+ * HBM byte counters. */
+int bt_stream_read(bt_runtime *rt, uint64_t src, uint64_t bytes, uint64_t scratch_word);
 /* Timing for Runtime.profile (runtime.py:773-786): events on the runtime's stream. */
 int bt_event_create(bt_runtime *rt, void **ev);
 int bt_event_record(bt_runtime *rt, void *ev);
@@ -77,9 +82,12 @@ int bt_stream(bt_runtime *rt, void **stream);
  * Columns layout (Tensor.columns(), a matmul's B): tiles of 64 rows (K) by 16 columns (N), ordered
  * [batch][column run][64-row chunk]. A tile is 64 exponent bytes, then its values in the order the 16x16x32 matrix
  * instruction reads B: lane l (0..63) holds rows 32h + 8(l / 16) + j, j = 0..7, of column l % 16, for h = 0, 1.
- * Exponent byte p = 16g + 8h + j belongs to row 32h + 8g + j. bfp8 tiles are 64 + 1024 bytes (lane l's 16 bytes at
- * 64 + 16l), bfp4 tiles 64 + 512 (8 bytes at 64 + 8l), and bf16 tiles 2048 bytes (32 bytes at 32l, no exponents).
- * Rows past K and columns past N are zero. */
+ * Exponent byte p = 16g + 8h + j belongs to row 32h + 8g + j and holds (e - 133) mod 256 (bfp8) or (e - 120) mod 256
+ * (bfp4). bfp8 tiles are 64 + 1024 bytes: lane l's 16 bytes at 64 + 16l, byte 8h + j the signed q of value j.
+ * bfp4 tiles are 64 + 512: lane l's 8 bytes at 64 + 8l, byte 4h + i holding values i (low nibble) and i + 4 (high),
+ * each as sign << 3 | magnitude. bf16 tiles are 2048 bytes (32 bytes at 32l, no exponents). Rows past K and columns
+ * past N are zero. A matmul reads exponents as signed bytes, so it takes block floats whose run exponents e lie in
+ * 5..255 (bfp8) or 0..247 (bfp4); readback is exact for any. */
 
 /* bf16 (round to nearest even first, as gpt2.bfp does: models/gpt2.py:19-30) or fp32 matrices -> plain planes.
  * src strides are in elements. */
