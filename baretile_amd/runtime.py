@@ -42,6 +42,7 @@ class Runtime:
     self.grid, self.readers = None, None  # kernel-cache key parts of the reference; unused here
     self.cores = [None] * 256  # one "worker" per compute unit, for code that sizes work by len(rt.cores)
     self.pins = []  # weak references to recordings, which keep the memory they allocated until they close
+    self.deferred = []  # frees asked for during a capture
 
   def check(self):
     if self.closed: raise RuntimeError("this runtime was closed, or another runtime took over its chip")
@@ -57,15 +58,23 @@ class Runtime:
     return addr.value
 
   def dram_free(self, addr):
-    """Release memory once the launches queued so far have finished. A recording's memory waits for the recording."""
+    """Release memory once the launches queued so far have finished. A recording's memory waits for the recording;
+    memory dropped while a recording captures is released after the capture ends."""
     if self.closed or not addr: return
-    if self.recording is not None and addr in self.recording.made: return
+    if self.recording is not None:
+      if addr not in self.recording.made: self.deferred.append(addr)
+      return
     for rec in list(self.pins):
       r = rec()
       if r is not None and addr in r.made:
         r.freed.add(addr)
         return
     _lib.call("free", self.handle, int(addr), 0)
+
+  def release_deferred(self):
+    """Frees held back during a capture, now that it has ended."""
+    held, self.deferred = self.deferred, []
+    for addr in held: self.dram_free(addr)
 
   def upload(self, addr, data):
     """Copy host bytes to device memory; returns once they have arrived."""

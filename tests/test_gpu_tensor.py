@@ -1,0 +1,221 @@
+"""The Tensor surface on the GPU, checked the way the reference's own tests check it (test/test_kernels.py), against
+NumPy and the oracle. Needs a GPU."""
+import math
+import numpy as np
+import pytest
+
+from baretile_amd.tensor import Tensor, jit
+from oracle import bfp as B, ops
+
+pytestmark = pytest.mark.gpu
+
+
+def bf(v): return float(B.bf16(np.float32(v)))
+
+
+def packed(v):  # half-up bf16 rounding of a computed result (test/conftest.py:11-13)
+  b = np.asarray(v, np.float32).view(np.uint32).astype(np.uint64)
+  return (((b + 0x8000) >> 16) << 16).astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def value(t): return np.array(t.tolist()).reshape(t.shape)
+
+
+def test_readme_and_ramp_known_answers(rt):
+  # README.md:74-83 and ramps/1_tensors.py:27-31
+  x, w = Tensor.of(rt, [[1.0, 2.0], [3.0, 4.0]]), Tensor.of(rt, [[2.0, 0.0], [0.0, 3.0]])
+  assert ((x @ w).relu()).tolist() == [[2.0, 6.0], [6.0, 12.0]]
+  assert (x @ x).relu().tolist() == [[7.0, 10.0], [15.0, 22.0]]
+
+
+def test_round_trip_formats(rt):
+  rng = np.random.default_rng(0)
+  a = rng.normal(0, 3, (3, 5, 7))
+  assert value(Tensor.of(rt, a.tolist(), "fp32")).tolist() == a.astype(np.float32).astype(np.float64).tolist()
+  assert value(Tensor.of(rt, a.tolist())).tolist() == B.bf16(a).astype(np.float64).tolist()
+  i = rng.integers(-2**31, 2**31 - 1, (4, 9))
+  assert Tensor.of(rt, i.tolist(), "int32").tolist() == i.tolist()
+
+
+def test_matmul_exact(rt):
+  # test_kernels.py:637-651
+  a = [[float((r * 7 + c * 3) % 3 - 1) for c in range(64)] for r in range(32)]
+  b = [[float((r * 5 + c) % 3 - 1) for c in range(32)] for r in range(64)]
+  assert (Tensor.of(rt, a) @ Tensor.of(rt, b)).tolist() == (np.array(a) @ np.array(b)).tolist()
+  rng = np.random.default_rng(1)
+  x = [[bf(v) for v in row] for row in rng.uniform(-8, 8, (96, 64))]
+  eye = np.eye(64).tolist()
+  assert (Tensor.of(rt, x) @ Tensor.of(rt, eye)).tolist() == x
+  d = [bf(v) for v in rng.uniform(1, 2, 64)]
+  diag = np.diag(d).tolist()
+  assert (Tensor.of(rt, x) @ Tensor.of(rt, diag)).tolist() == packed(np.array(x) * np.array(d)).tolist()
+
+
+def test_matmul_transposed_and_batched(rt):
+  rng = np.random.default_rng(2)
+  a, b = B.bf16(rng.uniform(-1, 1, (3, 40, 70))), B.bf16(rng.uniform(-1, 1, (3, 50, 70)))
+  got = value(Tensor.of(rt, a) @ Tensor.of(rt, b).T)
+  want = a @ b.transpose(0, 2, 1)
+  assert np.all(np.abs(got - want) <= 2.0 ** -8 * (np.abs(a) @ np.abs(b).transpose(0, 2, 1)))
+  one = B.bf16(rng.uniform(-1, 1, (70, 30)))  # a batch of A against one B
+  got = value(Tensor.of(rt, a) @ Tensor.of(rt, one))
+  assert np.all(np.abs(got - a @ one) <= 2.0 ** -8 * (np.abs(a) @ np.abs(one)))
+
+
+@pytest.mark.parametrize("dtype", ["bfp8", "bfp4"])
+def test_bfp(rt, dtype):
+  # test_kernels.py:709-724: a matmul by a block-float B is bit for bit the bf16 matmul by its values; then fused with
+  # what follows and with a bf16 matmul
+  rng = np.random.default_rng(5)
+  on = lambda *shape: Tensor.of(rt, rng.normal(0, 1, shape).tolist())
+  for b, m, k, n in ((1, 64, 9000, 40), (1, 1, 768, 2304), (1, 100, 256, 200), (2, 100, 256, 96), (1, 32, 2048, 64)):
+    x, w = on(b, m, k), on(b, k, n).cast(dtype)
+    assert (x @ w).tolist() == (x @ Tensor.of(rt, w.tolist())).tolist(), (b, m, k, n)
+  x, w, v, bias = on(64, 192), on(192, 96).cast(dtype), on(192, 96), on(1, 96)
+  assert (x @ w + x @ v + bias).relu().tolist() == (x @ Tensor.of(rt, w.tolist()) + x @ v + bias).relu().tolist()
+
+
+@pytest.mark.parametrize("dtype", ["bfp8", "bfp4"])
+def test_bfp_numpy(rt, dtype):
+  # test_models.py:587-593: the device's cast equals the NumPy model's, bit for bit, on N(0,1) * e^N(0,2)
+  rng = np.random.default_rng(5)
+  a = rng.normal(0, 1, (64, 96)) * np.exp(rng.normal(0, 2, (64, 96)))
+  got = np.array(Tensor.of(rt, a.tolist()).cast(dtype).tolist())
+  assert np.array_equal(got, B.bfp(B.bf16(a), dtype))
+  got = np.array(Tensor.of(rt, a.tolist()).cast(dtype).columns().tolist())  # by columns reads back unchanged
+  assert np.array_equal(got, B.bfp(B.bf16(a), dtype))
+
+
+def test_put_block_float_known_answer(rt):
+  # test_kernels.py:2096-2103: [2, 3] cast among zeros reads back as bf16 0x4000, 0x4040
+  for dtype in ("bfp8", "bfp4"):
+    row = Tensor.of(rt, [[2.0, 3.0] + [0.0] * 30]).cast(dtype)
+    bits = np.frombuffer(row.tobytes(), np.uint16)
+    assert list(bits[:2]) == [0x4000, 0x4040]
+
+
+def unfused(t):  # the same tree with one launch per op
+  if t.op is None: return t
+  srcs = [unfused(s) if isinstance(s, Tensor) else s for s in t.srcs]
+  if t.op == "matmul": return (srcs[0] @ srcs[1]).realize()
+  out = Tensor(t.rt, t.rows, t.cols, t.op, tuple(srcs), t.batch, t.dtype, t.args)
+  out.lead = t.lead
+  return out.realize()
+
+
+def test_fusion(rt):
+  # test_kernels.py:987-1004: a fused chain gives the bits of one launch per op
+  rng = np.random.default_rng(3)
+  a, b, c, d = (Tensor.of(rt, B.bf16(rng.uniform(-3, 3, (128, 96))).tolist()) for _ in range(4))
+  for build in (lambda a, b, c, d: (a + b) * c - d * a, lambda a, b, c, d: (a + b) * ((c - d) + a * a)):
+    launches = rt.launches
+    got = build(a, b, c, d).tolist()
+    assert rt.launches - launches == 1, "one kernel"
+    assert got == unfused(build(a, b, c, d)).tolist()
+
+
+def test_matmul_fusion(rt):
+  # test_kernels.py:1081-1092
+  rng = np.random.default_rng(4)
+  rnd = lambda r, c: Tensor.of(rt, B.bf16(rng.uniform(-1, 1, (r, c))).tolist())
+  a, b, c, d, e, f = rnd(64, 96), rnd(96, 128), rnd(64, 128), rnd(64, 128), rnd(64, 64), rnd(64, 128)
+  for build in (lambda: (a @ b) + c, lambda: (a @ b) * d - c, lambda: (a @ b) + (e @ f)):
+    assert build().tolist() == unfused(build()).tolist()
+
+
+def test_fused_cast(rt):
+  # test_kernels.py:1006-1020: a cast at the root is part of the kernel and equals casting the computed value
+  rng = np.random.default_rng(16)
+  x, y = (Tensor.of(rt, rng.normal(0, 2, (70, 100)).astype(np.float32).tolist(), "fp32") for _ in range(2))
+  a, b, c = (Tensor.of(rt, rng.normal(0, 2, s).tolist()) for s in ((70, 100), (70, 100), (100, 40)))
+  for build in (lambda: (x * 3 + y).bfloat16(), lambda: (x * 50 + y).cast("int32"), lambda: (x * y).sum(1).bfloat16(),
+                lambda: (a * b + a).float(), lambda: a.softmax(-1).float(), lambda: (a @ c).float()):
+    fused = build().realize()
+    t = build()
+    t.srcs[0].realize()
+    assert fused.tobytes() == t.realize().tobytes()
+
+
+def test_reductions_and_softmax(rt):
+  rng = np.random.default_rng(8)
+  a = rng.normal(0, 1, (2, 3, 50, 70))
+  t = Tensor.of(rt, a.tolist(), "fp32")
+  for axis in (None, 0, 1, 2, 3, -1):
+    want = a.astype(np.float32).astype(np.float64).sum(axis=axis, keepdims=True)
+    assert np.allclose(value(t.sum(axis)), want, rtol=1e-5, atol=1e-4), axis
+    assert np.allclose(value(t.max(axis)), a.astype(np.float32).max(axis=axis, keepdims=True)), axis
+  s = Tensor.of(rt, a[0, 0].tolist(), "fp32").softmax(-1)
+  assert np.allclose(value(s), ops.softmax(a[0, 0].astype(np.float32)), rtol=1e-5, atol=1e-6)
+
+
+def test_elementwise_ops_against_numpy(rt):
+  rng = np.random.default_rng(9)
+  a = rng.uniform(0.5, 3, (40, 70)).astype(np.float32)
+  t = Tensor.of(rt, a.tolist(), "fp32")
+  checks = [(t.exp(), np.exp(a)), (t.log(), np.log(a)), (t.sqrt(), np.sqrt(a)), (t.reciprocal(), 1 / a),
+            (t.rsqrt(), 1 / np.sqrt(a)), (t.sigmoid(), 1 / (1 + np.exp(-a))), (t.silu(), a / (1 + np.exp(-a))),
+            (t.gelu(), ops.gelu(a)), (t.maximum(1.5), np.maximum(a, 1.5)), (t.minimum(1.5), np.minimum(a, 1.5)),
+            ((t > 1.5).where(t, -t), np.where(a > 1.5, a, -a)), (t.sin(), np.sin(a)), (t.cos(), np.cos(a))]
+  for got, want in checks: assert np.allclose(value(got), want, rtol=2e-5, atol=2e-6)
+
+
+def test_views_slices_split_merge(rt):
+  rng = np.random.default_rng(10)
+  a = B.bf16(rng.normal(0, 1, (6, 40, 96)))
+  t = Tensor.of(rt, a.tolist())
+  assert np.array_equal(value(t[2]), a[2:3])
+  assert np.array_equal(value(t[1:5:2, 3:30:3, 7:90]), a[1:5:2, 3:30:3, 7:90])
+  m = Tensor.of(rt, a[0].tolist())
+  parts = m.split(3)
+  assert np.array_equal(value(parts), a[0].reshape(40, 3, 32).transpose(1, 0, 2))
+  assert np.array_equal(value(parts.merge()), a[:1])
+  assert np.array_equal(value((parts * 2).merge()), a[:1] * 2)
+  assert np.array_equal(value(t.T), a.transpose(0, 2, 1))
+  assert np.array_equal(value(t.reshape(3, 2, 40, 96)), a.reshape(3, 2, 40, 96))
+  r = Tensor.of(rt, a[:2].tolist()).repeat_interleave(3)
+  assert np.array_equal(value(r + 0), np.repeat(a[:2], 3, 0))
+
+
+def test_leading_broadcast(rt):
+  rng = np.random.default_rng(11)
+  a, b = rng.normal(0, 1, (2, 1, 5, 7)), rng.normal(0, 1, (1, 3, 5, 7))
+  got = value(Tensor.of(rt, a.tolist(), "fp32") + Tensor.of(rt, b.tolist(), "fp32"))
+  assert np.allclose(got, (a.astype(np.float32) + b.astype(np.float32)))
+
+
+def test_gather_put_attend(rt):
+  rng = np.random.default_rng(12)
+  table = B.bf16(rng.normal(0, 1, (300, 64)))
+  t = Tensor.of(rt, table.tolist())
+  assert np.array_equal(value(t.gather([5, 299, 0, 5])), table[None, [5, 299, 0, 5]])
+  with pytest.raises(IndexError): t.gather([300])
+  cache = Tensor.zeros(rt, 96, 64, batch=4)
+  x = B.bf16(rng.normal(0, 1, (4, 3, 64)))
+  cache.put(Tensor.of(rt, [[10, 20, 10]], "int32"), Tensor.of(rt, x.tolist()))
+  want = np.zeros((4, 96, 64))
+  want[:, 20], want[:, 10] = x[:, 1], x[:, 2]
+  assert np.array_equal(value(cache), want)
+  q = B.bf16(rng.normal(0, 1, (8, 5, 64)) / 8)
+  k, v = B.bf16(rng.normal(0, 1, (2, 96, 64))), B.bf16(rng.normal(0, 1, (2, 96, 64)))
+  places = rng.integers(40, 96, (1, 5, 1))
+  kt, vt = Tensor.of(rt, k.tolist()).repeat_interleave(4), Tensor.of(rt, v.tolist()).repeat_interleave(4)
+  got = value(Tensor.of(rt, q.tolist()).attend(kt, vt, Tensor.of(rt, places.tolist(), "int32")))
+  assert np.allclose(got, ops.attention(q, k, v, places, 0, 4), rtol=0.011, atol=0.011)
+
+
+def test_jit_replays_with_new_inputs(rt):
+  rng = np.random.default_rng(13)
+  w = Tensor.of(rt, rng.normal(0, 0.1, (64, 96)).tolist()).cast("bfp8").columns()
+  f = jit(lambda x: (x @ w).relu() * 2)
+  xs = [Tensor.of(rt, rng.normal(0, 1, (4, 64)).tolist()) for _ in range(5)]
+  want = [((x @ w).relu() * 2).tolist() for x in xs]
+  got = [f(x).tolist() for x in xs]
+  assert got == want
+
+
+def test_errors(rt):
+  x = Tensor.of(rt, [[1.0, 2.0]])
+  with pytest.raises(ValueError): Tensor.of(rt, [])
+  with pytest.raises(ValueError): x @ Tensor.of(rt, [[1.0, 2.0]])
+  with pytest.raises(ValueError): x.cast("fp8")
+  with pytest.raises(ValueError): x + Tensor.of(rt, [[1.0, 2.0, 3.0]])
