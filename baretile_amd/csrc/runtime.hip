@@ -34,6 +34,7 @@ int enter(bt_runtime *rt, Runtime **out) {
   if (!r) return fail(BT_EINVAL, "no runtime");
   if (r->closed) return fail(BT_ESTATE, "the runtime is closed");
   BT_HIP(hipSetDevice(r->device));
+  (void)hipGetLastError();  // an error left by an earlier call must not be blamed on this one's launch
   *out = r;
   return BT_OK;
 }

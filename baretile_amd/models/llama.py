@@ -1,0 +1,218 @@
+"""Llama-family decoders on baretile_amd tensors: the device side of baretile/models/llama.py.
+
+The functions keep the reference's names and meaning (llama.py:48-373): precision, rms, rope, rotary, fuse, layer,
+attention, mlp, forward, prefill, kv_cache, upload. They run on Tensor only. The NumPy twin that the reference keeps
+in the same functions is this repository's CPU oracle (oracle/llama_ref.py), which the tests compare against.
+
+The numbers follow the reference's device path (llama.py:88-183):
+  - the residual stream is fp32 and each half of a block adds onto it in its last matmul's kernel;
+  - RMSNorm reads the stream rounded to bf16, then rounds each step in bf16;
+  - RoPE takes bf16 tables that carry 1/sqrt(head width) for q's heads (llama.py:209-227);
+  - the MLP is silu(gate) * up with gate and up side by side (llama.py:174-183);
+  - attention runs in one kernel from each token's place.
+Llama-family only: Qwen's DeltaNet and experts, gpt-oss sinks and sliding windows other than the plain causal one
+are outside this backend's scope.
+"""
+import math
+from types import SimpleNamespace
+import numpy as np
+from baretile_amd.tensor import Tensor, jit
+
+
+def model(**kw):
+  """A config: dim, heads, kv, layers, eps, theta, vocab, ffn, and optionally head_dim and precision."""
+  base = dict(head_dim=None, vocab=None, ffn=None, precision=None)
+  return SimpleNamespace(**(base | kw))
+
+
+def smol(layers=30, vocab=49152):
+  """SmolLM-135M's shapes (test/test_models.py:639-645): 576 wide, 9 query and 3 KV heads of 64, FFN 1536."""
+  return model(dim=576, heads=9, kv=3, layers=layers, eps=1e-5, theta=10000.0, vocab=vocab, ffn=1536)
+
+
+def head(c): return c.head_dim or c.dim // c.heads
+
+
+def precision(c, mode="bf16", kv=None):
+  """{(op, block): (format, phases)}, as llama.py:48-83 gives for the Llama family. bf16 and bfp8 put every matrix
+  and the output layer in that format; bfp4 puts gate_up in bfp4 and the rest in bfp8; tt is tt_transformers'
+  performance mode. Phases are kept as data: the matrix cores multiply bf16 exactly at any count."""
+  if mode not in ("bf16", "bfp8", "bfp4", "tt"): raise ValueError(f"unknown precision mode: {mode}")
+  if kv is not None and kv not in ("bf16", "bfp8", "bfp4"): raise ValueError(f"unknown KV cache format: {kv}")
+  def entry(op):
+    if mode in ("bf16", "bfp8"): return mode, 4
+    fmt = "bfp4" if op == "gate_up" else "bfp8"
+    return fmt, (1 if fmt == "bfp4" else 2) if mode == "tt" else 4
+  table = {(op, l): entry(op) for l in range(c.layers) for op in ("qkv", "o", "gate_up", "down")}
+  if mode == "tt" and (c.layers, c.dim) == (32, 4096): table["gate_up", 31] = ("bfp8", 2)
+  table["head", None] = entry("head")
+  table["attention", "decode"] = (None, 2 if mode == "tt" else 4)
+  table["attention", "prefill"] = (None, 4)
+  table["kv", None] = (kv or ("bfp8" if mode == "tt" else "bf16"), None)
+  return table
+
+
+def weight_format(name, prec):
+  """A weight's storage format (llama.py:464-474): the block matrices and the output layer from prec, else bf16."""
+  if not prec: return "bf16"
+  if name == "embed.T": key = ("head", None)
+  elif name.startswith("layers.") and name.endswith("_proj"):
+    key = (name.split(".")[-1][:-len("_proj")], int(name.split(".")[1]))
+  else: return "bf16"
+  return prec.get(key, ("bf16", 4))[0]
+
+
+def _bf16(a):  # float32 rounded to bf16 (nearest even) and back
+  b = np.asarray(a, np.float32).view(np.uint32).astype(np.uint64)
+  return (((b + 0x7FFF + (b >> 16 & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
+
+
+def frequencies(c):
+  """RoPE's inverse frequencies, in fp32 as Hugging Face computes them (llama.py:187-192)."""
+  hd = head(c)
+  return (1 / c.theta ** (np.arange(0, hd, 2, dtype=np.float32) / hd)).astype(np.float32)
+
+
+def rotary(c, n):
+  """(cos, sin, turn) for positions 0 .. n-1 (llama.py:209-227). The tables are bf16 and repeat a head's row across
+  the heads of q, k and v: q's carry 1/sqrt(head width), v's have cos 1 and sin 0. x @ turn is (-x2, x1)."""
+  hd = head(c)
+  angles = np.arange(n, dtype=np.float32)[:, None] * frequencies(c)[None]
+  def table(g, still):
+    t = np.concatenate([g(angles), g(angles)], 1).astype(np.float32)
+    heads = [t * np.float32(hd ** -0.5)] * c.heads + [t] * c.kv + [np.full_like(t, still)] * c.kv
+    return _bf16(np.concatenate(heads, 1))
+  turn = np.zeros((hd, hd), np.float32)
+  half = np.arange(hd // 2)
+  turn[half + hd // 2, half], turn[half, half + hd // 2] = -1, 1
+  return table(np.cos, 1.0), table(np.sin, 0.0), turn
+
+
+def fuse(w, c):
+  """q, k, v side by side as qkv_proj, and gate, up as gate_up_proj, in each block (llama.py:238-291)."""
+  w = dict(w)
+  for l in range(c.layers):
+    p = f"layers.{l}."
+    if p + "q_proj" in w:
+      w[p + "qkv_proj"] = np.concatenate([w.pop(p + n) for n in ("q_proj", "k_proj", "v_proj")], 1)
+    if p + "gate_proj" in w:
+      w[p + "gate_up_proj"] = np.concatenate([w.pop(p + n) for n in ("gate_proj", "up_proj")], 1)
+  return w
+
+
+def upload(rt, w, c, places=None):
+  """NumPy weights (laid out for x @ w, q/k/v and gate/up fused) to the device (llama.py:479-495). Matrices go to
+  their precision's format and into the matmul's tiles once; norms and the embedding stay bf16; the tied output layer
+  is embed.T in the head's format. Adds the RoPE tables for `places` positions."""
+  prec = c.precision
+  out = {}
+  for name, a in w.items():
+    if name in ("cos", "sin", "turn"): continue
+    a = np.asarray(a, np.float32)
+    if a.ndim == 1: a = a[None]
+    t = Tensor.of(rt, a)
+    if name.endswith("_proj") or name == "embed.T":
+      fmt = weight_format(name, prec)
+      t = (t.cast(fmt) if fmt != "bf16" else t).columns()
+    out[name] = t
+  if "embed.T" not in out: out["embed.T"] = Tensor.of(rt, np.ascontiguousarray(np.asarray(w["embed"], np.float32).T)).cast(
+    weight_format("embed.T", prec) if weight_format("embed.T", prec) != "bf16" else "bf16").columns()
+  if places:
+    cos, sin, turn = rotary(c, places)
+    out["cos"], out["sin"], out["turn"] = Tensor.of(rt, cos), Tensor.of(rt, sin), Tensor.of(rt, turn).columns()
+  return out
+
+
+def kv_cache(rt, c, size):
+  """A (2 * kv, size, head) bf16 cache of zeros per block: key heads, then value heads (llama.py:365-373)."""
+  return [Tensor.zeros(rt, size, head(c), batch=2 * c.kv) for _ in range(c.layers)]
+
+
+def rms(x, w, c):
+  """RMSNorm of the stream rounded to bf16, scaled by w (llama.py:88-95)."""
+  x = x.bfloat16()
+  return x * ((x * x).mean(2) + c.eps).rsqrt() * w
+
+
+def rope(x, cos, sin, turn):
+  """x cos + (x @ turn) sin (llama.py:103-104); the matmul runs the rest as its epilogue."""
+  return x * cos + (x @ turn) * sin
+
+
+def attention(h, p, c, rot, places, cache, rows):
+  """One block's attention over its cache (llama.py:132-172): qkv, RoPE written straight into the heads' row layout,
+  the new keys and values put into the cache at rows, then one attention kernel from each token's place."""
+  hd, rep, nh = head(c), c.heads // c.kv, c.heads + 2 * c.kv
+  qkv = h.matmul(p["qkv_proj"])
+  qkv = rope(qkv.split(nh), rot[0].split(nh), rot[1].split(nh), rot[2]).merge()
+  heads = qkv.split(nh)
+  cache.put(rows, heads[c.heads:c.heads + 2 * c.kv, :, :])
+  q, k, v = heads[:c.heads, :, :], cache[:c.kv, :, :], cache[c.kv:, :, :]
+  o = q.attend(k.repeat_interleave(rep), v.repeat_interleave(rep), places)
+  return o.merge().matmul(p["o_proj"], "fp32")
+
+
+def mlp(h, p):
+  """SwiGLU: silu(h @ gate) * (h @ up), then down, with gate and up side by side (llama.py:174-183)."""
+  m = p["down_proj"].rows
+  gate_up = h.matmul(p["gate_up_proj"])
+  return (gate_up[:, :m].silu() * gate_up[:, m:]).matmul(p["down_proj"], "fp32")
+
+
+def block(w, l):
+  pre = f"layers.{l}."
+  return {k[len(pre):]: v for k, v in w.items() if k.startswith(pre)}
+
+
+def layer(x, p, c, rot, places, cache, rows):
+  """Attention, then the MLP, each after an RMSNorm and added onto the fp32 stream in its own kernel (llama.py:106-130)."""
+  x = (x + attention(rms(x, p["input_layernorm"], c), p, c, rot, places, cache, rows)).realize()
+  return (x + mlp(rms(x, p["post_attention_layernorm"], c), p)).realize()
+
+
+def forward(ids, places, w, c, caches, every=False):
+  """Logits after ids (an int32 row) at places (an int32 row), updating each block's cache (llama.py:325-354):
+  the last token's, or every token's with every, in fp32."""
+  n = ids.cols
+  x = w["embed"].gather(ids).float()
+  rot = (w["cos"].gather(places), w["sin"].gather(places), w["turn"])
+  column = places.reshape(1, n, 1)
+  blocks = [block(w, l) for l in range(c.layers)]
+  for l in range(c.layers): x = layer(x, blocks[l], c, rot, column, caches[l], places)
+  h = rms(x, w["norm"], c)
+  if not every and n > 1: h = h[:, n - 1:n, :]  # the last token's row
+  return h.matmul(w["embed.T"], "fp32")
+
+
+def prefill(ids, w, c, caches, tokens):
+  """A prompt from position 0 in chunks of `tokens` (llama.py:356-363); the logits after its last token."""
+  if not len(ids) or tokens < 1: raise ValueError("prefill needs a nonempty prompt and a chunk of at least one token")
+  rt = w["norm"].rt
+  for i in range(0, len(ids), tokens):
+    out = forward(Tensor.of(rt, [list(ids[i:i + tokens])], "int32"),
+                  Tensor.of(rt, [list(range(i, min(i + tokens, len(ids))))], "int32"), w, c, caches)
+  return out
+
+
+def argmax(logits):
+  """The index of the largest of one row of fp32 logits, read back once."""
+  return int(np.argmax(np.frombuffer(logits.tobytes(), np.float32)))
+
+
+def generate(w, c, prompt, steps, size, feed=None):
+  """Greedy decode: prefill the prompt, then `steps` tokens, each step one replay of the recorded forward (jit).
+  With feed, step i is fed feed[i] instead of its own pick (the reference's NumPy-fed protocol, gpt2.py:147-161).
+  Returns (picks, per-step logits as float32 arrays)."""
+  rt = w["norm"].rt
+  caches = kv_cache(rt, c, size)
+  logits = prefill(prompt, w, c, caches, len(prompt))
+  step = jit(lambda i, p: forward(i, p, w, c, caches))
+  picks, outs = [], []
+  for s in range(steps):
+    row = np.frombuffer(logits.tobytes(), np.float32).copy()
+    outs.append(row)
+    picks.append(int(np.argmax(row)))
+    if s + 1 == steps: break
+    tok = picks[-1] if feed is None else feed[s]
+    logits = step(Tensor.of(rt, [[tok]], "int32"), Tensor.of(rt, [[len(prompt) + s]], "int32"))
+  return picks, outs

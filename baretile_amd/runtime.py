@@ -41,40 +41,33 @@ class Runtime:
     self.times = []  # (launch, name, start event, end event) while timing
     self.grid, self.readers = None, None  # kernel-cache key parts of the reference; unused here
     self.cores = [None] * 256  # one "worker" per compute unit, for code that sizes work by len(rt.cores)
-    self.pins = []  # weak references to recordings, which keep the memory they allocated until they close
-    self.deferred = []  # frees asked for during a capture
+    self.deferred = []  # (address, captured) frees asked for during a capture
 
   def check(self):
     if self.closed: raise RuntimeError("this runtime was closed, or another runtime took over its chip")
 
   # ---- memory
   def dram_alloc(self, size):
-    """Allocate size bytes of device memory (at least 256, aligned to 256) from the stream-ordered pool. Memory
-    allocated while a jit recording is open stays with the recording."""
+    """Allocate size bytes of device memory (at least 256, aligned to 256): from the stream-ordered pool, or, while
+    a jit recording captures, a plain allocation that the recording's graph keeps using."""
     self.check()
     addr = c_uint64()
     _lib.call("alloc", self.handle, int(size), byref(addr))
-    if self.recording is not None: self.recording.made.add(addr.value)
     return addr.value
 
-  def dram_free(self, addr):
-    """Release memory once the launches queued so far have finished. A recording's memory waits for the recording;
-    memory dropped while a recording captures is released after the capture ends."""
+  def dram_free(self, addr, captured=False):
+    """Release memory once the launches queued so far have finished (runtime.py:814-820). Frees asked for while a
+    recording captures wait until the capture has ended; memory allocated during a capture is freed by hipFree."""
     if self.closed or not addr: return
     if self.recording is not None:
-      if addr not in self.recording.made: self.deferred.append(addr)
+      self.deferred.append((addr, captured))
       return
-    for rec in list(self.pins):
-      r = rec()
-      if r is not None and addr in r.made:
-        r.freed.add(addr)
-        return
-    _lib.call("free", self.handle, int(addr), 0)
+    _lib.call("free", self.handle, int(addr), 1 if captured else 0)
 
   def release_deferred(self):
     """Frees held back during a capture, now that it has ended."""
     held, self.deferred = self.deferred, []
-    for addr in held: self.dram_free(addr)
+    for addr, captured in held: self.dram_free(addr, captured)
 
   def upload(self, addr, data):
     """Copy host bytes to device memory; returns once they have arrived."""

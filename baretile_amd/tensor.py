@@ -58,16 +58,19 @@ def _bf16_bits(values):
 
 
 class Storage:
-  """Device memory that tensors share. Freed, stream-ordered, when the last tensor using it goes."""
-  __slots__ = ("rt", "addr", "nbytes", "columns", "__weakref__")
+  """Device memory that tensors share, freed when the last tensor using it goes. Memory allocated while a jit
+  recording captures belongs to the recording too, which keeps it for as long as its graph can replay."""
+  __slots__ = ("rt", "addr", "nbytes", "columns", "captured", "__weakref__")
 
   def __init__(self, rt, nbytes):
-    self.rt, self.nbytes, self.columns = rt, nbytes, None
+    self.rt, self.nbytes, self.columns, self.addr = rt, nbytes, None, None
+    self.captured = rt.recording is not None
     self.addr = rt.dram_alloc(max(256, nbytes))
+    if self.captured: rt.recording.storages.append(self)
 
   def __del__(self):
     try:
-      if self.addr is not None: self.rt.dram_free(self.addr)
+      if self.addr is not None: self.rt.dram_free(self.addr, self.captured)
     except Exception:
       pass
 
@@ -938,16 +941,14 @@ def _realize_matmul(m, root, into):
 
 # ---- jit
 class Recording:
-  """Launches captured into a HIP graph, with the memory they allocated, for replay (tensor.py:1171-1229)."""
+  """Launches captured into a HIP graph for replay, holding the memory they allocated (tensor.py:1171-1229)."""
   def __init__(self, rt):
-    self.rt, self.graph, self.made, self.freed, self.active = rt, None, set(), set(), False
-    self._ref = weakref.ref(self)
+    self.rt, self.graph, self.storages, self.held, self.active = rt, None, [], [], False
 
   def __enter__(self):
     if self.rt.recording is not None: raise RuntimeError("cannot nest recordings on the same runtime")
     self.close()
     self.rt.recording = self
-    self.rt.pins.append(self._ref)
     self.active = True
     _lib.call("graph_begin", self.rt.handle)
     return self
@@ -956,25 +957,27 @@ class Recording:
     g = ctypes.c_void_p()
     try: _lib.call("graph_end", self.rt.handle, ctypes.byref(g))
     finally:
+      # memory let go during the capture may still be read by the graph: it is freed with the graph
       self.rt.recording, self.active = None, False
-      self.rt.release_deferred()
+      self.held, self.rt.deferred = self.held + self.rt.deferred, []
     self.graph = g
     if kind is not None: self.close()
 
   def send(self):
+    """Queue the recorded launches once more."""
     if self.active or self.graph is None: raise RuntimeError("recording is not ready for replay")
     _lib.call("graph_launch", self.rt.handle, self.graph)
     self.rt.launches += 1
 
   def close(self):
+    """Destroy the graph, then let go of its memory: storage no live tensor holds is freed."""
     if self.graph is not None and not self.rt.closed:
+      self.rt.wait()
       _lib.call("graph_destroy", self.graph)
     self.graph = None
-    if not self.rt.closed:
-      for addr in self.made:
-        try: _lib.call("free", self.rt.handle, addr, 1)
-        except Exception: pass
-    self.made, self.freed = set(), set()
+    self.storages = []
+    held, self.held = self.held, []
+    for addr, captured in held: self.rt.dram_free(addr, captured)
 
   def __del__(self):
     try:

@@ -1,0 +1,68 @@
+"""The Llama decoder on the GPU against the NumPy oracle (oracle/llama_ref.py), with SmolLM-135M's shapes and random
+weights, as test/test_models.py checks its chip path against its NumPy path. Needs a GPU."""
+import numpy as np
+import pytest
+
+from baretile_amd.models import llama
+from baretile_amd.tensor import Tensor
+from oracle import llama_ref as L
+
+pytestmark = pytest.mark.gpu
+
+
+def setup(rt, layers, vocab, mode, places=96, seed=12):
+  rng = np.random.default_rng(seed)
+  c, w = L.smol(rng, layers, vocab=vocab, places=places)
+  prec = L.precision(c, mode)
+  ref = L.arrays(w, prec)  # the weights as the device holds them: block floats rounded as cast rounds them
+  dc = llama.model(dim=576, heads=9, kv=3, layers=layers, eps=1e-5, theta=10000.0, vocab=vocab, ffn=1536,
+                   precision=llama.precision(llama.model(layers=layers, dim=576), mode))
+  host = {k: v for k, v in w.items() if k not in ("cos", "sin", "turn", "embed.T")}
+  dw = llama.upload(rt, host, dc, places=places)
+  return c, ref, dc, dw
+
+
+@pytest.mark.parametrize("mode", ["bf16", "bfp8"])
+def test_block_and_logits_match_numpy(rt, mode):
+  # test_models.py:818-851: a prompt, then a decode step against the cache, within 3% of the largest logit
+  c, ref, dc, dw = setup(rt, 2, 256, mode)
+  ids = [7, 200, 31, 64, 5, 9, 100, 3]
+  caches = llama.kv_cache(rt, dc, 96)
+  got = np.array(llama.forward(Tensor.of(rt, [ids], "int32"), Tensor.of(rt, [list(range(8))], "int32"), dw, dc, caches,
+                               every=True).tolist())
+  want = L.forward(ids, range(8), ref, c, L.kv_cache(c, 96), every=True)
+  assert np.abs(got - want).max() <= 0.03 * np.abs(want).max(), np.abs(got - want).max()
+  assert (got.argmax(-1) == want.argmax(-1)).mean() >= 0.75
+  rcaches = L.kv_cache(c, 96)
+  L.forward(ids, range(8), ref, c, rcaches)
+  step = np.array(llama.forward(Tensor.of(rt, [[42]], "int32"), Tensor.of(rt, [[8]], "int32"), dw, dc, caches).tolist())[0]
+  want = L.forward([42], [8], ref, c, rcaches)[0]
+  assert np.abs(step - want).max() <= 0.03 * np.abs(want).max()
+
+
+def test_greedy_decode_numpy_fed(rt):
+  # gpt2.py:147-161's protocol: both sides are fed the NumPy pick each step; their picks agree where the NumPy top two
+  # are apart by more than the device's logit error
+  c, ref, dc, dw = setup(rt, 2, 512, "bfp8", places=64, seed=3)
+  rng = np.random.default_rng(0)
+  prompt = [int(i) for i in rng.integers(0, 512, 16)]
+  want_toks, want_logits = L.greedy(prompt, 24, ref, c, 64)
+  got_toks, got_logits = llama.generate(dw, dc, prompt, 24, 64, feed=want_toks)
+  for s, (g, wl) in enumerate(zip(got_logits, want_logits)):
+    top2 = np.sort(wl)[-2:]
+    err = np.abs(g - wl).max()
+    assert err <= 0.03 * np.abs(wl).max(), (s, err)
+    if top2[1] - top2[0] > 2 * err: assert got_toks[s] == want_toks[s], s
+
+
+def test_jit_decode_matches_eager(rt):
+  c, ref, dc, dw = setup(rt, 2, 256, "bfp8", places=64)
+  prompt = [3, 1, 4, 1, 5, 9, 2, 6]
+  a, _ = llama.generate(dw, dc, prompt, 6, 64)
+  caches = llama.kv_cache(rt, dc, 64)
+  logits = llama.prefill(prompt, dw, dc, caches, len(prompt))
+  b = []
+  for s in range(6):
+    b.append(llama.argmax(logits))
+    logits = llama.forward(Tensor.of(rt, [[b[-1]]], "int32"), Tensor.of(rt, [[len(prompt) + s]], "int32"), dw, dc, caches)
+  assert a == b
