@@ -45,7 +45,8 @@ class AttentionArgs(ctypes.Structure):
               ("q_sh", c_int64), ("q_sr", c_int64), ("k_sh", c_int64), ("k_sr", c_int64), ("v_sh", c_int64),
               ("v_sr", c_int64), ("o_sh", c_int64), ("o_sr", c_int64), ("places_sh", c_int64),
               ("heads", c_int32), ("rep", c_int32), ("rows", c_int32), ("keys", c_int32), ("head_dim", c_int32),
-              ("window", c_int32)]
+              ("window", c_int32), ("parts", c_int32), ("pad_", c_int32), ("scratch", c_uint64),
+              ("scratch_bytes", c_uint64)]
 
 
 RT = c_void_p
@@ -68,6 +69,7 @@ SIGNATURES = {
   "bt_reduce": [RT, POINTER(Program), c_int, c_int, I64, I64, I64, I64, I64, POINTER(Operand)],
   "bt_matmul": [RT, POINTER(Operand), c_int, U64, I64, I64, I64, I64, I64, POINTER(Program), POINTER(Operand)],
   "bt_attention": [RT, POINTER(AttentionArgs)],
+  "bt_attention_scratch": [POINTER(AttentionArgs), POINTER(c_uint64)],
   "bt_gather": [RT, c_int, U64, I64, I64, I64, U64, I64, U64, I64],
   "bt_put": [RT, c_int, U64, I64, I64, I64, I64, I64, U64, I64, U64, I64, I64],
 }

@@ -5,14 +5,39 @@
 namespace bt {
 
 // A thread an element, in row-major order of the result.
+constexpr int EW_V = 1;  // elements per thread
+
+// A thread takes EW_V elements of the flattened result, 256 apart, so every load and store of a wavefront is
+// contiguous along the columns. One element a thread keeps the evaluator's code small; the grid has the parallelism. The flat index fits 31 bits (the launcher checks), and the row and batch entry are
+// split off it by multiplication (FastDiv).
 template <int DT>
-__global__ void __launch_bounds__(256) elementwise_kernel(const bt_program prog, int64_t batch, int64_t rows,
-                                                          int64_t cols, const bt_operand out) {
+__global__ void __launch_bounds__(256) elementwise_kernel(const bt_program prog, uint32_t total, FastDiv cols,
+                                                          FastDiv rows, const bt_operand out) {
+  const uint32_t base = blockIdx.x * (256u * EW_V) + threadIdx.x;
+  Coords<EW_V> at;
+#pragma unroll
+  for (int v = 0; v < EW_V; v++) {
+    const uint32_t t = base + 256u * v;
+    at.ok[v] = t < total;
+    const uint32_t u = at.ok[v] ? t : 0u, q = fdiv(u, cols), bb = fdiv(q, rows);
+    at.c[v] = u - q * cols.d, at.r[v] = q - bb * rows.d, at.b[v] = bb;
+  }
+  uint32_t io[EW_V] = {};
+  run_program_v<DT, EW_V>(prog, at, io);
+#pragma unroll
+  for (int v = 0; v < EW_V; v++)
+    if (at.ok[v]) store_value<DT>(out, operand_matrix(out, at.b[v]) * out.sb + at.r[v] * out.sr + at.c[v] * out.sc, io[v]);
+}
+
+// The same for results of 2^31 elements or more: one element per thread, 64-bit index arithmetic.
+template <int DT>
+__global__ void __launch_bounds__(256) elementwise_wide_kernel(const bt_program prog, int64_t batch, int64_t rows,
+                                                               int64_t cols, const bt_operand out) {
   int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  int64_t total = batch * rows * cols;
+  const int64_t total = batch * rows * cols;
   for (; t < total; t += (int64_t)gridDim.x * blockDim.x) {
-    int64_t c = t % cols, r = t / cols % rows, b = t / cols / rows;
-    uint32_t v = run_program<DT>(prog, b, r, c, 0);
+    const int64_t c = t % cols, r = t / cols % rows, b = t / cols / rows;
+    const uint32_t v = run_program<DT>(prog, b, r, c, 0);
     store_value<DT>(out, operand_matrix(out, b) * out.sb + r * out.sr + c * out.sc, v);
   }
 }
@@ -22,12 +47,12 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+__device__ __forceinline__ float nan_max(float a, float b) {
+  return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b);
+}
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float w = __shfl_xor(v, o, 64);
-    v = (v != v || w != w) ? __builtin_nanf("") : fmaxf(v, w);
-  }
+  for (int o = 32; o > 0; o >>= 1) v = nan_max(v, __shfl_xor(v, o, 64));
   return v;
 }
 __device__ __forceinline__ int32_t wave_imax(int32_t v) {
@@ -36,35 +61,62 @@ __device__ __forceinline__ int32_t wave_imax(int32_t v) {
   return v;
 }
 
-// A wavefront an output element. Lanes stride along the reduced axis; the wave combines their partial results.
-// Sums accumulate in fp32. With DT bf16 each program value is rounded first, as the reference's pack of the folded
-// operand is; the reduced value is rounded again when it is stored.
-template <int DT>
-__global__ void __launch_bounds__(256) reduce_kernel(const bt_program prog, int kind, int axis, int64_t batch,
+constexpr int RED_V = 1;  // values a lane fetches before folding them
+
+// Sums or maxima of a program's values along one axis. WPO wavefronts share each output: a whole block of WPO waves
+// for long sweeps with few outputs, else one (four outputs a block). Lanes stride along the reduced axis; the partial
+// results are combined across the wave, then across the block's waves through LDS. Sums accumulate in fp32. With DT
+// bf16 each program value is rounded first, as the reference's pack of the folded operand is; the reduced value is
+// rounded again when it is stored.
+template <int DT, int WPO>
+__global__ void __launch_bounds__(WPO > 4 ? 64 * WPO : 256) reduce_kernel(const bt_program prog, int kind, int axis, int64_t batch,
                                                      int64_t rows, int64_t cols, int64_t sweep, int64_t step,
                                                      const bt_operand out) {
-  int lane = threadIdx.x & 63;
-  int64_t w = (int64_t)blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
-  int64_t ob = axis == 0 ? batch / sweep : batch, orows = axis == 1 ? 1 : rows, ocols = axis == 2 ? 1 : cols;
-  if (w >= ob * orows * ocols) return;
-  int64_t c = w % ocols, r = w / ocols % orows, b = w / ocols / orows;
-  int64_t n = axis == 0 ? sweep : axis == 1 ? rows : cols;
-  int64_t base = axis == 0 ? (b / step) * step * sweep + b % step : 0;
+  __shared__ uint32_t part[WPO];
+  const int lane = threadIdx.x & 63;
+  const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t w = WPO > 1 ? (int64_t)blockIdx.x : (int64_t)blockIdx.x * 4 + wib;
+  const int64_t ob = axis == 0 ? batch / sweep : batch, orows = axis == 1 ? 1 : rows, ocols = axis == 2 ? 1 : cols;
+  if (w >= ob * orows * ocols) return;  // uniform across the block when WPO > 1
+  const int64_t c = w % ocols, r = w / ocols % orows, b = w / ocols / orows;
+  const int64_t n = axis == 0 ? sweep : axis == 1 ? rows : cols;
+  const int64_t base = axis == 0 ? (b / step) * step * sweep + b % step : 0;
+  const int64_t stride = 64 * WPO;
   float facc = kind == BT_REDUCE_SUM ? 0.0f : -__builtin_inff();
   int32_t iacc = INT32_MIN;
-  for (int64_t i = lane; i < n; i += 64) {
-    int64_t bb = axis == 0 ? base + i * step : b, rr = axis == 1 ? i : r, cc = axis == 2 ? i : c;
-    uint32_t v = run_program<DT>(prog, bb, rr, cc, 0);
-    if (DT == BT_INT32) iacc = max(iacc, (int32_t)v);
-    else if (kind == BT_REDUCE_SUM) facc += __uint_as_float(v);
-    else {
-      float f = __uint_as_float(v);
-      facc = (f != f || facc != facc) ? __builtin_nanf("") : fmaxf(facc, f);
+  for (int64_t i0 = (WPO > 1 ? wib * 64 : 0) + lane; i0 < n; i0 += stride * RED_V) {
+    Coords<RED_V> at;
+#pragma unroll
+    for (int v = 0; v < RED_V; v++) {
+      const int64_t i = i0 + stride * v;
+      at.ok[v] = i < n;
+      const int64_t ii = at.ok[v] ? i : 0;
+      at.b[v] = axis == 0 ? base + ii * step : b, at.r[v] = axis == 1 ? ii : r, at.c[v] = axis == 2 ? ii : c;
+    }
+    uint32_t io[RED_V] = {};
+    run_program_v<DT, RED_V>(prog, at, io);
+#pragma unroll
+    for (int v = 0; v < RED_V; v++) {
+      if (!at.ok[v]) continue;
+      if (DT == BT_INT32) iacc = max(iacc, (int32_t)io[v]);
+      else if (kind == BT_REDUCE_SUM) facc += __uint_as_float(io[v]);
+      else facc = nan_max(facc, __uint_as_float(io[v]));
     }
   }
   uint32_t res;
   if (DT == BT_INT32) res = (uint32_t)wave_imax(iacc);
   else res = __float_as_uint(kind == BT_REDUCE_SUM ? wave_sum(facc) : wave_max(facc));
+  if (WPO > 1) {
+    if (lane == 0) part[wib] = res;
+    __syncthreads();
+    if (wib != 0) return;
+    for (int k = 1; k < WPO; k++) {
+      const uint32_t o = part[k];
+      if (DT == BT_INT32) res = (uint32_t)max((int32_t)res, (int32_t)o);
+      else if (kind == BT_REDUCE_SUM) res = __float_as_uint(__uint_as_float(res) + __uint_as_float(o));
+      else res = __float_as_uint(nan_max(__uint_as_float(res), __uint_as_float(o)));
+    }
+  }
   if (lane == 0) {
     if (DT == BT_BF16) res = __float_as_uint(round_packed(__uint_as_float(res)));
     store_value<DT>(out, operand_matrix(out, b) * out.sb + r * out.sr + c * out.sc, res);
@@ -148,12 +200,23 @@ int bt_elementwise(bt_runtime *rt, const bt_program *prog, int64_t batch, int64_
   if (int s = check_program(prog)) return s;
   if (int s = check_out(out)) return s;
   if (batch <= 0 || rows <= 0 || cols <= 0) return fail(BT_EINVAL, "elementwise shape must be positive");
-  int64_t total = batch * rows * cols;
-  unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 1 << 20);
-  if (prog->dtype == BT_BF16) elementwise_kernel<BT_BF16><<<blocks, 256, 0, r->stream>>>(*prog, batch, rows, cols, *out);
-  else if (prog->dtype == BT_FP32)
-    elementwise_kernel<BT_FP32><<<blocks, 256, 0, r->stream>>>(*prog, batch, rows, cols, *out);
-  else elementwise_kernel<BT_INT32><<<blocks, 256, 0, r->stream>>>(*prog, batch, rows, cols, *out);
+  const int64_t total = batch * rows * cols;
+  if (total < (1ll << 31)) {
+    const unsigned blocks = (unsigned)((total + 256 * EW_V - 1) / (256 * EW_V));
+    const FastDiv fc = make_fastdiv((uint32_t)cols), fr = make_fastdiv((uint32_t)rows);
+    if (prog->dtype == BT_BF16)
+      elementwise_kernel<BT_BF16><<<blocks, 256, 0, r->stream>>>(*prog, (uint32_t)total, fc, fr, *out);
+    else if (prog->dtype == BT_FP32)
+      elementwise_kernel<BT_FP32><<<blocks, 256, 0, r->stream>>>(*prog, (uint32_t)total, fc, fr, *out);
+    else elementwise_kernel<BT_INT32><<<blocks, 256, 0, r->stream>>>(*prog, (uint32_t)total, fc, fr, *out);
+  } else {
+    const unsigned blocks = 1u << 20;
+    if (prog->dtype == BT_BF16)
+      elementwise_wide_kernel<BT_BF16><<<blocks, 256, 0, r->stream>>>(*prog, batch, rows, cols, *out);
+    else if (prog->dtype == BT_FP32)
+      elementwise_wide_kernel<BT_FP32><<<blocks, 256, 0, r->stream>>>(*prog, batch, rows, cols, *out);
+    else elementwise_wide_kernel<BT_INT32><<<blocks, 256, 0, r->stream>>>(*prog, batch, rows, cols, *out);
+  }
   BT_LAUNCHED("elementwise");
   return BT_OK;
 }
@@ -174,12 +237,22 @@ int bt_reduce(bt_runtime *rt, const bt_program *prog, int kind, int axis, int64_
                                                         (long long)sweep, (long long)step, (long long)batch);
   }
   int64_t outs = (axis == 0 ? batch / sweep : batch) * (axis == 1 ? 1 : rows) * (axis == 2 ? 1 : cols);
-  unsigned blocks = (unsigned)((outs + 3) / 4);
-  if (prog->dtype == BT_BF16)
-    reduce_kernel<BT_BF16><<<blocks, 256, 0, r->stream>>>(*prog, kind, axis, batch, rows, cols, sweep, step, *out);
-  else if (prog->dtype == BT_FP32)
-    reduce_kernel<BT_FP32><<<blocks, 256, 0, r->stream>>>(*prog, kind, axis, batch, rows, cols, sweep, step, *out);
-  else reduce_kernel<BT_INT32><<<blocks, 256, 0, r->stream>>>(*prog, kind, axis, batch, rows, cols, sweep, step, *out);
+  const int64_t n = axis == 0 ? sweep : axis == 1 ? rows : cols;
+  if (outs >= (1ll << 33)) return fail(BT_EINVAL, "a reduction of %lld outputs is too large", (long long)outs);
+#define BT_REDUCE(WPO, blocks)                                                                                    \
+  do {                                                                                                          \
+    const unsigned threads = WPO > 4 ? 64 * WPO : 256;                                                          \
+    if (prog->dtype == BT_BF16)                                                                                 \
+      reduce_kernel<BT_BF16, WPO><<<blocks, threads, 0, r->stream>>>(*prog, kind, axis, batch, rows, cols, sweep, step, *out); \
+    else if (prog->dtype == BT_FP32)                                                                            \
+      reduce_kernel<BT_FP32, WPO><<<blocks, threads, 0, r->stream>>>(*prog, kind, axis, batch, rows, cols, sweep, step, *out); \
+    else reduce_kernel<BT_INT32, WPO><<<blocks, threads, 0, r->stream>>>(*prog, kind, axis, batch, rows, cols, sweep, step, *out); \
+  } while (0)
+  // with too few outputs to fill the chip, a block of waves on each output: about one value a lane
+  if (outs < 2048 && n > 512) BT_REDUCE(16, (unsigned)outs);
+  else if (outs < 2048 && n > 128) BT_REDUCE(4, (unsigned)outs);
+  else BT_REDUCE(1, (unsigned)((outs + 3) / 4));
+#undef BT_REDUCE
   BT_LAUNCHED("reduce");
   return BT_OK;
 }

@@ -165,8 +165,7 @@ __device__ __forceinline__ void store_tile(const MatmulArgs &args, const f32x4 &
   for (int i = 0; i < 4; i++) {
     const int mm = mt * 16 + 4 * g + i;
     if (mm >= args.m) break;
-    const float v = acc[i];
-    const uint32_t x = __float_as_uint(DT == BT_BF16 ? round_packed(v) : v);
+    const uint32_t x = __float_as_uint(DT == BT_BF16 ? round_packed(acc[i]) : acc[i]);
     const uint32_t y = args.prog.n_inst ? run_program<DT>(args.prog, b, mm, n, x) : x;
     store_value<DT>(args.out, obase + (int64_t)mm * args.out.sr, y);
   }

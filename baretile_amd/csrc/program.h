@@ -111,34 +111,190 @@ __device__ __forceinline__ int32_t int_op(int op, int32_t a, int32_t b) {
   }
 }
 
+// ---- evaluation of V elements at once ------------------------------------------------------------------------------
+// A program runs in two phases: every input is fetched for all V elements first, so the loads are in flight together
+// and their latencies overlap, then the instructions run over the V values each, so decoding an instruction and
+// selecting its registers (uniform scalar branches) is paid once per V elements.
+
+template <int V> struct Vals { uint32_t x[V]; };
+
+// The register file of one element: a vector, so that reading or writing register i (a uniform index from the
+// instruction) is a register-relative move (v_movrels / v_movreld) rather than an access to scratch memory.
+typedef uint32_t regfile __attribute__((ext_vector_type(BT_MAX_REGS)));
+typedef uint32_t prefile __attribute__((ext_vector_type(BT_MAX_INPUTS)));
+
+template <int V>
+__device__ __forceinline__ Vals<V> regs_get(const regfile (&r)[V], int i) {
+  Vals<V> o;
+#pragma unroll
+  for (int v = 0; v < V; v++) o.x[v] = r[v][i];
+  return o;
+}
+
+template <int V>
+__device__ __forceinline__ void regs_set(regfile (&r)[V], int i, const Vals<V> &x) {
+#pragma unroll
+  for (int v = 0; v < V; v++) r[v][i] = x.x[v];
+}
+
+template <int V>
+__device__ __forceinline__ Vals<V> pre_get(const prefile (&p)[V], int i) {
+  Vals<V> o;
+#pragma unroll
+  for (int v = 0; v < V; v++) o.x[v] = p[v][i];
+  return o;
+}
+
+// Where each of V elements sits in the result: batch entry, row, column, and whether it exists.
+template <int V> struct Coords {
+  int64_t b[V], r[V], c[V];
+  bool ok[V];
+};
+
+// Every input of prog at the V elements; 0 where an element does not exist.
+template <int DT, int V>
+__device__ __forceinline__ void fetch_inputs(const bt_program &prog, const Coords<V> &at, prefile (&pre)[V]) {
+#pragma unroll
+  for (int k = 0; k < BT_MAX_INPUTS; k++) {
+#pragma unroll
+    for (int v = 0; v < V; v++)
+      pre[v][k] = k < prog.n_inputs && at.ok[v] ? load_operand<DT>(prog.in[k], at.b[v], at.r[v], at.c[v]) : 0u;
+  }
+}
+
+// The transcendental and other long operations, kept out of line: each expands to dozens of instructions, and inlined
+// into every op's branch they would make the evaluator larger than the instruction cache.
+__device__ __attribute__((noinline)) float long_op(int op, float a) {
+  switch (op) {
+    case BT_OP_EXP: return expf(a);
+    case BT_OP_EXP2: return exp2f(a);
+    case BT_OP_LOG: return logf(a);
+    case BT_OP_LOG2: return log2f(a);
+    case BT_OP_SQRT: return sqrtf(a);
+    case BT_OP_RECIP: return 1.0f / a;
+    case BT_OP_RSQRT: return 1.0f / sqrtf(a);
+    case BT_OP_SIN: return sinf(a);
+    case BT_OP_COS: return cosf(a);
+    case BT_OP_SIGMOID: return 1.0f / (1.0f + expf(-a));
+    case BT_OP_SILU: return a / (1.0f + expf(-a));
+    case BT_OP_GELU: return gelu_tanh(a);
+    case BT_OP_TANH: return tanhf(a);
+    default: return a;
+  }
+}
+
+// One instruction over V values. op is uniform, so the switch is a scalar branch around straight vector code.
+template <int DT, int V>
+__device__ __forceinline__ Vals<V> apply_op(int op, const Vals<V> &a, const Vals<V> &b) {
+  Vals<V> o;
+  if (DT == BT_INT32) {
+#pragma unroll
+    for (int v = 0; v < V; v++) o.x[v] = (uint32_t)int_op(op, (int32_t)a.x[v], (int32_t)b.x[v]);
+    return o;
+  }
+  float f[V], x[V], y[V];
+#pragma unroll
+  for (int v = 0; v < V; v++) { x[v] = __uint_as_float(a.x[v]); y[v] = __uint_as_float(b.x[v]); }
+#define BT_OP(code, expr)                              \
+  case code:                                           \
+    _Pragma("unroll") for (int v = 0; v < V; v++) {    \
+      const float A = x[v], B = y[v];                  \
+      (void)B;                                         \
+      f[v] = (expr);                                   \
+    }                                                  \
+    break;
+  switch (op) {
+    BT_OP(BT_OP_ADD, A + B)
+    BT_OP(BT_OP_SUB, A - B)
+    BT_OP(BT_OP_MUL, A * B)
+    BT_OP(BT_OP_DIV, A / B)
+    BT_OP(BT_OP_MAX, (A != A || B != B) ? __builtin_nanf("") : fmaxf(A, B))
+    BT_OP(BT_OP_MIN, (A != A || B != B) ? __builtin_nanf("") : fminf(A, B))
+    BT_OP(BT_OP_CMPLT, A < B ? 1.0f : 0.0f)
+    BT_OP(BT_OP_CMPLE, A <= B ? 1.0f : 0.0f)
+    BT_OP(BT_OP_CMPNE, A != B ? 1.0f : 0.0f)
+    BT_OP(BT_OP_CMPEQ, A == B ? 1.0f : 0.0f)
+    BT_OP(BT_OP_NEG, -A)
+    BT_OP(BT_OP_RELU, A > 0.0f ? A : 0.0f)
+    BT_OP(BT_OP_FTOB, round_packed(A))
+    default:
+#pragma unroll
+      for (int v = 0; v < V; v++) f[v] = long_op(op, x[v]);
+  }
+#undef BT_OP
+#pragma unroll
+  for (int v = 0; v < V; v++) o.x[v] = __float_as_uint(DT == BT_BF16 ? round_packed(f[v]) : f[v]);
+  return o;
+}
+
+// Runs prog on V elements whose inputs are in pre. io holds the incoming value (register 0: a matmul epilogue's
+// result) and receives the result register's bits.
+template <int DT, int V>
+__device__ __forceinline__ void eval_program(const bt_program &prog, const prefile (&pre)[V], uint32_t (&io)[V]) {
+  regfile regs[V];
+#pragma unroll
+  for (int v = 0; v < V; v++) {
+    regs[v] = (regfile)(0u);
+    regs[v][0] = io[v];
+  }
+  for (int i = 0; i < prog.n_inst; i++) {
+    const bt_inst in = prog.inst[i];
+    Vals<V> o;
+    if (in.op == BT_OP_LOAD) o = pre_get<V>(pre, in.a);
+    else if (in.op == BT_OP_CONST) {
+#pragma unroll
+      for (int v = 0; v < V; v++) o.x[v] = in.imm;
+    } else if (in.op == BT_OP_MOV) o = regs_get<V>(regs, in.a);
+    else if (in.op == BT_OP_WHERE) {
+      const Vals<V> cnd = regs_get<V>(regs, in.a), t = regs_get<V>(regs, in.b), e = regs_get<V>(regs, in.c);
+#pragma unroll
+      for (int v = 0; v < V; v++) {
+        const bool on = DT == BT_INT32 ? cnd.x[v] != 0 : __uint_as_float(cnd.x[v]) != 0.0f;
+        o.x[v] = on ? t.x[v] : e.x[v];
+      }
+    } else {
+      o = apply_op<DT, V>(in.op, regs_get<V>(regs, in.a), regs_get<V>(regs, in.b));
+    }
+    regs_set<V>(regs, in.dst, o);
+  }
+  const Vals<V> res = regs_get<V>(regs, prog.result);
+#pragma unroll
+  for (int v = 0; v < V; v++) io[v] = res.x[v];
+}
+
+// Runs prog at V elements: fetch, then evaluate. io as for eval_program.
+template <int DT, int V>
+__device__ __forceinline__ void run_program_v(const bt_program &prog, const Coords<V> &at, uint32_t (&io)[V]) {
+  prefile pre[V];
+  fetch_inputs<DT, V>(prog, at, pre);
+  eval_program<DT, V>(prog, pre, io);
+}
+
 // Runs prog at element (b, r, c). acc, if the program reads register 0 as a preloaded value (a matmul epilogue), is
 // placed there first. Returns the result register's bits.
 template <int DT>
 __device__ __forceinline__ uint32_t run_program(const bt_program &prog, int64_t b, int64_t r, int64_t c,
                                                 uint32_t acc) {
-  uint32_t regs[BT_MAX_REGS];
-#pragma unroll
-  for (int i = 0; i < BT_MAX_REGS; i++) regs[i] = 0;
-  regs[0] = acc;
-  for (int i = 0; i < prog.n_inst; i++) {
-    const bt_inst in = prog.inst[i];
-    uint32_t v;
-    if (in.op == BT_OP_LOAD) v = load_operand<DT>(prog.in[in.a], b, r, c);
-    else if (in.op == BT_OP_CONST) v = in.imm;
-    else if (in.op == BT_OP_MOV) v = reg_get(regs, in.a);
-    else if (in.op == BT_OP_WHERE) {
-      uint32_t cnd = reg_get(regs, in.a);
-      bool on = DT == BT_INT32 ? cnd != 0 : __uint_as_float(cnd) != 0.0f;
-      v = on ? reg_get(regs, in.b) : reg_get(regs, in.c);
-    } else if (DT == BT_INT32) {
-      v = (uint32_t)int_op(in.op, (int32_t)reg_get(regs, in.a), (int32_t)reg_get(regs, in.b));
-    } else {
-      float x = float_op(in.op, __uint_as_float(reg_get(regs, in.a)), __uint_as_float(reg_get(regs, in.b)), 0.0f);
-      v = __float_as_uint(DT == BT_BF16 ? round_packed(x) : x);
-    }
-    reg_set(regs, in.dst, v);
-  }
-  return reg_get(regs, prog.result);
+  Coords<1> at;
+  at.b[0] = b, at.r[0] = r, at.c[0] = c, at.ok[0] = true;
+  uint32_t io[1] = {acc};
+  run_program_v<DT, 1>(prog, at, io);
+  return io[0];
+}
+
+// n / d for 32-bit n, with a multiplier and shift the host computed for d (the round-up method of Granlund and
+// Montgomery, "Division by invariant integers using multiplication", 1994): q = (umulhi(n, m) + n) >> s.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv &f) {
+  return (uint32_t)(((uint64_t)__umulhi(n, f.m) + n) >> f.s);
+}
+inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t s = 0;
+  while ((1ull << s) < d) s++;
+  const uint64_t m = ((1ull << 32) * ((1ull << s) - d)) / d + 1;
+  return FastDiv{d, (uint32_t)m, s};
 }
 
 // Stores a result computed in DT as out's dtype at element offset `at`.

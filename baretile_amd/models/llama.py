@@ -199,19 +199,23 @@ def argmax(logits):
   return int(np.argmax(np.frombuffer(logits.tobytes(), np.float32)))
 
 
-def generate(w, c, prompt, steps, size, feed=None):
+def generate(w, c, prompt, steps, size, feed=None, clock=None, replay=True):
   """Greedy decode: prefill the prompt, then `steps` tokens, each step one replay of the recorded forward (jit).
   With feed, step i is fed feed[i] instead of its own pick (the reference's NumPy-fed protocol, gpt2.py:147-161).
+  With clock (a list), the time.perf_counter() at which each pick is known is appended to it. replay=False runs every
+  step eagerly, one launch per kernel, as the first call of a jit does.
   Returns (picks, per-step logits as float32 arrays)."""
+  import time
   rt = w["norm"].rt
   caches = kv_cache(rt, c, size)
   logits = prefill(prompt, w, c, caches, len(prompt))
-  step = jit(lambda i, p: forward(i, p, w, c, caches))
+  step = (jit if replay else lambda f: f)(lambda i, p: forward(i, p, w, c, caches))
   picks, outs = [], []
   for s in range(steps):
     row = np.frombuffer(logits.tobytes(), np.float32).copy()
     outs.append(row)
     picks.append(int(np.argmax(row)))
+    if clock is not None: clock.append(time.perf_counter())
     if s + 1 == steps: break
     tok = picks[-1] if feed is None else feed[s]
     logits = step(Tensor.of(rt, [[tok]], "int32"), Tensor.of(rt, [[len(prompt) + s]], "int32"))

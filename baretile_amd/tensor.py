@@ -670,8 +670,15 @@ class Tensor:
     out.lead = self.lead
     args = _lib.AttentionArgs(q.addr, k.addr, v.addr, out.addr, places.addr, q.sb, q.sr, k.sb, k.sr, v.sb, v.sr,
                               out.sb, out.sr, q.rows if places.batch > 1 else 0, q.batch, rep, q.rows, k.rows, q.cols,
-                              window)
+                              window, parts or 0, 0, 0, 0)
+    need = ctypes.c_uint64()
+    _lib.call("attention_scratch", ctypes.byref(args), ctypes.byref(need))
+    scratch = None
+    if need.value:  # the parts' partial sums, freed (stream-ordered) once the launches that use them are queued
+      scratch = Storage(self.rt, need.value)
+      args.scratch, args.scratch_bytes = scratch.addr, need.value
     self.rt.run("attention", "attention", ctypes.byref(args))
+    del scratch
     return out
 
   def gather(self, ids):

@@ -144,6 +144,69 @@ def cpu_leg(fmt, rows, seconds=10.0):
   return per * 1e6, n
 
 
+def decode_leg(tokens=128, prompt_len=32, check=True, replay=True):
+  """greedy decode of a SmolLM-135M-shaped Llama (30 layers, 576 wide, 9/3 heads of 64, FFN 1536,
+  vocab 49152) with random weights (linears N(0, 0.02), norms N(1, 0.1), embedding N(0, 1), seed 0), bfp8 linears
+  and tied output layer, bf16 norms, embedding and KV cache, a 32-token uniform prompt and 128 new tokens.
+
+  The device runs the stream twice: autonomously (its own picks fed back; timed) and NumPy-fed (the oracle's picks fed,
+  gpt2.py:147-161). The oracle (oracle/llama_ref.py) runs the same decode on the host; its per-token time is the CPU
+  baseline. Returns a dict of tok/s, token identity and per-step logit error against the oracle."""
+  from oracle import llama_ref as L
+  from baretile_amd.models import llama
+  from baretile_amd.runtime import Runtime
+  from baretile_amd.tensor import Tensor
+  size = prompt_len + tokens
+  t0 = time.perf_counter()
+  c, w = L.smol(np.random.default_rng(0), 30, vocab=49152, places=size)
+  prompt = [int(i) for i in np.random.default_rng(1).integers(0, 49152, prompt_len)]
+  log("decode: weights made in", round(time.perf_counter() - t0, 1), "s")
+  rt = Runtime()
+  try:
+    dc = llama.model(dim=576, heads=9, kv=3, layers=30, eps=1e-5, theta=10000.0, vocab=49152, ffn=1536,
+                     precision=llama.precision(llama.model(layers=30, dim=576), "bfp8"))
+    host = {k: v for k, v in w.items() if k not in ("cos", "sin", "turn", "embed.T")}
+    dw = llama.upload(rt, host, dc, places=size)
+    rt.wait()
+    llama.generate(dw, dc, prompt, 4, size, replay=replay)  # loads the code objects
+    clock = []
+    start = time.perf_counter()
+    toks, logits = llama.generate(dw, dc, prompt, tokens, size, clock=clock, replay=replay)
+    first = clock[0] - start  # prefill of the prompt and the first pick
+    steady = (clock[-1] - clock[2]) / (len(clock) - 3)  # replays of the recorded step (the 2nd step records)
+    out = {"tok/s": round((len(clock) - 1) / (clock[-1] - clock[0]), 1), "steady_tok/s": round(1 / steady, 1),
+           "ms_per_token": round(1000 * (clock[-1] - clock[0]) / (len(clock) - 1), 4),
+           "prefill_ms": round(1000 * first, 3), "tokens": tokens, "prompt": prompt_len, "graph_replay": replay,
+           "kernels_per_token": None}
+    caches = llama.kv_cache(rt, dc, size)
+    ids, places = Tensor.of(rt, [[prompt[0]]], "int32"), Tensor.of(rt, [[0]], "int32")
+    base = rt.launches
+    llama.forward(ids, places, dw, dc, caches).realize()
+    out["kernels_per_token"] = rt.launches - base  # launches of one eager decode step: what a replay holds
+    del caches
+    if not check: return out, None
+    t0 = time.perf_counter()
+    ref = L.arrays(w, L.precision(c, "bfp8"))
+    log("decode: oracle weights in", round(time.perf_counter() - t0, 1), "s")
+    t0 = time.perf_counter()
+    rtoks, rlogits = L.greedy(prompt, tokens, ref, c, size)
+    cpu_s = time.perf_counter() - t0
+    fed, flogits = llama.generate(dw, dc, prompt, tokens, size, feed=rtoks)
+    errs = [float(np.abs(g - r).max() / np.abs(r).max()) for g, r in zip(flogits, rlogits)]
+    margins = [float(np.diff(np.sort(r)[-2:])[0]) for r in rlogits]
+    same = next((i for i, (a, b) in enumerate(zip(toks, rtoks)) if a != b), len(toks))
+    out.update({"tokens_identical": toks == rtoks, "identical_prefix": same,
+                "numpy_fed_agreement": float(np.mean([a == b for a, b in zip(fed, rtoks)])),
+                "max_rel_logit_err": round(max(errs), 5), "min_top2_margin": round(min(margins), 4)})
+    cpu = {"value": round(tokens / cpu_s, 2), "unit": "tok/s", "cores": blas_threads()[0], "kind": "port",
+           "sample": f"the oracle's autonomous greedy decode of the same model: {prompt_len}-token prefill then "
+           f"{tokens} tokens, {cpu_s:.1f} s in all, NumPy float32 ({blas_threads()[1]} BLAS), bfp8 weights "
+           "dequantized beforehand"}
+    return out, cpu
+  finally:
+    rt.close()
+
+
 def blas_threads():
   try:
     from threadpoolctl import threadpool_info
@@ -161,7 +224,9 @@ def main():
   ap.add_argument("--warmup", type=int, default=400)
   ap.add_argument("--cpu-seconds", type=float, default=10.0)
   ap.add_argument("--no-cpu", action="store_true")
-  ap.add_argument("--only", default=None, help="time one configuration, e.g. bfp4_B1 (for profiling runs)")
+  ap.add_argument("--only", default=None, help="time one configuration, e.g. bfp4_B1 or decode (for profiling runs)")
+  ap.add_argument("--no-decode", action="store_true", help="skip the SmolLM decode (BASELINE config 3)")
+  ap.add_argument("--eager", action="store_true", help="decode without graph replay (for kernel-trace profiles)")
   args = ap.parse_args()
   if args.gpus != 1:
     print(f"bench.py runs on one GPU: this build has no multi-GPU path, and --gpus {args.gpus} is not supported",
@@ -182,6 +247,13 @@ def main():
                                    "stream_read_us": round(read_us, 3), "stream_read_GB/s": round(wb / read_us / 1e3, 1),
                                    "frac_of_stream_read": round(read_us / us, 4)}
       log(fmt, rows, configs[f"{fmt}_B{rows}"])
+  decode, decode_cpu = None, None
+  if not args.no_decode and args.only in (None, "decode"):
+    decode, decode_cpu = decode_leg(check=not args.no_cpu, replay=not args.eager)
+    log("decode", decode)
+    if args.only == "decode":
+      print(json.dumps({"decode": decode, "decode_cpu_baseline": decode_cpu}), flush=True)
+      return
   head = configs.get("bfp4_B1") or next(iter(configs.values()))
   cpu = None
   if not args.no_cpu:
@@ -201,6 +273,7 @@ def main():
                  "frac": head["frac_hbm_peak"], "traffic": measured_traffic()},
     "cpu_baseline": cpu,
     "configs": configs,
+    "decode": decode, "decode_cpu_baseline": decode_cpu,
   }
   print(json.dumps(line), flush=True)
 

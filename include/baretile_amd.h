@@ -178,15 +178,24 @@ int bt_matmul(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_t b, int64_
  * tensor.py:797-841) -------------------------------------------------------------------------------------------
  *
  * out[e, r, :] = softmax(q[e, r, :] . k[e / rep, j, :] + mask) @ v[e / rep, j, :] over keys j < keys, where the mask
- * hides j > places[r] and, with window > 0, j <= places[r] - window. Scores, maxima and sums are fp32; out is bf16.
+ * hides j > places[r] and, with window > 0, j <= places[r] - window. Scores, maxima and sums are fp32, p is packed to
+ * bf16 before it is summed and multiplied by v (as the reference packs it, kernels.py:815-823); out is bf16.
  * q, k, v, out are bf16 with element strides (head, row); places is int32 with a head stride of 0 or rows. No scale
- * is applied: baretile's RoPE pre-scales q (llama.py:210-216). */
+ * is applied: baretile's RoPE pre-scales q (llama.py:210-216).
+ *
+ * parts splits a decode step's keys (at most 16 query rows per key head: rep * rows <= 16) between that many blocks,
+ * as attention_kernel's parts does; 0 picks a count from the shape. With more than one part the blocks write fp32
+ * partial sums into scratch (bt_attention_scratch gives the bytes; 16-byte aligned) and a second launch combines
+ * them. Calls that share one scratch buffer must not overlap. */
 typedef struct {
   uint64_t q, k, v, out, places;
   int64_t q_sh, q_sr, k_sh, k_sr, v_sh, v_sr, o_sh, o_sr, places_sh;
-  int32_t heads, rep, rows, keys, head_dim, window;
+  int32_t heads, rep, rows, keys, head_dim, window, parts, pad_;
+  uint64_t scratch, scratch_bytes;
 } bt_attention_args;
 int bt_attention(bt_runtime *rt, const bt_attention_args *args);
+/* The scratch bytes bt_attention needs for args (0 when it runs in one part). */
+int bt_attention_scratch(const bt_attention_args *args, uint64_t *bytes);
 
 /* ---- rows in and out of a cache: replaces gather_kernel (kernels.py:1007-1049) and put_kernel
  * (kernels.py:1083-1168) ------------------------------------------------------------------------------------------ */

@@ -71,7 +71,7 @@ def bfp_fields(a, dtype="bfp8"):
   if dtype not in FORMATS: raise ValueError(f"unknown block-float format {dtype}")
   a = np.asarray(a)
   if a.shape[-1] % RUN: raise ValueError("the last axis must be a multiple of 16")
-  bits = bf16_bits(a).astype(np.int64)
+  bits = bf16_bits(a).astype(np.int32)
   s, e = bits >> 15 & 1, bits >> 7 & 255
   m = (bits & 127) | np.where(e != 0, 128, 0)
   top = _runs(e).max(-1, keepdims=True)
@@ -86,11 +86,10 @@ def bfp(a, dtype="bfp8"):
   """The values a block-float cast gives, as float64 (gpt2.py:19-30). A negative value that rounds to zero gives -0.0."""
   if dtype not in FORMATS: raise ValueError(f"unknown block-float format {dtype}")
   a = np.asarray(a)
-  bits = bf16_bits(a).astype(np.int64)
-  s = bits >> 15 & 1
+  s = bf16_bits(a) >> 15 & 1
   top, q = bfp_fields(a, dtype)
   scale = 2.0 ** (top.astype(np.int64) - (133 if dtype == "bfp8" else 129))
-  mag = np.abs(q.astype(np.int64))
+  mag = np.abs(q.astype(np.int32))
   vals = np.where(_runs(s) == 1, -1.0, 1.0) * _runs(mag) * scale[..., None]
   return vals.reshape(a.shape)
 

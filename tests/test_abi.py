@@ -41,8 +41,27 @@ def test_errors_map_to_exceptions():
   with pytest.raises(ValueError, match="no runtime"): _lib.call("alloc", None, 16, ctypes.byref(ctypes.c_uint64()))
 
 
-def test_struct_sizes_match_the_header():
+def test_struct_sizes_match_the_header(tmp_path):
+  # the ctypes mirrors against what a C compiler makes of include/baretile_amd.h: sizes and every field's offset
+  import shutil, subprocess
   from baretile_amd import _lib
-  assert ctypes.sizeof(_lib.Operand) == 48 and ctypes.sizeof(_lib.Inst) == 12
-  assert ctypes.sizeof(_lib.Program) == 16 + 12 * _lib.MAX_INST + 48 * _lib.MAX_INPUTS
-  assert ctypes.sizeof(_lib.AttentionArgs) == 5 * 8 + 9 * 8 + 6 * 4
+  cc = shutil.which("gcc") or shutil.which("cc")
+  if cc is None: pytest.skip("no C compiler")
+  structs = {"bt_operand": _lib.Operand, "bt_inst": _lib.Inst, "bt_program": _lib.Program,
+             "bt_attention_args": _lib.AttentionArgs}
+  cname = {("bt_program", "inputs"): "in"}  # Python can't name a field `in`
+  lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "baretile_amd.h"', "int main(void) {"]
+  for name, cls in structs.items():
+    lines.append(f'  printf("{name} %zu\\n", sizeof({name}));')
+    for field, *_ in cls._fields_:
+      lines.append(f'  printf("{name}.{field} %zu\\n", offsetof({name}, {cname.get((name, field), field)}));')
+  lines.append("  return 0; }")
+  src = tmp_path / "sizes.c"
+  src.write_text("\n".join(lines) + "\n")
+  exe = tmp_path / "sizes"
+  subprocess.run([cc, "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+  got = dict(l.split() for l in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines())
+  for name, cls in structs.items():
+    assert int(got[name]) == ctypes.sizeof(cls), name
+    for field, *_ in cls._fields_:
+      assert int(got[f"{name}.{field}"]) == getattr(cls, field).offset, (name, field)

@@ -287,7 +287,7 @@ def test_reductions(rt):
 
 # ---- attention --------------------------------------------------------------------------------------------------
 
-def attend(rt, q, k, v, places, window=0):
+def attend(rt, q, k, v, places, window=0, parts=0):
   """q (E, rows, hd), k/v (E/rep, keys, hd), places (1|E, rows) -> bf16 result as float32."""
   E, rows, hd = q.shape
   kvh, keys, _ = k.shape
@@ -295,21 +295,50 @@ def attend(rt, q, k, v, places, window=0):
   dp = up(rt, np.asarray(places, np.int32))
   o = rt.dram_alloc(E * rows * hd * 2)
   args = _lib.AttentionArgs(dq, dk, dv, o, dp, rows * hd, hd, keys * hd, hd, keys * hd, hd, rows * hd, hd,
-                            rows if np.asarray(places).shape[0] > 1 else 0, E, E // kvh, rows, keys, hd, window)
+                            rows if np.asarray(places).shape[0] > 1 else 0, E, E // kvh, rows, keys, hd, window, parts,
+                            0, 0, 0)
+  need = ctypes.c_uint64()
+  _lib.call("attention_scratch", ctypes.byref(args), ctypes.byref(need))
+  if need.value:
+    args.scratch, args.scratch_bytes = rt.dram_alloc(need.value), need.value
   rt.run("attention", "attention", ctypes.byref(args))
   return bits_to_float(down(rt, o, (E, rows, hd), np.uint16))
 
 
-def test_attention_matches_oracle(rt):
-  rng = np.random.default_rng(43)
-  for e, rows, hd, keys, rep, window in ((4, 8, 64, 96, 2, 0), (2, 40, 128, 200, 1, 50), (8, 1, 128, 512, 4, 0),
-                                         (32, 1, 128, 4096, 4, 0), (9, 32, 64, 160, 3, 0)):
-    q, k, v = (B.bf16(rng.normal(0, 1, s)) for s in ((e, rows, hd), (e // rep, keys, hd), (e // rep, keys, hd)))
-    q = B.bf16(q / np.sqrt(hd))
+# (heads, rows, head width, keys, heads per key head, window, parts): decode tiles (rep * rows <= 16) in one part and
+# split into parts, prefill tiles, windows, and BASELINE config 4's decode shape
+ATTENTION_CASES = [(4, 8, 64, 96, 2, 0, 0), (2, 40, 128, 200, 1, 50, 0), (8, 1, 128, 512, 4, 0, 0),
+                   (32, 1, 128, 4096, 4, 0, 0), (9, 32, 64, 160, 3, 0, 0), (9, 1, 64, 160, 3, 0, 0),
+                   (8, 1, 128, 1000, 4, 0, 7), (8, 2, 64, 700, 4, 100, 0), (8, 256, 128, 300, 4, 0, 0),
+                   (6, 130, 64, 130, 3, 17, 0), (32, 1, 128, 16384, 4, 0, 0)]
+
+
+@pytest.mark.parametrize("case", ATTENTION_CASES, ids=lambda c: "e{}r{}d{}k{}rep{}w{}p{}".format(*c))
+def test_attention_matches_oracle(rt, case):
+  e, rows, hd, keys, rep, window, parts = case
+  rng = np.random.default_rng(43 + sum(case))
+  q, k, v = (B.bf16(rng.normal(0, 1, s)) for s in ((e, rows, hd), (e // rep, keys, hd), (e // rep, keys, hd)))
+  q = B.bf16(q / np.sqrt(hd))
+  if rows == keys:  # causal prefill from position 0
+    places = np.broadcast_to(np.arange(rows), (e, rows))
+  else:
     places = rng.integers(max(0, keys - rows - 60), keys, (e, rows))
-    got = attend(rt, q, k, v, places, window)
-    want = ops.attention(q, k, v, places[..., None], window, rep)
-    assert np.allclose(got, want, rtol=0.011, atol=0.011), (e, rows, hd, keys, np.abs(got - want).max())
+  got = attend(rt, q, k, v, places, window, parts)
+  want = ops.attention(q, k, v, places[..., None], window, rep)
+  assert np.allclose(got, want, rtol=0.011, atol=0.011), (case, np.abs(got - want).max())
+
+
+def test_attention_rows_without_keys_are_zero(rt):
+  # a place before the first key hides every key: p is zero and so is the output (kernels.py:823-826)
+  rng = np.random.default_rng(5)
+  for rows, keys in ((1, 200), (40, 64)):
+    q, k, v = (B.bf16(rng.normal(0, 1, s)) for s in ((4, rows, 64), (2, keys, 64), (2, keys, 64)))
+    places = rng.integers(0, keys, (4, rows))
+    places[1] = -1
+    got = attend(rt, q, k, v, places)
+    assert np.array_equal(got[1], np.zeros_like(got[1]))
+    want = ops.attention(q, k, v, places[..., None], 0, 2)
+    assert np.allclose(got[[0, 2, 3]], want[[0, 2, 3]], rtol=0.011, atol=0.011)
 
 
 def test_attention_extremes(rt):
