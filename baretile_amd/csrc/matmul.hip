@@ -155,7 +155,7 @@ __device__ __forceinline__ void load_b(Chunk &r, const uint8_t *t, int lane) {
 constexpr int GROUP_A = 12, GROUP_B = 8;  // chunks requested together (A-side, B-side)
 
 // The epilogue of both kernels: lane holds rows 4g .. 4g+3 of the 16 x 16 tile at (mt, run), column col.
-template <int DT>
+template <int DT, bool INL = false>
 __device__ __forceinline__ void store_tile(const MatmulArgs &args, const f32x4 &acc, int b, int mt, int run, int g,
                                            int col) {
   const int n = run * 16 + col;
@@ -166,7 +166,7 @@ __device__ __forceinline__ void store_tile(const MatmulArgs &args, const f32x4 &
     const int mm = mt * 16 + 4 * g + i;
     if (mm >= args.m) break;
     const uint32_t x = __float_as_uint(DT == BT_BF16 ? round_packed(acc[i]) : acc[i]);
-    const uint32_t y = args.prog.n_inst ? run_program<DT>(args.prog, b, mm, n, x) : x;
+    const uint32_t y = args.prog.n_inst ? run_program<DT, INL>(args.prog, b, mm, n, x) : x;
     store_value<DT>(args.out, obase + (int64_t)mm * args.out.sr, y);
   }
 }
@@ -336,6 +336,369 @@ __global__ void __launch_bounds__(256) skinny_kernel(const MatmulArgs args) {
   store_tile<DT>(args, acc, p.b, p.mt, p.run, g, col);
 }
 
+// The end of both GEMM kernels: the block's BM x BN starting values are in LDS (row stride ES bytes, ESZ bytes each:
+// bf16-rounded for a bf16 epilogue, fp32 otherwise). Without a program, and with rows of the output contiguous and
+// 16-byte aligned, each lane copies 16 bytes at a time; otherwise each value goes through the program and is stored.
+template <int DT, int BM, int BN, int ES, int ESZ>
+__device__ __forceinline__ void gemm_epilogue(const MatmulArgs &args, const uint8_t *lds, int b, int m0, int n0,
+                                              int tid) {
+  const int rows = min(BM, args.m - m0), cols = min(BN, args.n - n0);
+  const int64_t obase = operand_matrix(args.out, b) * args.out.sb;
+  const int osz = args.out.dtype == BT_BF16 ? 2 : 4;
+  const bool same = (DT == BT_FP32 && args.out.dtype == BT_FP32) || (DT == BT_BF16 && args.out.dtype == BT_BF16);
+  const bool direct = args.prog.n_inst == 0 && same && args.out.sc == 1 && cols == BN &&
+                      (args.out.ptr + (uint64_t)(obase + (int64_t)m0 * args.out.sr + n0) * osz) % 16 == 0 &&
+                      (args.out.sr * osz) % 16 == 0;
+  if (direct) {
+    constexpr int PER_ROW = BN * ESZ / 16;  // 16-byte pieces of a row
+    uint8_t *out = (uint8_t *)args.out.ptr + (obase + (int64_t)m0 * args.out.sr + n0) * osz;
+#pragma unroll 1
+    for (int e = tid; e < rows * PER_ROW; e += 256) {
+      const int r = e / PER_ROW, piece = e % PER_ROW;
+      *(uint4 *)(out + (int64_t)r * args.out.sr * osz + piece * 16) = *(const uint4 *)(lds + r * ES + piece * 16);
+    }
+    return;
+  }
+#pragma unroll 1
+  for (int e = tid; e < rows * BN; e += 256) {
+    const int r = e / BN, c = e % BN;
+    if (c >= cols) continue;
+    const uint8_t *at = lds + r * ES + c * ESZ;
+    const uint32_t x = DT == BT_FP32 ? *(const uint32_t *)at : (uint32_t)*(const uint16_t *)at << 16;
+    const uint32_t y = args.prog.n_inst ? run_program<DT, true>(args.prog, b, m0 + r, n0 + c, x) : x;
+    store_value<DT>(args.out, obase + (int64_t)(m0 + r) * args.out.sr + (int64_t)(n0 + c) * args.out.sc, y);
+  }
+}
+
+// ---- the prefill GEMM ----------------------------------------------------------------------------------------------
+// Blocks of BM x BN outputs with 4 waves in 2 x 2, each wave WM x WN tiles of 16 x 16, stepping K by one 64-row chunk.
+// Per chunk the block stages A's BM x 64 rows (bf16, row-major, rows padded to 72 halfwords so the fragment reads hit
+// distinct banks) and B's BN / 16 tiles in LDS. B is turned into bf16 once, by the block, as it is staged: q * 2^d per
+// value, exact, laid out per tile as [k half][lane][8 values], the matrix instruction's operand order, so each wave
+// reads its fragments with one 16-byte load per lane. Two stages: the global loads of the next chunk are in flight in
+// registers while the current one is multiplied, and one barrier a chunk keeps the stages apart.
+// At the end the accumulators go through LDS once more, as the values the epilogue starts from (bf16-rounded for a
+// bf16 epilogue, fp32 otherwise), so that the epilogue runs as one loop over the block in row order: its program is
+// evaluated by code that appears once, and its stores are whole rows.
+template <int WM, int WN, int DT> struct Gemm {
+  static constexpr int BM = 32 * WM, BN = 32 * WN, AS = 72;
+  static constexpr int A_BYTES = BM * AS * 2, B_BYTES = BN / 16 * 2048, STAGE = A_BYTES + B_BYTES;
+  static constexpr int APT = BM * 8 / 256;       // 16-byte pieces of A a thread stages per chunk
+  static constexpr int BPT = BN / 16 * 64 / 256;  // tile lanes of B a thread stages per chunk
+  static constexpr int ESZ = DT == BT_FP32 ? 4 : 2, ES = BN * ESZ + 16;  // epilogue value size, row stride (bytes)
+  static constexpr int LDS = 2 * STAGE > BM * ES ? 2 * STAGE : BM * ES;
+};
+
+template <int FMT, int DT, int WM, int WN>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gemm_kernel(const MatmulArgs args, int mblocks, int nblocks) {
+  using G = Gemm<WM, WN, DT>;
+  constexpr int TB = Tile<FMT>::bytes;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[G::LDS];
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, col = lane & 15;
+  const int wib = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wib >> 1, wn = wib & 1;
+  // Blocks are dealt to the 8 XCDs in turn: renumber them so each XCD's blocks are consecutive, then walk those in
+  // groups of 8 block rows, so the blocks sharing an L2 also share rows of A and columns of B.
+  const int per = mblocks * nblocks, total = per * args.batch, full = total / 8 * 8;
+  int pid = blockIdx.x;
+  if (pid < full) pid = (pid % 8) * (full / 8) + pid / 8;
+  const int b = pid / per;
+  pid %= per;
+  constexpr int GROUP = 8;
+  const int width = GROUP * nblocks, first = pid / width * GROUP, gsz = min(mblocks - first, GROUP);
+  const int bm = first + pid % width % gsz, bn = pid % width / gsz;
+  const int m0 = bm * G::BM, n0 = bn * G::BN;
+
+  const uint16_t *abase = (const uint16_t *)args.a.ptr + operand_matrix(args.a, b) * args.a.sb;
+  const __amdgpu_buffer_rsrc_t ar = buffer(abase, (uint32_t)(((int64_t)(args.m - 1) * args.a.sr + args.k) * 2));
+  const uint8_t *bbase = args.b + (args.b_matrix_bytes ? b * args.b_matrix_bytes : 0);
+
+  uint4 areg[G::APT], bq0[G::BPT], bq1[G::BPT], bex[G::BPT];
+  auto fetch = [&](int c) {
+    const int k0 = c * 64;
+#pragma unroll
+    for (int i = 0; i < G::APT; i++) {
+      const int piece = tid + 256 * i, row = piece >> 3, kc = (piece & 7) * 8;
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(
+          ar, (uint32_t)(((int64_t)(m0 + row) * args.a.sr + k0 + kc) * 2), 0, 0);
+      areg[i] = k0 + kc < args.k ? make_uint4(v[0], v[1], v[2], v[3]) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < G::BPT; i++) {
+      const int slot = tid + 256 * i, tile = slot >> 6, tl = slot & 63, run = n0 / 16 + tile;
+      bq0[i] = bq1[i] = bex[i] = make_uint4(0, 0, 0, 0);
+      if (run < args.nruns) {
+        const uint8_t *t = bbase + ((int64_t)run * args.chunks + c) * TB;
+        if (FMT == BT_BF16) {
+          bq0[i] = gload((const uint4 *)(t + 32 * tl));
+          bq1[i] = gload((const uint4 *)(t + 32 * tl + 16));
+        } else {
+          if (FMT == BT_BFP8) bq0[i] = gload((const uint4 *)(t + 64 + 16 * tl));
+          else {
+            const uint2 q = gload((const uint2 *)(t + 64 + 8 * tl));
+            bq0[i] = make_uint4(q.x, q.y, 0, 0);
+          }
+          bex[i] = gload((const uint4 *)(t + 16 * (tl >> 4)));
+        }
+      }
+    }
+  };
+  auto stage_in = [&](uint8_t *st) {
+#pragma unroll
+    for (int i = 0; i < G::APT; i++) {
+      const int piece = tid + 256 * i, row = piece >> 3, kc = (piece & 7) * 8;
+      *(uint4 *)(st + (row * G::AS + kc) * 2) = areg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < G::BPT; i++) {
+      const int slot = tid + 256 * i, tile = slot >> 6, tl = slot & 63;
+      bf16x8 h0, h1;
+      if (FMT == BT_BF16) {
+        h0 = *(const bf16x8 *)&bq0[i];
+        h1 = *(const bf16x8 *)&bq1[i];
+      } else if (FMT == BT_BFP8) {
+        h0 = q8_to_bf16<true>(make_uint2(bq0[i].x, bq0[i].y), make_uint2(bex[i].x, bex[i].y));
+        h1 = q8_to_bf16<true>(make_uint2(bq0[i].z, bq0[i].w), make_uint2(bex[i].z, bex[i].w));
+      } else {
+        h0 = q4_to_bf16_scaled(bq0[i].x, make_uint2(bex[i].x, bex[i].y));
+        h1 = q4_to_bf16_scaled(bq0[i].y, make_uint2(bex[i].z, bex[i].w));
+      }
+      uint8_t *bl = st + G::A_BYTES + tile * 2048 + tl * 16;
+      *(bf16x8 *)bl = h0;
+      *(bf16x8 *)(bl + 1024) = h1;
+    }
+  };
+
+  f32x4 acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; i++)
+#pragma unroll
+    for (int j = 0; j < WN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  fetch(0);
+  stage_in(lds);
+  __syncthreads();
+  for (int c = 0; c < args.chunks; c++) {
+    uint8_t *st = lds + (c & 1) * G::STAGE;
+    // the next chunk's loads go out first; its staging comes after this chunk's matrix instructions are issued, so
+    // the conversions run while the matrix cores work
+    const bool more = c + 1 < args.chunks;
+    if (more) fetch(c + 1);
+    const uint16_t *al = (const uint16_t *)st + (wm * WM * 16 + col) * G::AS + 8 * g;
+    const uint8_t *bl = st + G::A_BYTES + wn * WN * 2048 + lane * 16;
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++) {
+      bf16x8 af[WM], bv[WN];
+#pragma unroll
+      for (int i = 0; i < WM; i++) af[i] = *(const bf16x8 *)(al + 16 * i * G::AS + 32 * kk);
+#pragma unroll
+      for (int j = 0; j < WN; j++) bv[j] = *(const bf16x8 *)(bl + j * 2048 + kk * 1024);
+#pragma unroll
+      for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int j = 0; j < WN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) stage_in(lds + ((c + 1) & 1) * G::STAGE);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < WM; i++)
+#pragma unroll
+    for (int j = 0; j < WN; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        uint8_t *at = lds + (wm * WM * 16 + 16 * i + 4 * g + r) * G::ES + (wn * WN * 16 + 16 * j + col) * G::ESZ;
+        if (DT == BT_FP32) *(float *)at = acc[i][j][r];
+        else *(uint16_t *)at = (uint16_t)bf16_packed(acc[i][j][r]);
+      }
+  __syncthreads();
+  gemm_epilogue<DT, G::BM, G::BN, G::ES, G::ESZ>(args, lds, b, m0, n0, tid);
+}
+
+// ---- the prefill GEMM with loads straight into LDS ------------------------------------------------------------------
+// As gemm_kernel, but the global loads of A and of B's raw tiles go straight into LDS (buffer_load ... lds), S chunks
+// deep, so the loads of the next S - 1 chunks are in flight while one is multiplied, without holding registers.
+// A wave's such load writes 1 KB of LDS in lane order; which 16 bytes of the matrix each lane fetches sets the layout:
+//   A: row r of the block (64 halfwords, 128 bytes) holds its 16-byte column c at position c ^ ((r >> 1) & 7), so the
+//      16 lanes that read one column of 16 rows for a fragment hit 16 different groups of 4 banks;
+//   B bf16: the tile in the operand order, [k half][lane][8 values];
+//   B block float: the raw tiles, which the block then turns into bf16 operand order once per chunk.
+// Needs K a multiple of 64: a chunk's loads cannot zero the columns of A past K.
+template <int FMT, int DT, int WM, int WN, int S> struct Gemm2 {
+  static constexpr int BM = 32 * WM, BN = 32 * WN, TB = Tile<FMT>::bytes;
+  static constexpr bool CONVERT = FMT != BT_BF16;
+  static constexpr int A_LOADS = BM / 8;                        // wave loads of 1 KB
+  static constexpr int B_REAL = (BN / 16 * TB + 1023) / 1024;   // B's, and rounded up to whole rounds of 4 waves:
+  static constexpr int B_LOADS = (B_REAL + 3) / 4 * 4;          // the extra ones read nothing into a junk KB
+  static constexpr int PER_WAVE = (A_LOADS + B_LOADS) / 4;
+  static constexpr int A_BYTES = BM * 128, STAGE = A_BYTES + B_REAL * 1024;
+  static constexpr int BBF = CONVERT ? BN / 16 * 2048 : 0;
+  static constexpr int BPT = BN / 16 * 64 / 256;
+  static constexpr int ESZ = DT == BT_FP32 ? 4 : 2, ES = BN * ESZ + 16;
+  static constexpr int JUNK = S * STAGE + BBF, MAIN = JUNK + 1024;
+  static constexpr int LDS = MAIN > BM * ES ? MAIN : BM * ES;
+};
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// A buffer resource as four dwords, for inline assembly: base, stride 0, `bytes` records, the same flags as buffer().
+__device__ __forceinline__ i32x4 buffer_words(const void *base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)(uintptr_t)base;
+  return i32x4{(int)(uint32_t)p, (int)(uint32_t)(p >> 32) & 0xFFFF, (int)bytes, 0x00020000};
+}
+
+// 16 bytes a lane from the buffer at voff into LDS at lds + 16 * lane: one wave writes 1 KB. Issued as assembly so
+// that the compiler, which can't tell which LDS bytes such a load writes, doesn't wait for every one of them before
+// each LDS read; the kernel waits for them itself (wait_vm). Loads complete in order, so the compiler's own waits
+// on other loads stay correct (at worst they wait for these too).
+__device__ __forceinline__ void lds_load16(const i32x4 &rsrc, uint32_t voff, const void *lds) {
+  const uint32_t at = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds;
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(at)
+               : "memory", "m0");
+}
+
+// Waits until at most N vector memory loads of this wave are outstanding. Assembly too: the compiler would drop a
+// wait for loads it doesn't know of.
+template <int N> __device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+template <int FMT, int DT, int WM, int WN, int S>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gemm2_kernel(const MatmulArgs args, int mblocks, int nblocks) {
+  using G = Gemm2<FMT, DT, WM, WN, S>;
+  constexpr int TB = G::TB;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[G::LDS];
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, col = lane & 15;
+  const int wib = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wib >> 1, wn = wib & 1;
+  const int per = mblocks * nblocks, total = per * args.batch, full = total / 8 * 8;
+  int pid = blockIdx.x;
+  if (pid < full) pid = (pid % 8) * (full / 8) + pid / 8;
+  const int b = pid / per;
+  pid %= per;
+  constexpr int GROUP = 8;
+  const int width = GROUP * nblocks, first = pid / width * GROUP, gsz = min(mblocks - first, GROUP);
+  const int bm = first + pid % width % gsz, bn = pid % width / gsz;
+  const int m0 = bm * G::BM, n0 = bn * G::BN;
+
+  const uint16_t *abase = (const uint16_t *)args.a.ptr + operand_matrix(args.a, b) * args.a.sb;
+  const i32x4 ar = buffer_words(abase, (uint32_t)(((int64_t)(args.m - 1) * args.a.sr + args.k) * 2));
+  const uint8_t *bbase = args.b + (args.b_matrix_bytes ? b * args.b_matrix_bytes : 0);
+  const i32x4 br = buffer_words(bbase, (uint32_t)((int64_t)args.nruns * args.chunks * TB));
+  constexpr uint32_t NOWHERE = 0xFFFFFFF0u;  // an offset past every buffer: the load writes zeros
+
+  // the 16-byte source of each lane for each of the wave's loads of one chunk (the chunk adds 128 bytes to A's and
+  // one tile to B's offsets)
+  uint32_t src[G::PER_WAVE];
+#pragma unroll
+  for (int j = 0; j < G::PER_WAVE; j++) {
+    const int li = wib + 4 * j;  // the block's load index
+    if (li < G::A_LOADS) {
+      const int slot = li * 64 + lane, r = slot >> 3, c = (slot & 7) ^ ((r >> 1) & 7);
+      src[j] = (uint32_t)(((int64_t)(m0 + r) * args.a.sr + 8 * c) * 2);
+    } else {
+      const int slot = (li - G::A_LOADS) * 64 + lane;
+      int tile, off;
+      if (FMT == BT_BF16) {
+        tile = slot >> 7;
+        const int q = slot & 127;
+        off = 32 * (q & 63) + 16 * (q >> 6);
+      } else {
+        tile = slot * 16 / TB;
+        off = slot * 16 % TB;
+      }
+      const int run = n0 / 16 + tile;
+      src[j] = li - G::A_LOADS < G::B_REAL && tile < G::BN / 16 && run < args.nruns
+                   ? (uint32_t)((int64_t)run * args.chunks * TB + off) : NOWHERE;
+    }
+  }
+  auto issue = [&](int c) {  // chunk c's loads into stage c % S
+    uint8_t *st = lds + (c % S) * G::STAGE;
+#pragma unroll
+    for (int j = 0; j < G::PER_WAVE; j++) {
+      const int li = wib + 4 * j;
+      const bool isa = li < G::A_LOADS;
+      const uint32_t off = src[j] == NOWHERE ? NOWHERE : src[j] + (isa ? c * 128u : (uint32_t)c * TB);
+      uint8_t *dst = isa ? st + li * 1024
+                     : li - G::A_LOADS < G::B_REAL ? st + G::A_BYTES + (li - G::A_LOADS) * 1024 : lds + G::JUNK;
+      lds_load16(isa ? ar : br, off, dst);
+    }
+  };
+
+  f32x4 acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; i++)
+#pragma unroll
+    for (int j = 0; j < WN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int c = 0; c < S - 1; c++)
+    if (c < args.chunks) issue(c);
+  uint8_t *bbf = lds + S * G::STAGE;
+  for (int c = 0; c < args.chunks; c++) {
+    // chunk c has landed once at most the later chunks' loads are outstanding (fewer near the end)
+    if (c + S - 2 < args.chunks) wait_vm<G::PER_WAVE * (S - 2)>();
+    else wait_vm<0>();
+    __syncthreads();
+    uint8_t *st = lds + (c % S) * G::STAGE;
+    if (G::CONVERT) {
+      const uint8_t *raw = st + G::A_BYTES;
+#pragma unroll
+      for (int i = 0; i < G::BPT; i++) {
+        const int slot = tid + 256 * i, tile = slot >> 6, tl = slot & 63;
+        const uint8_t *t = raw + tile * TB;
+        const uint4 ex = *(const uint4 *)(t + 16 * (tl >> 4));
+        bf16x8 h0, h1;
+        if (FMT == BT_BFP8) {
+          const uint4 q = *(const uint4 *)(t + 64 + 16 * tl);
+          h0 = q8_to_bf16<true>(make_uint2(q.x, q.y), make_uint2(ex.x, ex.y));
+          h1 = q8_to_bf16<true>(make_uint2(q.z, q.w), make_uint2(ex.z, ex.w));
+        } else {
+          const uint2 q = *(const uint2 *)(t + 64 + 8 * tl);
+          h0 = q4_to_bf16_scaled(q.x, make_uint2(ex.x, ex.y));
+          h1 = q4_to_bf16_scaled(q.y, make_uint2(ex.z, ex.w));
+        }
+        uint8_t *bl = bbf + tile * 2048 + tl * 16;
+        *(bf16x8 *)bl = h0;
+        *(bf16x8 *)(bl + 1024) = h1;
+      }
+      __syncthreads();
+    }
+    if (c + S - 1 < args.chunks) issue(c + S - 1);  // into the stage chunk c - 1 used
+    const uint8_t *bsrc = G::CONVERT ? bbf : st + G::A_BYTES;
+    const uint8_t *bl = bsrc + wn * WN * 2048 + lane * 16;
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++) {
+      bf16x8 af[WM], bv[WN];
+#pragma unroll
+      for (int i = 0; i < WM; i++) {
+        const int r = wm * WM * 16 + 16 * i + col, cc = (g + 4 * kk) ^ ((r >> 1) & 7);
+        af[i] = *(const bf16x8 *)(st + r * 128 + 16 * cc);
+      }
+#pragma unroll
+      for (int j = 0; j < WN; j++) bv[j] = *(const bf16x8 *)(bl + j * 2048 + kk * 1024);
+#pragma unroll
+      for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int j = 0; j < WN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  __syncthreads();  // every wave is done with the stages
+#pragma unroll
+  for (int i = 0; i < WM; i++)
+#pragma unroll
+    for (int j = 0; j < WN; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        uint8_t *at = lds + (wm * WM * 16 + 16 * i + 4 * g + r) * G::ES + (wn * WN * 16 + 16 * j + col) * G::ESZ;
+        if (DT == BT_FP32) *(float *)at = acc[i][j][r];
+        else *(uint16_t *)at = (uint16_t)bf16_packed(acc[i][j][r]);
+      }
+  __syncthreads();
+  gemm_epilogue<DT, G::BM, G::BN, G::ES, G::ESZ>(args, lds, b, m0, n0, tid);
+}
+
 int validate_program(const bt_program *prog);
 int check_out(const bt_operand *out);
 
@@ -348,12 +711,60 @@ static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bo
   else skinny_kernel<FMT, DT, false><<<blocks, 256, 0, s>>>(args);
 }
 
+// The deepest pipeline (3 or 2 chunks) whose LDS fits the 160 KB of a CU.
+template <int FMT, int DT, int WM, int WN> constexpr int gemm2_stages() {
+  return Gemm2<FMT, DT, WM, WN, 3>::LDS <= 160 * 1024 ? 3 : 2;
+}
+
+template <int FMT, int DT, int WM, int WN>
+static void launch_gemm(const MatmulArgs &args, hipStream_t s) {
+  const int bm = 32 * WM, bn = 32 * WN;
+  const int mb = (args.m + bm - 1) / bm, nb = (args.n + bn - 1) / bn;
+  const unsigned blocks = (unsigned)((int64_t)mb * nb * args.batch);
+  if (args.k % 64 == 0) {
+    constexpr int S = gemm2_stages<FMT, DT, WM, WN>();
+    static_assert(Gemm2<FMT, DT, WM, WN, S>::LDS <= 160 * 1024, "GEMM LDS");
+    gemm2_kernel<FMT, DT, WM, WN, S><<<blocks, 256, 0, s>>>(args, mb, nb);
+  } else if constexpr (WM == 4 && WN == 4) {
+    gemm_kernel<FMT, DT, WM, WN><<<blocks, 256, 0, s>>>(args, mb, nb);
+  }
+}
+
+// The block shape for a GEMM: the largest tile whose grid still keeps the chip's 256 CUs busy through its last round.
+template <int FMT, int DT>
+static void launch_gemm_dt(const MatmulArgs &args, hipStream_t s) {
+  struct Option { int bm, bn; double eff; };  // eff: throughput of a full round relative to 256 x 256
+  const Option opts[3] = {{256, 256, 1.0}, {256, 128, 0.85}, {128, 128, 0.7}};
+  int best = 0;
+  double score = -1.0;
+  for (int o = 0; o < 3; o++) {
+    if (o < 2 && (args.m <= 128 || args.k % 64)) continue;  // K past whole chunks: the register-staged 128 x 128 kernel
+    if (o == 0 && DT == BT_FP32) continue;  // its fp32 epilogue values would not fit in LDS
+    const int64_t blocks = (int64_t)args.batch * ((args.m + opts[o].bm - 1) / opts[o].bm) * ((args.n + opts[o].bn - 1) / opts[o].bn);
+    const int64_t rounds = (blocks + 255) / 256;
+    const double sc = opts[o].eff * (double)blocks / (double)(rounds * 256);
+    if (sc > score + 1e-9) score = sc, best = o;
+  }
+  if constexpr (DT != BT_FP32) {
+    if (best == 0) return launch_gemm<FMT, DT, 8, 8>(args, s);
+  }
+  if (best == 1) launch_gemm<FMT, DT, 8, 4>(args, s);
+  else launch_gemm<FMT, DT, 4, 4>(args, s);
+}
+
 template <int FMT>
 static void launch_skinny(const MatmulArgs &args, hipStream_t s) {
   const int64_t waves = (int64_t)args.batch * args.mtiles * args.nruns;
   const unsigned blocks = (unsigned)((waves + 3) / 4);
   const bt_operand &a = args.a;
   const bool vec = a.sc == 1 && a.sr % 8 == 0 && a.ptr % 16 == 0 && a.sb % 8 == 0 && args.k % 8 == 0;
+  // many rows: the tiled GEMM, when A's rows are contiguous, aligned and within reach of one buffer resource
+  const bool gemm = vec && args.m > 64 && ((int64_t)(args.m - 1) * a.sr + args.k) * 2 < (1ll << 32);
+  if (gemm) {
+    if (args.prog.dtype == BT_FP32) launch_gemm_dt<FMT, BT_FP32>(args, s);
+    else launch_gemm_dt<FMT, BT_BF16>(args, s);
+    return;
+  }
   if (args.prog.dtype == BT_FP32) launch_dt<FMT, BT_FP32>(args, blocks, s, vec);
   else launch_dt<FMT, BT_BF16>(args, blocks, s, vec);
 }

@@ -164,7 +164,7 @@ __device__ __forceinline__ void fetch_inputs(const bt_program &prog, const Coord
 
 // The transcendental and other long operations, kept out of line: each expands to dozens of instructions, and inlined
 // into every op's branch they would make the evaluator larger than the instruction cache.
-__device__ __attribute__((noinline)) float long_op(int op, float a) {
+__device__ __forceinline__ float long_op_inline(int op, float a) {
   switch (op) {
     case BT_OP_EXP: return expf(a);
     case BT_OP_EXP2: return exp2f(a);
@@ -182,9 +182,12 @@ __device__ __attribute__((noinline)) float long_op(int op, float a) {
     default: return a;
   }
 }
+__device__ __attribute__((noinline)) float long_op(int op, float a) { return long_op_inline(op, a); }
 
-// One instruction over V values. op is uniform, so the switch is a scalar branch around straight vector code.
-template <int DT, int V>
+// One instruction over V values. op is uniform, so the switch is a scalar branch around straight vector code. INL
+// inlines the long operations too: for callers that hold many live registers (a GEMM's accumulators), which a call
+// would have to save to memory.
+template <int DT, int V, bool INL = false>
 __device__ __forceinline__ Vals<V> apply_op(int op, const Vals<V> &a, const Vals<V> &b) {
   Vals<V> o;
   if (DT == BT_INT32) {
@@ -219,7 +222,7 @@ __device__ __forceinline__ Vals<V> apply_op(int op, const Vals<V> &a, const Vals
     BT_OP(BT_OP_FTOB, round_packed(A))
     default:
 #pragma unroll
-      for (int v = 0; v < V; v++) f[v] = long_op(op, x[v]);
+      for (int v = 0; v < V; v++) f[v] = INL ? long_op_inline(op, x[v]) : long_op(op, x[v]);
   }
 #undef BT_OP
 #pragma unroll
@@ -229,7 +232,7 @@ __device__ __forceinline__ Vals<V> apply_op(int op, const Vals<V> &a, const Vals
 
 // Runs prog on V elements whose inputs are in pre. io holds the incoming value (register 0: a matmul epilogue's
 // result) and receives the result register's bits.
-template <int DT, int V>
+template <int DT, int V, bool INL = false>
 __device__ __forceinline__ void eval_program(const bt_program &prog, const prefile (&pre)[V], uint32_t (&io)[V]) {
   regfile regs[V];
 #pragma unroll
@@ -253,7 +256,7 @@ __device__ __forceinline__ void eval_program(const bt_program &prog, const prefi
         o.x[v] = on ? t.x[v] : e.x[v];
       }
     } else {
-      o = apply_op<DT, V>(in.op, regs_get<V>(regs, in.a), regs_get<V>(regs, in.b));
+      o = apply_op<DT, V, INL>(in.op, regs_get<V>(regs, in.a), regs_get<V>(regs, in.b));
     }
     regs_set<V>(regs, in.dst, o);
   }
@@ -263,22 +266,22 @@ __device__ __forceinline__ void eval_program(const bt_program &prog, const prefi
 }
 
 // Runs prog at V elements: fetch, then evaluate. io as for eval_program.
-template <int DT, int V>
+template <int DT, int V, bool INL = false>
 __device__ __forceinline__ void run_program_v(const bt_program &prog, const Coords<V> &at, uint32_t (&io)[V]) {
   prefile pre[V];
   fetch_inputs<DT, V>(prog, at, pre);
-  eval_program<DT, V>(prog, pre, io);
+  eval_program<DT, V, INL>(prog, pre, io);
 }
 
 // Runs prog at element (b, r, c). acc, if the program reads register 0 as a preloaded value (a matmul epilogue), is
 // placed there first. Returns the result register's bits.
-template <int DT>
+template <int DT, bool INL = false>
 __device__ __forceinline__ uint32_t run_program(const bt_program &prog, int64_t b, int64_t r, int64_t c,
                                                 uint32_t acc) {
   Coords<1> at;
   at.b[0] = b, at.r[0] = r, at.c[0] = c, at.ok[0] = true;
   uint32_t io[1] = {acc};
-  run_program_v<DT, 1>(prog, at, io);
+  run_program_v<DT, 1, INL>(prog, at, io);
   return io[0];
 }
 

@@ -213,6 +213,40 @@ def test_fused_relu_epilogue_config1(rt):
   assert np.all(np.abs(fused - np.maximum(ops.matmul(xw, wq), 0)) <= ops.matmul_bound(xw, wq))
 
 
+# (rows, K, N, output): rows > 64 run the tiled GEMM. 2048 x 8192 picks its 256 x 256 blocks, 2048 x 4096 in fp32 its
+# 256 x 128 blocks, the rest 128 x 128 blocks; 1000 and 520 leave a partial chunk of K and a partial run of N.
+GEMM_CASES = [(300, 1000, 520, "bf16"), (96, 576, 1536, "fp32"), (2048, 256, 8192, "bf16"), (2048, 192, 4096, "fp32")]
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bfp4"])
+@pytest.mark.parametrize("case", GEMM_CASES, ids=lambda c: "m{}k{}n{}{}".format(*c))
+def test_gemm_equals_row_slices(rt, fmt, case):
+  # The GEMM sums each output in the same order as the decode kernels (64-row chunks of K, lower half then upper), so
+  # it equals, bit for bit, the same product computed 64 rows at a time; with a fused epilogue (relu for bf16, a
+  # residual add for fp32) as well. And it is within the reference's bound of the oracle.
+  m, k, n, out = case
+  rng = np.random.default_rng(m + k + n)
+  x, w = rng.normal(0, 1, (m, k)), rng.normal(0, 0.05, (k, n)).astype(np.float32)
+  if fmt == "bf16":
+    cols, wq = bf16_columns(rt, w), B.bf16(w)
+  else:
+    exps, vals = pack(rt, w, fmt)
+    cols, wq = columns(rt, exps, vals, fmt, 1, k, n), bfp_values(w, fmt)
+  p = Program(out, epilogue=True)
+  if out == "bf16": prog = p.build(p.op("relu", p.value()))
+  else:
+    res = B.bf16(rng.normal(0, 1, (m, n)))
+    prog = p.build(p.op("add", p.value(), p.load(p.input(_lib.operand(up(rt, res.astype(np.float32)), "fp32", m * n, n, 1)))))
+  got = matmul(rt, x, cols, fmt, 1, n, out=out, prog=prog)[0]
+  plain = matmul(rt, x, cols, fmt, 1, n, out=out)[0]
+  sliced = np.concatenate([matmul(rt, x[i:i + 64], cols, fmt, 1, n, out=out)[0] for i in range(0, m, 64)])
+  assert np.array_equal(plain, sliced)
+  if out == "bf16": assert np.array_equal(got, np.maximum(plain, 0))
+  else: assert np.array_equal(got, (plain + res).astype(np.float32))
+  xw = B.bf16(x)
+  assert np.all(np.abs(plain - ops.matmul(xw, wq)) <= ops.matmul_bound(xw, wq))
+
+
 def test_epilogue_reads_other_inputs(rt):
   # (x @ w + bias) * d - c in one launch equals the unfused chain with bf16 rounding after each op
   rng = np.random.default_rng(3)
