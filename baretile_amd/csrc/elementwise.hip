@@ -5,28 +5,44 @@
 namespace bt {
 
 // A thread an element, in row-major order of the result.
-constexpr int EW_V = 1;  // elements per thread
-
-// A thread takes EW_V elements of the flattened result, 256 apart, so every load and store of a wavefront is
-// contiguous along the columns. One element a thread keeps the evaluator's code small; the grid has the parallelism. The flat index fits 31 bits (the launcher checks), and the row and batch entry are
-// split off it by multiplication (FastDiv).
-template <int DT>
+// A thread takes V elements of the flattened result, 256 apart, so every load and store of a wavefront is contiguous
+// along the columns. Small results take one element a thread, which keeps the evaluator's code small and the grid
+// wide; large ones take 8, so each instruction of the program is decoded once for 8 values. The flat index fits 31
+// bits (the launcher checks), and the row and batch entry are split off it by multiplication (FastDiv).
+template <int DT, int V>
 __global__ void __launch_bounds__(256) elementwise_kernel(const bt_program prog, uint32_t total, FastDiv cols,
                                                           FastDiv rows, const bt_operand out) {
-  const uint32_t base = blockIdx.x * (256u * EW_V) + threadIdx.x;
-  Coords<EW_V> at;
+  const uint32_t base = blockIdx.x * (256u * V) + threadIdx.x;
+  Coords<V> at;
 #pragma unroll
-  for (int v = 0; v < EW_V; v++) {
+  for (int v = 0; v < V; v++) {
     const uint32_t t = base + 256u * v;
     at.ok[v] = t < total;
     const uint32_t u = at.ok[v] ? t : 0u, q = fdiv(u, cols), bb = fdiv(q, rows);
     at.c[v] = u - q * cols.d, at.r[v] = q - bb * rows.d, at.b[v] = bb;
   }
-  uint32_t io[EW_V] = {};
-  run_program_v<DT, EW_V>(prog, at, io);
+  uint32_t io[V] = {};
+  run_program_v<DT, V>(prog, at, io);
 #pragma unroll
-  for (int v = 0; v < EW_V; v++)
+  for (int v = 0; v < V; v++)
     if (at.ok[v]) store_value<DT>(out, operand_matrix(out, at.b[v]) * out.sb + at.r[v] * out.sr + at.c[v] * out.sc, io[v]);
+}
+
+// Large results: a thread evaluates a segment of SEG neighbouring columns of one row (fetch_segment). segs is the
+// number of segments in a row.
+template <int DT>
+__global__ void __launch_bounds__(256) elementwise_seg_kernel(const bt_program prog, uint32_t nseg, FastDiv segs,
+                                                              FastDiv rows, int32_t cols, const bt_operand out) {
+  const uint32_t s = blockIdx.x * 256u + threadIdx.x;
+  if (s >= nseg) return;
+  const uint32_t q = fdiv(s, segs), bb = fdiv(q, rows);
+  const int64_t c0 = (int64_t)(s - q * segs.d) * SEG, r = q - bb * rows.d;
+  const int n = (int)min((int64_t)SEG, cols - c0);
+  prefile pre[SEG];
+  fetch_segment<DT>(prog, bb, r, c0, n, pre);
+  uint32_t io[SEG] = {};
+  eval_program<DT, SEG>(prog, pre, io);
+  store_segment<DT>(out, bb, r, c0, n, io);
 }
 
 // The same for results of 2^31 elements or more: one element per thread, 64-bit index arithmetic.
@@ -123,6 +139,55 @@ __global__ void __launch_bounds__(WPO > 4 ? 64 * WPO : 256) reduce_kernel(const 
   }
 }
 
+// Reductions along the last axis of large inputs: lanes take segments of SEG neighbouring columns (fetch_segment),
+// otherwise as reduce_kernel.
+template <int DT, int WPO>
+__global__ void __launch_bounds__(WPO > 4 ? 64 * WPO : 256) reduce_seg_kernel(const bt_program prog, int kind,
+                                                                               int64_t batch, int64_t rows,
+                                                                               int64_t cols, const bt_operand out) {
+  __shared__ uint32_t part[WPO];
+  const int lane = threadIdx.x & 63;
+  const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t w = WPO > 1 ? (int64_t)blockIdx.x : (int64_t)blockIdx.x * 4 + wib;
+  if (w >= batch * rows) return;  // uniform across the block when WPO > 1
+  const int64_t r = w % rows, b = w / rows, nseg = (cols + SEG - 1) / SEG;
+  float facc = kind == BT_REDUCE_SUM ? 0.0f : -__builtin_inff();
+  int32_t iacc = INT32_MIN;
+  for (int64_t sg = (WPO > 1 ? wib * 64 : 0) + lane; sg < nseg; sg += 64 * WPO) {
+    const int64_t c0 = sg * SEG;
+    const int n = (int)min((int64_t)SEG, cols - c0);
+    prefile pre[SEG];
+    fetch_segment<DT>(prog, b, r, c0, n, pre);
+    uint32_t io[SEG] = {};
+    eval_program<DT, SEG>(prog, pre, io);
+#pragma unroll
+    for (int v = 0; v < SEG; v++) {
+      if (v >= n) continue;
+      if (DT == BT_INT32) iacc = max(iacc, (int32_t)io[v]);
+      else if (kind == BT_REDUCE_SUM) facc += __uint_as_float(io[v]);
+      else facc = nan_max(facc, __uint_as_float(io[v]));
+    }
+  }
+  uint32_t res;
+  if (DT == BT_INT32) res = (uint32_t)wave_imax(iacc);
+  else res = __float_as_uint(kind == BT_REDUCE_SUM ? wave_sum(facc) : wave_max(facc));
+  if (WPO > 1) {
+    if (lane == 0) part[wib] = res;
+    __syncthreads();
+    if (wib != 0) return;
+    for (int k = 1; k < WPO; k++) {
+      const uint32_t o = part[k];
+      if (DT == BT_INT32) res = (uint32_t)max((int32_t)res, (int32_t)o);
+      else if (kind == BT_REDUCE_SUM) res = __float_as_uint(__uint_as_float(res) + __uint_as_float(o));
+      else res = __float_as_uint(nan_max(__uint_as_float(res), __uint_as_float(o)));
+    }
+  }
+  if (lane == 0) {
+    if (DT == BT_BF16) res = __float_as_uint(round_packed(__uint_as_float(res)));
+    store_value<DT>(out, operand_matrix(out, b) * out.sb + r * out.sr, res);
+  }
+}
+
 // A block a gathered row: 256 threads copy its 32-bit words (a bf16 row of odd width copies its last half word).
 __global__ void __launch_bounds__(256) gather_kernel(const uint8_t *table, int64_t rows, int64_t row_bytes,
                                                      int64_t table_rstride_bytes, const int32_t *ids, uint8_t *out,
@@ -148,6 +213,40 @@ __global__ void __launch_bounds__(256) put_kernel(uint8_t *dst, int64_t dst_rows
     int32_t p = ids[i];
     if (p < 0 || p >= dst_rows) continue;
     *(uint16_t *)(dst + b * dst_sb + p * dst_sr + at) = *(const uint16_t *)(x + b * x_sb + i * x_sr + at);
+  }
+}
+
+// One block per row i of x, for all batch entries at once. A later duplicate place wins (tensor.py:223-241): the block
+// first looks for a j > i with the same place, and writes nothing if there is one. Rows move in 16-byte pieces when
+// both sides allow it. For n up to PUT_SCAN rows; the scan is O(n) a block.
+constexpr int64_t PUT_SCAN = 8192;
+__global__ void __launch_bounds__(256) put_rows_kernel(uint8_t *dst, int64_t dst_rows, int64_t row_bytes,
+                                                       int64_t dst_sb, int64_t dst_sr, const int32_t *ids, int64_t n,
+                                                       const uint8_t *x, int64_t x_sb, int64_t x_sr, int64_t batch,
+                                                       int wide) {
+  __shared__ int later;
+  const int64_t i = blockIdx.x;
+  const int32_t p = ids[i];
+  if (p < 0 || p >= dst_rows) return;
+  if (threadIdx.x == 0) later = 0;
+  __syncthreads();
+  bool found = false;
+  for (int64_t j = i + 1 + threadIdx.x; j < n; j += blockDim.x) found |= ids[j] == p;
+  if (found) later = 1;
+  __syncthreads();
+  if (later) return;
+  if (wide) {
+    const int64_t pieces = row_bytes / 16;
+    for (int64_t e = threadIdx.x; e < batch * pieces; e += blockDim.x) {
+      const int64_t b = e / pieces, at = e % pieces * 16;
+      *(uint4 *)(dst + b * dst_sb + p * dst_sr + at) = *(const uint4 *)(x + b * x_sb + i * x_sr + at);
+    }
+  } else {
+    const int64_t halves = row_bytes / 2;
+    for (int64_t e = threadIdx.x; e < batch * halves; e += blockDim.x) {
+      const int64_t b = e / halves, at = e % halves * 2;
+      *(uint16_t *)(dst + b * dst_sb + p * dst_sr + at) = *(const uint16_t *)(x + b * x_sb + i * x_sr + at);
+    }
   }
 }
 
@@ -202,13 +301,29 @@ int bt_elementwise(bt_runtime *rt, const bt_program *prog, int64_t batch, int64_
   if (batch <= 0 || rows <= 0 || cols <= 0) return fail(BT_EINVAL, "elementwise shape must be positive");
   const int64_t total = batch * rows * cols;
   if (total < (1ll << 31)) {
-    const unsigned blocks = (unsigned)((total + 256 * EW_V - 1) / (256 * EW_V));
     const FastDiv fc = make_fastdiv((uint32_t)cols), fr = make_fastdiv((uint32_t)rows);
-    if (prog->dtype == BT_BF16)
-      elementwise_kernel<BT_BF16><<<blocks, 256, 0, r->stream>>>(*prog, (uint32_t)total, fc, fr, *out);
-    else if (prog->dtype == BT_FP32)
-      elementwise_kernel<BT_FP32><<<blocks, 256, 0, r->stream>>>(*prog, (uint32_t)total, fc, fr, *out);
-    else elementwise_kernel<BT_INT32><<<blocks, 256, 0, r->stream>>>(*prog, (uint32_t)total, fc, fr, *out);
+#define BT_EW(V)                                                                                                  \
+  do {                                                                                                            \
+    const unsigned blocks = (unsigned)((total + 256 * V - 1) / (256 * V));                                        \
+    if (prog->dtype == BT_BF16)                                                                                   \
+      elementwise_kernel<BT_BF16, V><<<blocks, 256, 0, r->stream>>>(*prog, (uint32_t)total, fc, fr, *out);        \
+    else if (prog->dtype == BT_FP32)                                                                              \
+      elementwise_kernel<BT_FP32, V><<<blocks, 256, 0, r->stream>>>(*prog, (uint32_t)total, fc, fr, *out);        \
+    else elementwise_kernel<BT_INT32, V><<<blocks, 256, 0, r->stream>>>(*prog, (uint32_t)total, fc, fr, *out);    \
+  } while (0)
+    const int64_t segs = (cols + SEG - 1) / SEG, nseg = batch * rows * segs;
+    if (total >= (1 << 16) && cols >= SEG && nseg < (1ll << 31)) {
+      const FastDiv fs = make_fastdiv((uint32_t)segs);
+      const unsigned blocks = (unsigned)((nseg + 255) / 256);
+      if (prog->dtype == BT_BF16)
+        elementwise_seg_kernel<BT_BF16><<<blocks, 256, 0, r->stream>>>(*prog, (uint32_t)nseg, fs, fr, (int32_t)cols, *out);
+      else if (prog->dtype == BT_FP32)
+        elementwise_seg_kernel<BT_FP32><<<blocks, 256, 0, r->stream>>>(*prog, (uint32_t)nseg, fs, fr, (int32_t)cols, *out);
+      else elementwise_seg_kernel<BT_INT32><<<blocks, 256, 0, r->stream>>>(*prog, (uint32_t)nseg, fs, fr, (int32_t)cols, *out);
+    } else {
+      BT_EW(1);
+    }
+#undef BT_EW
   } else {
     const unsigned blocks = 1u << 20;
     if (prog->dtype == BT_BF16)
@@ -248,6 +363,22 @@ int bt_reduce(bt_runtime *rt, const bt_program *prog, int kind, int axis, int64_
       reduce_kernel<BT_FP32, WPO><<<blocks, threads, 0, r->stream>>>(*prog, kind, axis, batch, rows, cols, sweep, step, *out); \
     else reduce_kernel<BT_INT32, WPO><<<blocks, threads, 0, r->stream>>>(*prog, kind, axis, batch, rows, cols, sweep, step, *out); \
   } while (0)
+  if (axis == 2 && cols >= 64 && outs * cols >= (1 << 16)) {  // large: segments of neighbouring columns
+#define BT_RSEG(WPO, blocks)                                                                                      \
+  do {                                                                                                          \
+    const unsigned threads = WPO > 4 ? 64 * WPO : 256;                                                          \
+    if (prog->dtype == BT_BF16)                                                                                 \
+      reduce_seg_kernel<BT_BF16, WPO><<<blocks, threads, 0, r->stream>>>(*prog, kind, batch, rows, cols, *out);   \
+    else if (prog->dtype == BT_FP32)                                                                            \
+      reduce_seg_kernel<BT_FP32, WPO><<<blocks, threads, 0, r->stream>>>(*prog, kind, batch, rows, cols, *out);   \
+    else reduce_seg_kernel<BT_INT32, WPO><<<blocks, threads, 0, r->stream>>>(*prog, kind, batch, rows, cols, *out); \
+  } while (0)
+    if (outs < 2048) BT_RSEG(4, (unsigned)outs);  // (16 waves would leave each lane too few registers)
+    else BT_RSEG(1, (unsigned)((outs + 3) / 4));
+#undef BT_RSEG
+    BT_LAUNCHED("reduce");
+    return BT_OK;
+  }
   // with too few outputs to fill the chip, a block of waves on each output: about one value a lane
   if (outs < 2048 && n > 512) BT_REDUCE(16, (unsigned)outs);
   else if (outs < 2048 && n > 128) BT_REDUCE(4, (unsigned)outs);
@@ -279,10 +410,19 @@ int bt_put(bt_runtime *rt, int dtype, uint64_t dst, int64_t batch, int64_t dst_r
   if (batch <= 0 || dst_rows <= 0 || cols <= 0 || n < 0) return fail(BT_EINVAL, "put shape");
   if (!n) return BT_OK;
   int size = dtype == BT_BF16 ? 2 : 4;
-  int64_t row_bytes = cols * size, pieces = (row_bytes / 2 + 255) / 256;
-  put_kernel<<<(unsigned)(batch * pieces), 256, 0, r->stream>>>((uint8_t *)dst, dst_rows, row_bytes, dst_sb * size,
-                                                                dst_sr * size, (const int32_t *)ids, n,
-                                                                (const uint8_t *)x, x_sb * size, x_sr * size, pieces);
+  int64_t row_bytes = cols * size;
+  if (n <= PUT_SCAN) {
+    const int wide = row_bytes % 16 == 0 && dst % 16 == 0 && x % 16 == 0 && (dst_sb * size) % 16 == 0 &&
+                     (dst_sr * size) % 16 == 0 && (x_sb * size) % 16 == 0 && (x_sr * size) % 16 == 0;
+    put_rows_kernel<<<(unsigned)n, 256, 0, r->stream>>>((uint8_t *)dst, dst_rows, row_bytes, dst_sb * size,
+                                                        dst_sr * size, (const int32_t *)ids, n, (const uint8_t *)x,
+                                                        x_sb * size, x_sr * size, batch, wide);
+  } else {
+    int64_t pieces = (row_bytes / 2 + 255) / 256;
+    put_kernel<<<(unsigned)(batch * pieces), 256, 0, r->stream>>>((uint8_t *)dst, dst_rows, row_bytes, dst_sb * size,
+                                                                  dst_sr * size, (const int32_t *)ids, n,
+                                                                  (const uint8_t *)x, x_sb * size, x_sr * size, pieces);
+  }
   BT_LAUNCHED("put");
   return BT_OK;
 }

@@ -359,14 +359,27 @@ __device__ __forceinline__ void gemm_epilogue(const MatmulArgs &args, const uint
     }
     return;
   }
+  // through the program, a segment of SEG neighbouring columns a thread (fetch_segment), so the program is decoded
+  // once for SEG values and contiguous inputs and outputs move 16 bytes at a time
+  (void)obase;
+  constexpr int GS = BN / SEG;
 #pragma unroll 1
-  for (int e = tid; e < rows * BN; e += 256) {
-    const int r = e / BN, c = e % BN;
-    if (c >= cols) continue;
-    const uint8_t *at = lds + r * ES + c * ESZ;
-    const uint32_t x = DT == BT_FP32 ? *(const uint32_t *)at : (uint32_t)*(const uint16_t *)at << 16;
-    const uint32_t y = args.prog.n_inst ? run_program<DT, true>(args.prog, b, m0 + r, n0 + c, x) : x;
-    store_value<DT>(args.out, obase + (int64_t)(m0 + r) * args.out.sr + (int64_t)(n0 + c) * args.out.sc, y);
+  for (int e = tid; e < rows * GS; e += 256) {
+    const int r = e / GS, c0 = e % GS * SEG;
+    if (c0 >= cols) continue;
+    const int n = min(SEG, cols - c0);
+    uint32_t io[SEG];
+#pragma unroll
+    for (int v = 0; v < SEG; v++) {
+      const uint8_t *src = lds + r * ES + (c0 + v) * ESZ;
+      io[v] = DT == BT_FP32 ? *(const uint32_t *)src : (uint32_t)*(const uint16_t *)src << 16;
+    }
+    if (args.prog.n_inst) {
+      prefile pre[SEG];
+      fetch_segment<DT>(args.prog, b, m0 + r, n0 + c0, n, pre);
+      eval_program<DT, SEG>(args.prog, pre, io);
+    }
+    store_segment<DT>(args.out, b, m0 + r, n0 + c0, n, io);
   }
 }
 

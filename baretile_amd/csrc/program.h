@@ -285,6 +285,117 @@ __device__ __forceinline__ uint32_t run_program(const bt_program &prog, int64_t 
   return io[0];
 }
 
+// ---- evaluation over row segments ----------------------------------------------------------------------------------
+// For results large enough to fill the chip many times: a thread evaluates SEG neighbouring columns c0 .. c0 + SEG - 1
+// of one row. Each input's address is worked out once per segment; an input whose columns are contiguous is read with
+// 16-byte loads, a broadcast one (column stride 0) with one load, any other value by value. The inputs are fetched by
+// a loop that is not unrolled, which keeps the code small; the latency of one input's loads is hidden by the many
+// other waves in flight.
+constexpr int SEG = 8;
+
+// A raw element of an input (bf16 bits in the low half, or 32 bits) as the program's dtype: the conversions of
+// load_operand.
+template <int DT>
+__device__ __forceinline__ uint32_t convert_raw(uint32_t raw, int dtype) {
+  if (dtype == BT_BF16) {
+    if (DT == BT_INT32) return (uint32_t)(int32_t)rintf(bf16_value(raw & 0xFFFFu));
+    return raw << 16;
+  }
+  if (dtype == BT_INT32 && DT != BT_INT32) {
+    const float f = (float)(int32_t)raw;
+    return __float_as_uint(DT == BT_BF16 ? round_packed(f) : f);
+  }
+  if (dtype == BT_FP32 && DT == BT_INT32) return (uint32_t)(int32_t)rintf(__uint_as_float(raw));
+  if (dtype == BT_FP32 && DT == BT_BF16) return __float_as_uint(round_packed(__uint_as_float(raw)));
+  return raw;
+}
+
+// The inputs of prog for the segment (b, r, c0 .. c0 + n - 1), n <= SEG; 0 past n.
+template <int DT>
+__device__ __forceinline__ void fetch_segment(const bt_program &prog, int64_t b, int64_t r, int64_t c0, int n,
+                                              prefile (&pre)[SEG]) {
+#pragma unroll
+  for (int v = 0; v < SEG; v++) pre[v] = (prefile)(0u);
+#pragma unroll 1
+  for (int k = 0; k < prog.n_inputs; k++) {
+    const bt_operand &o = prog.in[k];
+    const int64_t at = operand_matrix(o, b) * o.sb + r * o.sr + c0 * o.sc;
+    uint32_t raw[SEG];
+    if (o.dtype == BT_BF16) {
+      const uint16_t *p = (const uint16_t *)o.ptr + at;
+      if (o.sc == 1 && n == SEG && ((uintptr_t)p & 15) == 0) {
+        const uint4 w = *(const uint4 *)p;
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int v = 0; v < SEG; v++) raw[v] = ws[v / 2] >> (16 * (v & 1)) & 0xFFFFu;
+      } else if (o.sc == 0) {
+        const uint32_t x = *p;
+#pragma unroll
+        for (int v = 0; v < SEG; v++) raw[v] = x;
+      } else {
+#pragma unroll
+        for (int v = 0; v < SEG; v++) raw[v] = v < n ? p[v * o.sc] : 0u;
+      }
+    } else {
+      const uint32_t *p = (const uint32_t *)o.ptr + at;
+      if (o.sc == 1 && n == SEG && ((uintptr_t)p & 15) == 0) {
+        const uint4 w0 = *(const uint4 *)p, w1 = *(const uint4 *)(p + 4);
+        raw[0] = w0.x, raw[1] = w0.y, raw[2] = w0.z, raw[3] = w0.w;
+        raw[4] = w1.x, raw[5] = w1.y, raw[6] = w1.z, raw[7] = w1.w;
+      } else if (o.sc == 0) {
+        const uint32_t x = *p;
+#pragma unroll
+        for (int v = 0; v < SEG; v++) raw[v] = x;
+      } else {
+#pragma unroll
+        for (int v = 0; v < SEG; v++) raw[v] = v < n ? p[v * o.sc] : 0u;
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < SEG; v++) pre[v][k] = convert_raw<DT>(raw[v], o.dtype);
+  }
+}
+
+// The stored bits of a value computed in DT, for an output of dtype `dtype` (the conversions of store_value).
+template <int DT>
+__device__ __forceinline__ uint32_t stored_bits(uint32_t v, int dtype) {
+  if (dtype == BT_BF16) return bf16_packed(DT == BT_INT32 ? (float)(int32_t)v : __uint_as_float(v));
+  if (dtype == BT_FP32) return __float_as_uint(DT == BT_INT32 ? (float)(int32_t)v : __uint_as_float(v));
+  if (DT == BT_INT32) return v;
+  const float f = rintf(__uint_as_float(v));
+  return (uint32_t)(f != f ? 0 : f >= 2147483648.0f ? 2147483647 : f < -2147483648.0f ? (-2147483647 - 1) : (int32_t)f);
+}
+
+// Stores the segment's n values, with 16-byte stores when the output's columns are contiguous and aligned.
+template <int DT>
+__device__ __forceinline__ void store_segment(const bt_operand &out, int64_t b, int64_t r, int64_t c0, int n,
+                                              const uint32_t (&io)[SEG]) {
+  const int64_t at = operand_matrix(out, b) * out.sb + r * out.sr + c0 * out.sc;
+  uint32_t w[SEG];
+#pragma unroll
+  for (int v = 0; v < SEG; v++) w[v] = stored_bits<DT>(io[v], out.dtype);
+  if (out.dtype == BT_BF16) {
+    uint16_t *p = (uint16_t *)out.ptr + at;
+    if (out.sc == 1 && n == SEG && ((uintptr_t)p & 15) == 0) {
+      *(uint4 *)p = make_uint4(w[0] | w[1] << 16, w[2] | w[3] << 16, w[4] | w[5] << 16, w[6] | w[7] << 16);
+      return;
+    }
+#pragma unroll
+    for (int v = 0; v < SEG; v++)
+      if (v < n) p[v * out.sc] = (uint16_t)w[v];
+  } else {
+    uint32_t *p = (uint32_t *)out.ptr + at;
+    if (out.sc == 1 && n == SEG && ((uintptr_t)p & 15) == 0) {
+      *(uint4 *)p = make_uint4(w[0], w[1], w[2], w[3]);
+      *(uint4 *)(p + 4) = make_uint4(w[4], w[5], w[6], w[7]);
+      return;
+    }
+#pragma unroll
+    for (int v = 0; v < SEG; v++)
+      if (v < n) p[v * out.sc] = w[v];
+  }
+}
+
 // n / d for 32-bit n, with a multiplier and shift the host computed for d (the round-up method of Granlund and
 // Montgomery, "Division by invariant integers using multiplication", 1994): q = (umulhi(n, m) + n) >> s.
 struct FastDiv {

@@ -1,16 +1,24 @@
-"""Benchmark of baretile's hot path on one MI355X: the decode GEMV on block-float weights.
+"""Benchmark of baretile's hot path on one MI355X.
 
-A step is one launch of the fused matmul kernel for x [B, 576] @ W [576, 49152] with W packed as bfp4 (the headline,
-B = 1) or bfp8, fp32 accumulation and a bf16 result. Inputs are resident in HBM before timing starts. Each step reads a
-different copy of W from a pool larger than the 256 MB Infinity Cache, so every step streams its weights from HBM.
-Steps are captured into one HIP graph and replayed, and HIP events on the runtime's stream bracket the timed replay.
+The headline is the decode GEMV on block-float weights: one launch of the fused matmul kernel for
+x [B, 576] @ W [576, 49152] with W packed as bfp4 (B = 1) or bfp8, fp32 accumulation and a bf16 result. Inputs are
+resident in HBM before timing starts. Each step reads a different copy of W from a pool larger than the 256 MB
+Infinity Cache, so every step streams its weights from HBM. Steps are captured into one HIP graph and replayed, and
+HIP events on the runtime's stream bracket the timed replay. `value` is the achieved HBM bandwidth of the headline
+configuration: the algorithmic bytes of one step (packed W, x and the output) over the measured time per step. The
+other five GEMV configurations (bfp4 and bfp8 at B = 1, 4, 16) are in "configs".
 
-`value` is the achieved HBM bandwidth of the headline configuration: the algorithmic bytes of one step (packed W, x
-and the output) over the measured time per step. The other five configurations (bfp4 and bfp8 at B = 1, 4, 16) are
-reported in "configs". The CPU baseline is the NumPy restatement of the reference's path (oracle/), timed on the host
-cores on a bounded sample of the same workload.
+The other BASELINE configurations are reported beside it, each against its own roofline:
+  "c1"        config 1, relu(x @ W) with x [128, 576] and W [576, 1536] in bfp8, in one launch;
+  "attention" config 4, KV-cache attention alone: decode at 512, 4096 and 16384 keys at batch 1 and 8, and a 2048-row
+              causal prefill, 32 query and 8 key heads of 128;
+  "layer"     config 5, one Llama-3-8B-shaped block with bfp4 projections: a 2048-token prefill, then a batch-32
+              decode step against 4096 cached rows;
+  "decode"    config 3, SmolLM-135M-shaped greedy decode: tok/s, and the token streams against the NumPy oracle.
+The CPU baselines are the NumPy restatement of the reference's path (oracle/), timed on the host cores on bounded
+samples of the same workloads.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu]
 """
 import argparse, ctypes, json, os, sys, time
 from ctypes import byref, c_float, c_void_p
@@ -207,6 +215,225 @@ def decode_leg(tokens=128, prompt_len=32, check=True, replay=True):
     rt.close()
 
 
+def graph_us(rt, fn, n):
+  """us per call of fn() (launches only, no host copies) over n calls captured into one graph and replayed once."""
+  from baretile_amd import _lib
+  fn()
+  rt.wait()
+  graph = c_void_p()
+  _lib.call("graph_begin", rt.handle)
+  for _ in range(n): fn()
+  _lib.call("graph_end", rt.handle, byref(graph))
+  _lib.call("graph_launch", rt.handle, graph)
+  rt.wait()
+  start, end = c_void_p(), c_void_p()
+  _lib.call("event_create", rt.handle, byref(start))
+  _lib.call("event_create", rt.handle, byref(end))
+  _lib.call("event_record", rt.handle, start)
+  _lib.call("graph_launch", rt.handle, graph)
+  _lib.call("event_record", rt.handle, end)
+  ms = c_float()
+  _lib.call("event_elapsed", start, end, byref(ms))
+  rt.wait()
+  for h in (start, end): _lib.call("event_destroy", h)
+  _lib.call("graph_destroy", graph)
+  return ms.value * 1000 / n
+
+
+def bf16_bits(a):
+  b = np.asarray(a, np.float32).view(np.uint32).astype(np.uint64)
+  return ((b + 0x7FFF + (b >> 16 & 1)) >> 16).astype(np.uint16)
+
+
+def c1_leg(cpu_seconds, check=True):
+  """relu(x @ W), x bf16 [128, 576] N(0, 1), W [576, 1536] N(0, 0.02) in bfp8 (seed 0), in one
+  launch of the fused kernel. Roofline: intensity 153 flop/byte is below MI355X's ridge, so the bound is HBM bytes
+  (1,480,704 per call), though the 1.48 MB stay in cache."""
+  from baretile_amd import _lib
+  from baretile_amd.program import Program
+  from baretile_amd.runtime import Runtime
+  from oracle import bfp as B, ops
+  m, k, n = 128, 576, 1536
+  rng = np.random.default_rng(0)
+  x, w = rng.normal(0, 1, (m, k)).astype(np.float32), rng.normal(0, 0.02, (k, n)).astype(np.float32)
+  rt = Runtime()
+  try:
+    dx, dw = rt.dram_alloc(m * k * 2), rt.dram_alloc(k * n * 2)
+    rt.upload(dx, bf16_bits(x).tobytes())
+    rt.upload(dw, bf16_bits(w).tobytes())
+    exps, vals, cols = rt.dram_alloc(k * n // 16), rt.dram_alloc(k * n), rt.dram_alloc((k // 64) * (n // 16) * 1088)
+    rt.run("pack", "bfp_pack", _lib.BFP8, dw, _lib.BF16, 1, k, n, k * n, n, 1, exps, vals)
+    rt.run("columns", "bfp_columns", _lib.BFP8, exps, vals, 1, k, n, cols)
+    out = rt.dram_alloc(m * n * 2)
+    p = Program("bf16", epilogue=True)
+    prog = p.build(p.op("relu", p.value()))
+    a, o = _lib.operand(dx, "bf16", m * k, k, 1), _lib.operand(out, "bf16", m * n, n, 1)
+    us = graph_us(rt, lambda: _lib.call("matmul", rt.handle, byref(a), _lib.BFP8, cols, 1, 1, m, k, n, byref(prog),
+                                        byref(o)), 200)
+    got = (np.frombuffer(bytes(rt.download(out, m * n * 2)), np.uint16).astype(np.uint32) << 16).view(np.float32)
+    got = got.reshape(m, n)
+  finally:
+    rt.close()
+  flops, nbytes = 2 * m * k * n, m * k * 2 + (k // 64) * (n // 16) * 1088 + m * n * 2
+  res = {"us": round(us, 3), "TFLOP/s": round(flops / us / 1e6, 2), "GB/s": round(nbytes / us / 1e3, 1),
+         "roofline": {"bound": "hbm", "achieved": round(nbytes / us / 1e3, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                      "frac": round(nbytes / us / 1e3 / PEAK_GBS, 4)}, "flops": flops, "bytes": nbytes}
+  xw, wq = B.bf16(x), B.bfp(w, "bfp8")
+  want = ops.matmul(xw, wq)
+  res["parity"] = bool(np.all(np.abs(got - np.maximum(want, 0)) <= ops.matmul_bound(xw, wq)))
+  cpu = None
+  if check:
+    xf, wf = xw.astype(np.float32), wq.astype(np.float32)
+    np.maximum(xf @ wf, 0)
+    t0, reps = time.perf_counter(), 0
+    while time.perf_counter() - t0 < cpu_seconds:
+      np.maximum(xf @ wf, 0)
+      reps += 1
+    per = (time.perf_counter() - t0) / reps
+    cpu = {"value": round(flops / per / 1e12, 4), "unit": "TFLOP/s", "cores": blas_threads()[0], "kind": "port",
+           "sample": f"{reps} calls of np.maximum(x @ Wq, 0) in float32 with Wq the bfp8 values, {per * 1e6:.0f} us each"}
+  return res, cpu
+
+
+def attention_leg(check=True):
+  """bf16 q, k, v N(0, 1), 32 query heads over 8 key heads of 128 (batch entries fold into heads),
+  fp32 softmax, bf16 out. Decode: 1 query row against 512, 4096 and 16384 keys at batch 1 and 8, HBM-bound (bytes:
+  K and V, 4096 per key per batch entry, plus q and out). Prefill: 2048 causal rows at batch 1, matrix-core bound
+  (flops of the visible pairs: 4 * 32 * 128 * 2048 * 2049 / 2)."""
+  from baretile_amd import _lib
+  from baretile_amd.runtime import Runtime
+  from oracle import bfp as B, ops
+  rng = np.random.default_rng(0)
+  rt = Runtime()
+  res = {}
+  try:
+    cases = [("decode", b, ctx, 1) for b in (1, 8) for ctx in (512, 4096, 16384)] + [("prefill", 1, 2048, 2048)]
+    for kind, batch, keys, rows in cases:
+      E, kvh, hd = 32 * batch, 8 * batch, 128
+      q = rng.standard_normal((E, rows, hd), dtype=np.float32) * np.float32(hd ** -0.5)
+      k = rng.standard_normal((kvh, keys, hd), dtype=np.float32)
+      v = rng.standard_normal((kvh, keys, hd), dtype=np.float32)
+      places = np.broadcast_to(np.arange(rows, dtype=np.int32) if kind == "prefill" else np.full(rows, keys - 1, np.int32),
+                               (E, rows)).copy()
+      bufs = [rt.dram_alloc(a.size * 2) for a in (q, k, v)]
+      for d, a in zip(bufs, (q, k, v)): rt.upload(d, bf16_bits(a).tobytes())
+      dp, out = rt.dram_alloc(places.nbytes), rt.dram_alloc(E * rows * hd * 2)
+      rt.upload(dp, places.tobytes())
+      args = _lib.AttentionArgs(bufs[0], bufs[1], bufs[2], out, dp, rows * hd, hd, keys * hd, hd, keys * hd, hd,
+                                rows * hd, hd, rows, E, 4, rows, keys, hd, 0, 0, 0, 0, 0)
+      need = ctypes.c_uint64()
+      _lib.call("attention_scratch", byref(args), byref(need))
+      if need.value: args.scratch, args.scratch_bytes = rt.dram_alloc(need.value), need.value
+      us = graph_us(rt, lambda: _lib.call("attention", rt.handle, byref(args)), 50 if kind == "decode" else 10)
+      name = f"{kind}_B{batch}_ctx{keys}" if kind == "decode" else f"prefill_{rows}"
+      entry = {"us": round(us, 3)}
+      if kind == "decode":
+        nbytes = 2 * kvh * keys * hd * 2 + 2 * E * rows * hd * 2
+        entry.update({"GB/s": round(nbytes / us / 1e3, 1), "frac_hbm_peak": round(nbytes / us / 1e3 / PEAK_GBS, 4),
+                      "bytes": nbytes})
+      else:
+        flops = 4 * 32 * 128 * rows * (rows + 1) // 2
+        entry.update({"TFLOP/s": round(flops / us / 1e6, 1), "frac_mfma_peak": round(flops / us / 1e6 / 2500.0, 4),
+                      "flops": flops})
+      if check:  # key head 0 and its 4 query heads against the oracle
+        got = (np.frombuffer(bytes(rt.download(out, 4 * rows * hd * 2)), np.uint16).astype(np.uint32) << 16).view(np.float32)
+        want = ops.attention(B.bf16(q[:4]), B.bf16(k[:1]), B.bf16(v[:1]), places[:4, :, None], 0, 4)
+        entry["parity"] = bool(np.allclose(got.reshape(4, rows, hd), want, rtol=0.011, atol=0.011))
+      res[name] = entry
+      log("attention", name, entry)
+      rt.wait()
+      for d in bufs + [dp, out]: rt.dram_free(d)
+      if need.value: rt.dram_free(args.scratch)
+  finally:
+    rt.close()
+  cpu = None
+  if check:  # the oracle's decode at 4096 keys, batch 1, one query row per head
+    q = rng.standard_normal((32, 1, 128)).astype(np.float32)
+    k, v = rng.standard_normal((8, 4096, 128)).astype(np.float32), rng.standard_normal((8, 4096, 128)).astype(np.float32)
+    pl = np.full((32, 1, 1), 4095)
+    t0, reps = time.perf_counter(), 0
+    while time.perf_counter() - t0 < 3.0 or reps < 2:
+      ops.attention(q, k, v, pl, 0, 4)
+      reps += 1
+    per = (time.perf_counter() - t0) / reps
+    nbytes = 2 * 8 * 4096 * 128 * 2 + 2 * 32 * 128 * 2
+    cpu = {"value": round(nbytes / per / 1e9, 3), "unit": "GB/s", "cores": blas_threads()[0], "kind": "port",
+           "sample": f"{reps} calls of the oracle's attention (NumPy float64) at decode, 4096 keys, batch 1: "
+           f"{per * 1e3:.1f} ms each"}
+  return res, cpu
+
+
+def layer_leg(check=True):
+  """one Llama-3-8B-shaped block (4096 wide, 32 query and 8 key heads of 128, SwiGLU 14336) with
+  every projection N(0, 0.02) in bfp4 and bf16 norms: a 2048-token prefill from position 0 (matrix-core bound;
+  flops 2 * 2048 * 218,103,808 for the projections plus the causal attention), then one batch-32 decode step, each
+  slot at position 4095 of its own 4096-row bf16 cache (HBM-bound: the 122,683,392 bytes of bfp4 weights plus
+  32 * 4096 * 8 * 128 * 2 * 2 bytes of K and V)."""
+  from baretile_amd.models import llama
+  from baretile_amd.runtime import Runtime
+  from baretile_amd.tensor import Tensor
+  dim, heads, kv, hd, ffn, size, tokens, slots = 4096, 32, 8, 128, 14336, 4096, 2048, 32
+  rng = np.random.default_rng(0)
+  rt = Runtime()
+  res = {}
+  try:
+    c = llama.model(dim=dim, heads=heads, kv=kv, layers=1, eps=1e-5, theta=500000.0, ffn=ffn, head_dim=hd)
+    c.precision = {(op, 0): ("bfp4", 4) for op in ("qkv", "o", "gate_up", "down")}
+    shapes = {"qkv_proj": (dim, (heads + 2 * kv) * hd), "o_proj": (heads * hd, dim), "gate_up_proj": (dim, 2 * ffn),
+              "down_proj": (ffn, dim)}
+    w = {}
+    for name, shape in shapes.items():
+      w[f"layers.0.{name}"] = Tensor.of(rt, rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)).cast("bfp4").columns()
+    for name in ("input_layernorm", "post_attention_layernorm"):
+      w[f"layers.0.{name}"] = Tensor.of(rt, rng.normal(1, 0.1, (1, dim)).astype(np.float32))
+    cos, sin, turn = llama.rotary(c, size)
+    w["cos"], w["sin"], w["turn"] = Tensor.of(rt, cos), Tensor.of(rt, sin), Tensor.of(rt, turn).columns()
+    p = llama.block(w, 0)
+    wbytes = sum(shape[0] * shape[1] for shape in shapes.values()) * 576 // 1024
+    # prefill
+    x = Tensor.of(rt, rng.standard_normal((1, tokens, dim), dtype=np.float32), "fp32")
+    cache = Tensor.zeros(rt, size, hd, batch=2 * kv)
+    places = Tensor.of(rt, [list(range(tokens))], "int32")
+    rot = (w["cos"].gather(places), w["sin"].gather(places), w["turn"])
+    column = places.reshape(1, tokens, 1)
+    run = lambda: llama.layer(x, p, c, rot, column, cache, places)
+    run().realize()
+    rt.wait()
+    reps, t0 = 5, time.perf_counter()
+    for _ in range(reps): y = run()
+    rt.wait()
+    us = (time.perf_counter() - t0) / reps * 1e6
+    flops = 2 * tokens * sum(a * b for a, b in shapes.values()) + 4 * heads * hd * tokens * (tokens + 1) // 2
+    res["prefill_2048"] = {"us": round(us, 1), "TFLOP/s": round(flops / us / 1e6, 1),
+                           "frac_mfma_peak": round(flops / us / 1e6 / 2500.0, 4), "flops": flops,
+                           "finite": bool(np.isfinite(np.frombuffer(y.tobytes(), np.float32)).all())}
+    log("layer prefill", res["prefill_2048"])
+    del y, cache
+    # batch-32 decode at position 4095 of each slot's cache
+    keys = Tensor.of(rt, rng.standard_normal((slots * kv, size, hd), dtype=np.float32))
+    values = Tensor.of(rt, rng.standard_normal((slots * kv, size, hd), dtype=np.float32))
+    xs = Tensor.of(rt, rng.standard_normal((1, slots, dim), dtype=np.float32), "fp32")
+    at = Tensor.of(rt, [[size - 1] * slots], "int32")
+    rot = (w["cos"].gather(at), w["sin"].gather(at), w["turn"])
+    place = Tensor.of(rt, [[size - 1]], "int32")
+    step = lambda: llama.slots_layer(xs, p, c, rot, keys, values, place)
+    step().realize()
+    rt.wait()
+    reps, t0 = 20, time.perf_counter()
+    for _ in range(reps): y = step()
+    rt.wait()
+    us = (time.perf_counter() - t0) / reps * 1e6
+    nbytes = wbytes + slots * size * kv * hd * 2 * 2
+    res["decode_B32_ctx4096"] = {"us": round(us, 1), "GB/s": round(nbytes / us / 1e3, 1),
+                                 "frac_hbm_peak": round(nbytes / us / 1e3 / PEAK_GBS, 4), "bytes": nbytes,
+                                 "tok/s": round(slots / us * 1e6, 1),
+                                 "finite": bool(np.isfinite(np.frombuffer(y.tobytes(), np.float32)).all())}
+    log("layer decode", res["decode_B32_ctx4096"])
+  finally:
+    rt.close()
+  return res
+
+
 def blas_threads():
   try:
     from threadpoolctl import threadpool_info
@@ -224,7 +451,8 @@ def main():
   ap.add_argument("--warmup", type=int, default=400)
   ap.add_argument("--cpu-seconds", type=float, default=10.0)
   ap.add_argument("--no-cpu", action="store_true")
-  ap.add_argument("--only", default=None, help="time one configuration, e.g. bfp4_B1 or decode (for profiling runs)")
+  ap.add_argument("--only", default=None,
+                  help="one part: a GEMV configuration (bfp4_B1 ...), gemv, c1, attention, layer or decode")
   ap.add_argument("--no-decode", action="store_true", help="skip the SmolLM decode (BASELINE config 3)")
   ap.add_argument("--eager", action="store_true", help="decode without graph replay (for kernel-trace profiles)")
   args = ap.parse_args()
@@ -235,7 +463,7 @@ def main():
   configs = {}
   for fmt in ("bfp4", "bfp8"):
     for rows in (1, 4, 16):
-      if args.only and args.only != f"{fmt}_B{rows}": continue
+      if args.only and args.only != f"{fmt}_B{rows}" and args.only != "gemv": continue
       steps = args.steps if (fmt, rows) == ("bfp4", 1) else max(50, args.steps // 4)
       us, got, x, w, read_us = gpu_leg(fmt, rows, steps, args.warmup if (fmt, rows) == ("bfp4", 1) else steps)
       ok = check(got, x, w, fmt)
@@ -247,13 +475,20 @@ def main():
                                    "stream_read_us": round(read_us, 3), "stream_read_GB/s": round(wb / read_us / 1e3, 1),
                                    "frac_of_stream_read": round(read_us / us, 4)}
       log(fmt, rows, configs[f"{fmt}_B{rows}"])
-  decode, decode_cpu = None, None
+  extra = {}
+  if args.only in (None, "c1"):
+    extra["c1"], extra["c1_cpu_baseline"] = c1_leg(min(args.cpu_seconds, 5.0), check=not args.no_cpu)
+    log("c1", extra["c1"])
+  if args.only in (None, "attention"):
+    extra["attention"], extra["attention_cpu_baseline"] = attention_leg(check=not args.no_cpu)
+  if args.only in (None, "layer"):
+    extra["layer"] = layer_leg(check=not args.no_cpu)
   if not args.no_decode and args.only in (None, "decode"):
-    decode, decode_cpu = decode_leg(check=not args.no_cpu, replay=not args.eager)
-    log("decode", decode)
-    if args.only == "decode":
-      print(json.dumps({"decode": decode, "decode_cpu_baseline": decode_cpu}), flush=True)
-      return
+    extra["decode"], extra["decode_cpu_baseline"] = decode_leg(check=not args.no_cpu, replay=not args.eager)
+    log("decode", extra["decode"])
+  if args.only in ("c1", "attention", "layer", "decode"):
+    print(json.dumps(extra), flush=True)
+    return
   head = configs.get("bfp4_B1") or next(iter(configs.values()))
   cpu = None
   if not args.no_cpu:
@@ -273,7 +508,7 @@ def main():
                  "frac": head["frac_hbm_peak"], "traffic": measured_traffic()},
     "cpu_baseline": cpu,
     "configs": configs,
-    "decode": decode, "decode_cpu_baseline": decode_cpu,
+    **extra,
   }
   print(json.dumps(line), flush=True)
 

@@ -407,3 +407,22 @@ def test_gather_and_put(rt):
   want = cache.copy()
   for i, p in enumerate(places): want[:, p] = x[:, i]
   assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("n", [2048, 9000])
+def test_put_many_rows_later_duplicate_wins(rt, n):
+  # a prefill's worth of rows (the parallel path) and more (the ordered path), with repeats and places outside the
+  # cache, in fp32 and with row pieces too narrow for 16-byte moves
+  rng = np.random.default_rng(n)
+  for dtype, cols, np_t in ((_lib.BF16, 64, np.uint16), (_lib.FP32, 6, np.float32)):
+    size = n // 2
+    cache = np.zeros((3, size, cols), np_t)
+    dc = up(rt, cache)
+    x = (B.bf16_bits(rng.normal(0, 1, (3, n, cols))) if np_t is np.uint16
+         else rng.normal(0, 1, (3, n, cols)).astype(np.float32))
+    places = rng.integers(-3, size + 3, n).astype(np.int32)
+    rt.run("put", "put", dtype, dc, 3, size, cols, size * cols, cols, up(rt, places), n, up(rt, x), n * cols, cols)
+    want = cache.copy()
+    for i, p in enumerate(places):
+      if 0 <= p < size: want[:, p] = x[:, i]
+    assert np.array_equal(down(rt, dc, (3, size, cols), np_t), want), (dtype, n)

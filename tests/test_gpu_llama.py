@@ -5,7 +5,7 @@ import pytest
 
 from baretile_amd.models import llama
 from baretile_amd.tensor import Tensor
-from oracle import llama_ref as L
+from oracle import bfp as B, llama_ref as L
 
 pytestmark = pytest.mark.gpu
 
@@ -66,3 +66,41 @@ def test_jit_decode_matches_eager(rt):
     b.append(llama.argmax(logits))
     logits = llama.forward(Tensor.of(rt, [[b[-1]]], "int32"), Tensor.of(rt, [[len(prompt) + s]], "int32"), dw, dc, caches)
   assert a == b
+
+
+def test_slots_layer_matches_each_slot_in_numpy(rt):
+  # batched decode (llama.py:293-354 with slots): S slots, each with its own cache holding `place` earlier rows, one
+  # new token each; each slot's row equals the NumPy block run on that slot alone, within the block tolerance
+  rng = np.random.default_rng(7)
+  S, size, place, dim, heads, kv, hd, ffn = 3, 96, 40, 256, 4, 2, 64, 512
+  c = L.model(dim=dim, heads=heads, kv=kv, layers=1, eps=1e-5, theta=10000.0, vocab=None, ffn=ffn, head_dim=hd)
+  bf = lambda a: B.bf16(np.asarray(a, np.float32))
+  w = {"layers.0.input_layernorm": bf(rng.normal(1, 0.1, (1, dim))),
+       "layers.0.post_attention_layernorm": bf(rng.normal(1, 0.1, (1, dim))),
+       "layers.0.qkv_proj": bf(rng.normal(0, 0.02, (dim, (heads + 2 * kv) * hd))),
+       "layers.0.o_proj": bf(rng.normal(0, 0.02, (heads * hd, dim))),
+       "layers.0.gate_up_proj": bf(rng.normal(0, 0.02, (dim, 2 * ffn))),
+       "layers.0.down_proj": bf(rng.normal(0, 0.02, (ffn, dim))),
+       "norm": bf(rng.normal(1, 0.1, (1, dim))), "embed": bf(rng.normal(0, 1, (64, dim)))}
+  ref = L.arrays(w, L.precision(c, "bfp8"))
+  ref["cos"], ref["sin"], ref["turn"] = L.rotary(c, size)
+  dc = llama.model(dim=dim, heads=heads, kv=kv, layers=1, eps=1e-5, theta=10000.0, ffn=ffn, head_dim=hd,
+                   precision=llama.precision(llama.model(layers=1, dim=dim), "bfp8"))
+  dw = llama.upload(rt, w, dc, places=size)
+  K, V = (bf(rng.normal(0, 1, (S * kv, size, hd))) for _ in range(2))
+  K[:, place:], V[:, place:] = 0, 0
+  x = rng.normal(0, 1, (S, dim)).astype(np.float32)
+  rows = Tensor.of(rt, [[place] * S], "int32")
+  rot = (dw["cos"].gather(rows), dw["sin"].gather(rows), dw["turn"])
+  keys, values = Tensor.of(rt, K), Tensor.of(rt, V)
+  got = np.array(llama.slots_layer(Tensor.of(rt, x[None], "fp32"), llama.block(dw, 0), dc, rot, keys, values,
+                                   Tensor.of(rt, [[place]], "int32")).tolist()).reshape(S, dim)
+  mask = np.where(np.arange(size) > place, np.float32(-1e9), np.float32(0))[None]
+  for s in range(S):
+    cache = np.concatenate([K[s * kv:(s + 1) * kv], V[s * kv:(s + 1) * kv]]).astype(np.float64)
+    want = L.layer(x[s:s + 1], L.block(ref, 0), c, (ref["cos"][[place]], ref["sin"][[place]], ref["turn"]), mask,
+                   cache, [place])[0]
+    assert np.abs(got[s] - want).max() <= 0.03 * np.abs(want - x[s]).max(), (s, np.abs(got[s] - want).max())
+  # the new keys landed in each slot's rows of the caches
+  new_k = np.array(keys.tolist()).reshape(S * kv, size, hd)[:, place]
+  assert np.abs(new_k).max() > 0
