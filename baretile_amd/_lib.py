@@ -46,7 +46,7 @@ class AttentionArgs(ctypes.Structure):
               ("v_sr", c_int64), ("o_sh", c_int64), ("o_sr", c_int64), ("places_sh", c_int64),
               ("heads", c_int32), ("rep", c_int32), ("rows", c_int32), ("keys", c_int32), ("head_dim", c_int32),
               ("window", c_int32), ("parts", c_int32), ("pad_", c_int32), ("scratch", c_uint64),
-              ("scratch_bytes", c_uint64)]
+              ("scratch_bytes", c_uint64), ("firsts", c_uint64), ("firsts_sh", c_int64)]
 
 
 RT = c_void_p
@@ -72,6 +72,7 @@ SIGNATURES = {
   "bt_attention_scratch": [POINTER(AttentionArgs), POINTER(c_uint64)],
   "bt_gather": [RT, c_int, U64, I64, I64, I64, U64, I64, U64, I64],
   "bt_put": [RT, c_int, U64, I64, I64, I64, I64, I64, U64, I64, U64, I64, I64],
+  "bt_topk": [RT, c_int, U64, I64, I64, I64, I64, I64, c_int32, c_int32, U64, I64, I64, U64, U64],
 }
 
 _lib = None

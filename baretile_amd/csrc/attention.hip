@@ -16,9 +16,9 @@
 // values are keys {4g..4g+3} of the step's first tile and {16+4g..16+4g+3} of its second (g = l/16), and the value
 // operand is read from LDS in that same key order.
 //
-// Decode (at most 16 pairs per key head): the block's 4 waves split the keys of one tile, 64 at a time, and combine
-// their running sums in LDS at the end. Long caches are split further into parts, written as fp32 partial sums to
-// scratch and combined by a second kernel. Prefill: the block's waves take 4 consecutive tiles and share each block
+// Decode (at most 4 tiles, 64 pairs, per key head): the block's 4 waves split the keys of one tile, 64 at a time, and
+// combine their running sums in LDS at the end. Long caches are split further into parts, each a run of the tile's
+// visible keys, written as fp32 partial sums to scratch and combined by a second kernel. Prefill: the block's waves take 4 consecutive tiles and share each block
 // of 64 keys and values through LDS, double-buffered.
 #include "common.h"
 #include <algorithm>
@@ -59,6 +59,7 @@ __device__ __forceinline__ Pair pair_of(const bt_attention_args &a, int kvh, int
   const int pp = x.valid ? p : 0, h = pp % a.rep, r = pp / a.rep, e = kvh * a.rep + h;
   const int place = ((const int32_t *)a.places)[(int64_t)e * a.places_sh + r];
   x.lo = a.window > 0 ? max(0, place - a.window + 1) : 0;
+  if (a.firsts) x.lo = max(x.lo, ((const int32_t *)a.firsts)[(int64_t)e * a.firsts_sh + r]);
   x.hi = min(place, a.keys - 1);
   if (!x.valid) x.lo = 1, x.hi = 0;
   x.q = (int64_t)e * a.q_sh + (int64_t)r * a.q_sr;
@@ -217,10 +218,11 @@ __device__ __forceinline__ void store_state(float *ws, const State<HD> &st, int 
     for (int i = 0; i < 4; i++) ws[32 + (4 * g + i) * HD + 16 * c + n] = st.o[c][i];
 }
 
-// Decode: block (kvh, t, part); the 4 waves take the part's 64-key blocks in turn.
+// Decode: block (kvh, t, part). The tile's visible keys, from its smallest first to its largest last, are cut into
+// `parts` runs of whole 64-key blocks; the 4 waves take the part's blocks in turn.
 template <int HD>
 __global__ void __launch_bounds__(256) attention_decode_kernel(const bt_attention_args a, int tiles, int parts,
-                                                               int kpp, float *scratch) {
+                                                               float *scratch) {
   constexpr int VS = HD + 8, VR = KB * VS;  // halfwords of one wave's value block
   constexpr int PF = partial_floats<HD>();
   static_assert(4 * PF * 4 <= 4 * VR * 2, "the wave partials fit in the value blocks' LDS");
@@ -236,7 +238,8 @@ __global__ void __launch_bounds__(256) attention_decode_kernel(const bt_attentio
   load_q<HD>(a, pr, lane, qf);
   int lo, hi;
   tile_range(pr, lo, hi);
-  const int first = max(part * kpp, lo & ~(KB - 1)), last = min(min((part + 1) * kpp, a.keys) - 1, hi);
+  const int start = lo & ~(KB - 1), nblk = hi >= lo ? (hi - start) / KB + 1 : 0, per = (nblk + parts - 1) / parts;
+  const int first = start + part * per * KB, last = min(first + per * KB - 1, hi);
   State<HD> st;
   st.m = -__builtin_inff(), st.l = 0.0f;
 #pragma unroll
@@ -404,17 +407,17 @@ static int plan_attention(const bt_attention_args *a, AttnPlan *p) {
   if (a->places_sh != 0 && a->places_sh != a->rows) return fail(BT_EINVAL, "places' head stride is 0 or rows");
   if (((int64_t)(a->keys - 1) * std::max(a->k_sr, a->v_sr) + a->head_dim) * 2 >= (1ll << 32))
     return fail(BT_EINVAL, "a key head's rows must span less than 4 GiB");
+  if (a->firsts && a->firsts % 4) return fail(BT_EINVAL, "attention's firsts must be int32-aligned");
+  if (a->firsts && a->firsts_sh != 0 && a->firsts_sh != a->rows) return fail(BT_EINVAL, "firsts' head stride is 0 or rows");
   const int kvh = a->heads / a->rep, np = a->rep * a->rows;
   p->tiles = (np + 15) / 16;
-  p->decode = p->tiles == 1;
-  p->parts = 1, p->kpp = ((a->keys + KB - 1) / KB) * KB, p->scratch_bytes = 0;
+  p->decode = p->tiles <= 4;  // few query rows for each key head: split the keys instead
+  p->parts = 1, p->kpp = 0, p->scratch_bytes = 0;
   if (p->decode) {
     const int nblk = (a->keys + KB - 1) / KB;
     int parts = a->parts;
-    if (parts == 0) parts = std::min((2048 + kvh - 1) / kvh, (nblk + 3) / 4);
-    parts = std::max(1, std::min(parts, nblk));
-    p->kpp = ((nblk + parts - 1) / parts) * KB;
-    p->parts = (a->keys + p->kpp - 1) / p->kpp;
+    if (parts == 0) parts = std::min((2048 + kvh * p->tiles - 1) / (kvh * p->tiles), (nblk + 3) / 4);
+    p->parts = std::max(1, std::min(parts, nblk));
     const int pf = 32 + 16 * a->head_dim;
     if (p->parts > 1) p->scratch_bytes = (uint64_t)kvh * p->tiles * p->parts * pf * 4;
   }
@@ -447,8 +450,8 @@ int bt_attention(bt_runtime *rt, const bt_attention_args *a) {
   float *scratch = (float *)(uintptr_t)a->scratch;
   if (p.decode) {
     const unsigned blocks = (unsigned)(kvh * p.tiles * p.parts);
-    if (a->head_dim == 64) attention_decode_kernel<64><<<blocks, 256, 0, r->stream>>>(*a, p.tiles, p.parts, p.kpp, scratch);
-    else attention_decode_kernel<128><<<blocks, 256, 0, r->stream>>>(*a, p.tiles, p.parts, p.kpp, scratch);
+    if (a->head_dim == 64) attention_decode_kernel<64><<<blocks, 256, 0, r->stream>>>(*a, p.tiles, p.parts, scratch);
+    else attention_decode_kernel<128><<<blocks, 256, 0, r->stream>>>(*a, p.tiles, p.parts, scratch);
     BT_LAUNCHED("attention");
     if (p.parts > 1) {
       const unsigned cb = (unsigned)(kvh * p.tiles);

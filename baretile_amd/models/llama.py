@@ -139,16 +139,17 @@ def rope(x, cos, sin, turn):
   return x * cos + (x @ turn) * sin
 
 
-def attention(h, p, c, rot, places, cache, rows):
+def attention(h, p, c, rot, places, cache, rows, firsts=None):
   """One block's attention over its cache (llama.py:132-172): qkv, RoPE written straight into the heads' row layout,
-  the new keys and values put into the cache at rows, then one attention kernel from each token's place."""
+  the new keys and values put into the cache at rows, then one attention kernel from each token's place (and, with
+  slots, from its slot's first row)."""
   hd, rep, nh = head(c), c.heads // c.kv, c.heads + 2 * c.kv
   qkv = h.matmul(p["qkv_proj"])
   qkv = rope(qkv.split(nh), rot[0].split(nh), rot[1].split(nh), rot[2]).merge()
   heads = qkv.split(nh)
   cache.put(rows, heads[c.heads:c.heads + 2 * c.kv, :, :])
   q, k, v = heads[:c.heads, :, :], cache[:c.kv, :, :], cache[c.kv:, :, :]
-  o = q.attend(k.repeat_interleave(rep), v.repeat_interleave(rep), places)
+  o = q.attend(k.repeat_interleave(rep), v.repeat_interleave(rep), places, firsts=firsts)
   return o.merge().matmul(p["o_proj"], "fp32")
 
 
@@ -164,9 +165,9 @@ def block(w, l):
   return {k[len(pre):]: v for k, v in w.items() if k.startswith(pre)}
 
 
-def layer(x, p, c, rot, places, cache, rows):
+def layer(x, p, c, rot, places, cache, rows, firsts=None):
   """Attention, then the MLP, each after an RMSNorm and added onto the fp32 stream in its own kernel (llama.py:106-130)."""
-  x = (x + attention(rms(x, p["input_layernorm"], c), p, c, rot, places, cache, rows)).realize()
+  x = (x + attention(rms(x, p["input_layernorm"], c), p, c, rot, places, cache, rows, firsts)).realize()
   return (x + mlp(rms(x, p["post_attention_layernorm"], c), p)).realize()
 
 
@@ -188,17 +189,41 @@ def slots_layer(x, p, c, rot, keys, values, place):
   return (x + mlp(rms(x, p["post_attention_layernorm"], c), p)).realize()
 
 
-def forward(ids, places, w, c, caches, every=False):
+def starts(w, n, slots, part):
+  """The first cache row of each token's slot, for n tokens of `slots` sequences in turn, as an int32 row
+  (llama.py:320-323's firsts). Kept with the weights, so a recorded step finds it made."""
+  made = w.setdefault("starts", {})
+  if (n, slots, part) not in made:
+    made[n, slots, part] = Tensor.of(w["norm"].rt, [[i // (n // slots) * part for i in range(n)]], "int32")
+  return made[n, slots, part]
+
+
+def forward(ids, places, w, c, caches, every=False, slots=None):
   """Logits after ids (an int32 row) at places (an int32 row), updating each block's cache (llama.py:325-354):
-  the last token's, or every token's with every, in fp32."""
+  the last token's, or every token's with every, in fp32.
+
+  slots: decode that many sequences together, each with an equal run of consecutive tokens and a region of its own
+  of size / slots rows in every cache (llama.py:293-318); places count from each region's start, and the logits of
+  every token come back. A free slot's token sits at its region's last row, which is kept for it, and sees only the
+  region's first row."""
   n = ids.cols
   x = w["embed"].gather(ids).float()
   rot = (w["cos"].gather(places), w["sin"].gather(places), w["turn"])
-  column = places.reshape(1, n, 1)
+  firsts = None
+  if not slots:
+    rows, column = places, places.reshape(1, n, 1)
+  else:
+    size = caches[0].rows
+    if n % slots or size % slots: raise ValueError(f"{n} tokens and {size} cache rows don't split into {slots} slots")
+    part = size // slots
+    first = starts(w, n, slots, part)
+    rows = (places + first).realize()  # each token's cache row
+    column = (first + places * (places < part - 1)).realize().reshape(1, n, 1)  # a free slot's token: its first row
+    firsts = first.reshape(1, n, 1)
   blocks = [block(w, l) for l in range(c.layers)]
-  for l in range(c.layers): x = layer(x, blocks[l], c, rot, column, caches[l], places)
+  for l in range(c.layers): x = layer(x, blocks[l], c, rot, column, caches[l], rows, firsts)
   h = rms(x, w["norm"], c)
-  if not every and n > 1: h = h[:, n - 1:n, :]  # the last token's row
+  if not (every or slots) and n > 1: h = h[:, n - 1:n, :]  # the last token's row
   return h.matmul(w["embed.T"], "fp32")
 
 

@@ -647,9 +647,11 @@ class Tensor:
     return a._new("matmul", (a, x), (max(a.batch, x.batch), a.rows, x.cols), dtype)
 
   # ---- attention, rows in and out
-  def attend(self, k, v, places, window=0, fidelity=None, parts=None):
+  def attend(self, k, v, places, window=0, fidelity=None, parts=None, firsts=None):
     """softmax(self @ k^T + mask) @ v, with the mask from each query row's place (and window), in one kernel
-    (tensor.py:797-841). k and v may be repeat views (grouped-query attention). RoPE scales q beforehand."""
+    (tensor.py:797-841). k and v may be repeat views (grouped-query attention). RoPE scales q beforehand. firsts, an
+    int32 column like places, raises each row's first visible key: sequences that share one cache in regions of their
+    own (llama.py:293-318's slots)."""
     if len(self.shape) > 3: raise ValueError(f"attend takes three dimensions, not {self.shape}")
     if window < 0 or parts is not None and parts <= 0: raise ValueError("attention needs a nonnegative window and positive parts")
     if not (self.dtype == "bf16" and k.dtype == v.dtype == "bf16" and self.batch == k.batch == v.batch):
@@ -671,6 +673,12 @@ class Tensor:
     args = _lib.AttentionArgs(q.addr, k.addr, v.addr, out.addr, places.addr, q.sb, q.sr, k.sb, k.sr, v.sb, v.sr,
                               out.sb, out.sr, q.rows if places.batch > 1 else 0, q.batch, rep, q.rows, k.rows, q.cols,
                               window, parts or 0, 0, 0, 0)
+    if firsts is not None:
+      if not (firsts.rows == self.rows and firsts.batch in (1, self.batch) and firsts.cols == 1 and firsts.dtype == "int32"):
+        raise ValueError(f"attend needs firsts as an int32 column with a row for each query: {firsts.shape}")
+      firsts = firsts.realize()
+      if not firsts._contiguous(): firsts = firsts.contiguous()
+      args.firsts, args.firsts_sh = firsts.addr, q.rows if firsts.batch > 1 else 0
     need = ctypes.c_uint64()
     _lib.call("attention_scratch", ctypes.byref(args), ctypes.byref(need))
     scratch = None
@@ -680,6 +688,34 @@ class Tensor:
     self.rt.run("attention", "attention", ctypes.byref(args))
     del scratch
     return out
+
+  def topk(self, k, parts=1, labels=None):
+    """(values, int32 indices) of the k largest entries of each row, descending, in one kernel (tensor.py:685-706):
+    equal values keep column order (numpy's stable argsort of -x) and -0 equals 0; bf16 or fp32, k up to 64. With
+    parts, each of that many equal parts of a row gives its k, labelled by original column; topk again with those
+    labels combines the parts."""
+    k, parts = operator.index(k), operator.index(parts)
+    if k <= 0 or parts <= 0: raise ValueError("topk needs positive k and parts")
+    if labels is not None and labels.rt is not self.rt: raise ValueError("topk's labels must use the same runtime")
+    cols = self.cols // parts
+    if not (self.dtype in ("bf16", "fp32") and k <= min(cols, 64) and parts * cols == self.cols):
+      raise ValueError(f"topk needs bf16 or fp32, k up to 64 and a part's width, "
+                       f"and equal parts: {self.dtype}, k={k}, {parts} parts of {self.cols}")
+    if labels is not None and not (labels.dtype == "int32" and labels.shape == self.shape and parts == 1):
+      raise ValueError("topk's labels need int32, x's shape and parts=1")
+    x = self.realize()
+    if x.sc != 1 or x.rep != 1 or x.cyc: x = x.contiguous()
+    lab = None
+    if labels is not None:
+      lab = labels.realize()
+      if lab.sc != 1 or lab.rep != 1 or lab.cyc: lab = lab.contiguous()
+    values = Tensor(self.rt, x.rows, parts * k, batch=x.batch, dtype=x.dtype)
+    ids = Tensor(self.rt, x.rows, parts * k, batch=x.batch, dtype="int32")
+    values.lead = ids.lead = self.lead
+    self.rt.run("topk", "topk", _lib.DTYPES[x.dtype], x.addr, x.batch, x.rows, x.cols, x.sb if x.batch > 1 else 0, x.sr,
+                parts, k, lab.addr if lab is not None else 0, (lab.sb if lab.batch > 1 else 0) if lab is not None else 0,
+                lab.sr if lab is not None else 0, values.addr, ids.addr)
+    return values, ids
 
   def gather(self, ids):
     """Rows picked by ids: a Python list (bounds-checked) or an int32 row on the device (tensor.py:206-221)."""

@@ -183,7 +183,10 @@ int bt_matmul(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_t b, int64_
  * q, k, v, out are bf16 with element strides (head, row); places is int32 with a head stride of 0 or rows. No scale
  * is applied: baretile's RoPE pre-scales q (llama.py:210-216).
  *
- * parts splits a decode step's keys (at most 16 query rows per key head: rep * rows <= 16) between that many blocks,
+ * firsts, when given, raises each row's first visible key (a batch of sequences with their own regions of one cache,
+ * as the reference's slots use it, llama.py:293-318).
+ *
+ * parts splits a decode step's keys (at most 64 query rows per key head: rep * rows <= 64) between that many blocks,
  * as attention_kernel's parts does; 0 picks a count from the shape. With more than one part the blocks write fp32
  * partial sums into scratch (bt_attention_scratch gives the bytes; 16-byte aligned) and a second launch combines
  * them. Calls that share one scratch buffer must not overlap. */
@@ -192,6 +195,8 @@ typedef struct {
   int64_t q_sh, q_sr, k_sh, k_sr, v_sh, v_sr, o_sh, o_sr, places_sh;
   int32_t heads, rep, rows, keys, head_dim, window, parts, pad_;
   uint64_t scratch, scratch_bytes;
+  uint64_t firsts;    /* 0, or int32 with the first key each row sees (head stride firsts_sh: 0 or rows) */
+  int64_t firsts_sh;
 } bt_attention_args;
 int bt_attention(bt_runtime *rt, const bt_attention_args *args);
 /* The scratch bytes bt_attention needs for args (0 when it runs in one part). */
@@ -206,6 +211,14 @@ int bt_gather(bt_runtime *rt, int dtype, uint64_t table, int64_t rows, int64_t c
  * skipped. dst and x share dtype (bf16, fp32, int32). */
 int bt_put(bt_runtime *rt, int dtype, uint64_t dst, int64_t batch, int64_t dst_rows, int64_t cols, int64_t dst_sb,
            int64_t dst_sr, uint64_t ids, int64_t n, uint64_t x, int64_t x_sb, int64_t x_sr);
+
+/* ---- top-k: replaces topk_kernel (Tensor.topk, tensor.py:685-706) ----------------------------------------------
+ * values[b, r, p * k + j] and ids[b, r, p * k + j]: the k largest of part p of row r (parts equal parts of cols), in
+ * descending order with equal values in column order (numpy's stable argsort of -x), -0 equal to 0. ids are columns of
+ * the whole row, or labels[b, r, column] when labels is nonzero (element strides lsb, lsr). x is bf16 or fp32 with
+ * element strides sb, sr and contiguous columns; values has x's dtype and ids is int32, both contiguous. k <= 64. */
+int bt_topk(bt_runtime *rt, int dtype, uint64_t x, int64_t batch, int64_t rows, int64_t cols, int64_t sb, int64_t sr,
+            int32_t parts, int32_t k, uint64_t labels, int64_t lsb, int64_t lsr, uint64_t values, uint64_t ids);
 
 #ifdef __cplusplus
 }

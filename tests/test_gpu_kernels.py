@@ -362,6 +362,35 @@ def test_attention_matches_oracle(rt, case):
   assert np.allclose(got, want, rtol=0.011, atol=0.011), (case, np.abs(got - want).max())
 
 
+@pytest.mark.parametrize("slots,rep,part", [(4, 3, 100), (8, 4, 256), (16, 4, 64)])
+def test_attention_firsts_keep_each_slot_in_its_region(rt, slots, rep, part):
+  # one query row per slot, the slots' caches side by side in one (kv, slots * part, hd) cache: with each row's first
+  # key at its slot's first row, every row sees only its own region (llama.py:293-318). 8 or 16 slots of 4 heads make
+  # 2 or 4 tiles of 16 query rows per key head.
+  rng = np.random.default_rng(slots * rep)
+  kvh, hd = 2, 128
+  E = kvh * rep
+  q = B.bf16(rng.normal(0, 1, (E, slots, hd)) / np.sqrt(hd))
+  k, v = (B.bf16(rng.normal(0, 1, (kvh, slots * part, hd))) for _ in range(2))
+  at = rng.integers(0, part, slots)
+  places = np.broadcast_to(np.arange(slots) * part + at, (E, slots)).astype(np.int32)
+  firsts = np.broadcast_to(np.arange(slots) * part, (E, slots)).astype(np.int32)
+  dq, dk, dv = (up(rt, B.bf16_bits(t)) for t in (q, k, v))
+  o = rt.dram_alloc(E * slots * hd * 2)
+  args = _lib.AttentionArgs(dq, dk, dv, o, up(rt, places.copy()), slots * hd, hd, slots * part * hd, hd,
+                            slots * part * hd, hd, slots * hd, hd, slots, E, rep, slots, slots * part, hd, 0, 0, 0, 0, 0,
+                            up(rt, firsts.copy()), slots)
+  need = ctypes.c_uint64()
+  _lib.call("attention_scratch", ctypes.byref(args), ctypes.byref(need))
+  if need.value: args.scratch, args.scratch_bytes = rt.dram_alloc(need.value), need.value
+  rt.run("attention", "attention", ctypes.byref(args))
+  got = bits_to_float(down(rt, o, (E, slots, hd), np.uint16))
+  for u in range(slots):
+    region = slice(u * part, (u + 1) * part)
+    want = ops.attention(q[:, u:u + 1], k[:, region], v[:, region], np.full((E, 1, 1), at[u]), 0, rep)
+    assert np.allclose(got[:, u:u + 1], want, rtol=0.011, atol=0.011), (u, np.abs(got[:, u:u + 1] - want).max())
+
+
 def test_attention_rows_without_keys_are_zero(rt):
   # a place before the first key hides every key: p is zero and so is the output (kernels.py:823-826)
   rng = np.random.default_rng(5)

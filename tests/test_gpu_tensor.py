@@ -219,3 +219,35 @@ def test_errors(rt):
   with pytest.raises(ValueError): x @ Tensor.of(rt, [[1.0, 2.0]])
   with pytest.raises(ValueError): x.cast("fp8")
   with pytest.raises(ValueError): x + Tensor.of(rt, [[1.0, 2.0, 3.0]])
+
+
+def test_topk(rt):
+  # test_kernels.py:2029-2062: the k largest of each row in the order of numpy's stable argsort of -x (the first of
+  # equals first, -0 equal to 0); bf16 rows of several widths and a batch; fp32 rows in parts, then the best of the
+  # parts by their labels
+  rng = np.random.default_rng(37)
+  for batch, rows, cols, k in ((1, 1, 128, 8), (1, 3, 16, 4), (1, 40, 40, 1), (2, 33, 256, 32), (1, 2, 49152, 64)):
+    x = rng.normal(0, 2, (batch, rows, cols))
+    x[0, -1, :3], x[0, -1, 3:] = [-0.0, 0.0, -0.0], -np.abs(x[0, -1, 3:]) - 1  # -0 and 0, equal and the largest
+    x[0, 0, 9] = x[0, 0, 3] = x[0, 0].max()  # a tie
+    x = B.bf16(x)
+    values, ids = Tensor.of(rt, x).topk(k)
+    want = np.argsort(-x, -1, kind="stable")[..., :k]
+    got_ids = np.array(ids.tolist()).reshape(batch, rows, k)
+    got_values = np.array(values.tolist()).reshape(batch, rows, k)
+    assert np.array_equal(got_ids, want), (batch, rows, cols, k)
+    assert np.array_equal(got_values, np.take_along_axis(x, want, -1)), (batch, rows, cols, k)
+  for rows, cols, parts, k in ((5, 2560, 4, 64), (40, 1024, 2, 32)):
+    x = rng.normal(0, 3, (rows, cols)).astype(np.float32)
+    x[0, 100] = x[0, cols // 2 + 3] = x[0].max() + 1  # a tie across parts
+    values, ids = Tensor.of(rt, x, "fp32").topk(k, parts)
+    w = cols // parts
+    want = np.concatenate([np.argsort(-x[:, p * w:(p + 1) * w], -1, kind="stable")[:, :k] + p * w for p in range(parts)], 1)
+    assert np.array_equal(np.array(ids.tolist()), want)
+    assert np.array_equal(np.array(values.tolist(), np.float32), np.take_along_axis(x, want, -1))
+    values, ids = values.topk(k, labels=ids)
+    want = np.argsort(-x, -1, kind="stable")[:, :k]
+    assert np.array_equal(np.array(ids.tolist()), want)
+    assert np.array_equal(np.array(values.tolist(), np.float32), np.take_along_axis(x, want, -1))
+  with pytest.raises(ValueError): Tensor.of(rt, x, "fp32").topk(65)
+  with pytest.raises(ValueError): Tensor.of(rt, x, "fp32").topk(4, parts=3)
