@@ -161,13 +161,24 @@ __device__ __forceinline__ void store_tile(const MatmulArgs &args, const f32x4 &
   const int n = run * 16 + col;
   if (n >= args.n) return;
   const int64_t obase = operand_matrix(args.out, b) * args.out.sb + (int64_t)n * args.out.sc;
+  // two loops, so the program's setup (its operands' fields, loop invariant) is hoisted only into the loop that needs
+  // it, never onto the path of a plain store
+  if (args.prog.n_inst == 0) {
+#pragma unroll 1
+    for (int i = 0; i < 4; i++) {
+      const int mm = mt * 16 + 4 * g + i;
+      if (mm >= args.m) break;
+      store_value<DT>(args.out, obase + (int64_t)mm * args.out.sr,
+                      __float_as_uint(DT == BT_BF16 ? round_packed(acc[i]) : acc[i]));
+    }
+    return;
+  }
 #pragma unroll 1
   for (int i = 0; i < 4; i++) {
     const int mm = mt * 16 + 4 * g + i;
     if (mm >= args.m) break;
     const uint32_t x = __float_as_uint(DT == BT_BF16 ? round_packed(acc[i]) : acc[i]);
-    const uint32_t y = args.prog.n_inst ? run_program<DT, INL>(args.prog, b, mm, n, x) : x;
-    store_value<DT>(args.out, obase + (int64_t)mm * args.out.sr, y);
+    store_value<DT>(args.out, obase + (int64_t)mm * args.out.sr, run_program<DT, INL>(args.prog, b, mm, n, x));
   }
 }
 
