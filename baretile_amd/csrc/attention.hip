@@ -281,32 +281,57 @@ __global__ void __launch_bounds__(256) attention_decode_kernel(const bt_attentio
   finish_tile<HD>(a, ws, 4, kvh, t, part, parts, tiles, scratch);
 }
 
-// Joins the parts of each tile: M = max m_p, L = sum e^(m_p - M) l_p, out = sum e^(m_p - M) O_p / L.
+// Joins the parts of each tile: M = max m_p, L = sum e^(m_p - M) l_p, out = sum e^(m_p - M) O_p / L. The block
+// first finds every pair's M, weights and L with its 16 groups of 16 threads splitting the parts (weights kept in
+// LDS), then each thread sums its output columns over the parts, loads independent of one another.
+constexpr int MAX_PARTS = 256;
 template <int HD>
 __global__ void __launch_bounds__(256) attention_combine_kernel(const bt_attention_args a, int tiles, int parts,
                                                                 const float *scratch) {
   constexpr int PF = partial_floats<HD>();
+  __shared__ float wgt[MAX_PARTS * 16];  // [part][pair]
+  __shared__ float red[16][16], mx[16], ls[16];
   const int t = blockIdx.x % tiles, kvh = blockIdx.x / tiles;
-  const int pr_i = threadIdx.x / 16, c0 = threadIdx.x % 16;
-  const Pair pr = pair_of(a, kvh, 16 * t + pr_i);
-  if (!pr.valid) return;
   const float *src = scratch + (int64_t)(kvh * tiles + t) * parts * PF;
+  const int pr = threadIdx.x & 15, grp = threadIdx.x >> 4;
   float M = -__builtin_inff();
-  for (int p = 0; p < parts; p++) M = fmaxf(M, src[p * PF + pr_i]);
-  float L = 0.0f, o[HD / 16];
+  for (int p = grp; p < parts; p += 16) M = fmaxf(M, src[p * PF + pr]);
+  red[grp][pr] = M;
+  __syncthreads();
+  if (grp == 0) {
+    for (int g = 1; g < 16; g++) M = fmaxf(M, red[g][pr]);
+    mx[pr] = M;
+  }
+  __syncthreads();
+  M = mx[pr];
+  float L = 0.0f;
+  for (int p = grp; p < parts; p += 16) {
+    const float w = M == -__builtin_inff() ? 0.0f : __expf(src[p * PF + pr] - M);
+    wgt[p * 16 + pr] = w;
+    L += w * src[p * PF + 16 + pr];
+  }
+  red[grp][pr] = L;
+  __syncthreads();
+  if (grp == 0) {
+    for (int g = 1; g < 16; g++) L += red[g][pr];
+    ls[pr] = L;
+  }
+  __syncthreads();
+  const int pi = threadIdx.x / 16, c0 = threadIdx.x % 16;
+  const Pair pair = pair_of(a, kvh, 16 * t + pi);
+  if (!pair.valid) return;
+  float o[HD / 16];
 #pragma unroll
   for (int c = 0; c < HD / 16; c++) o[c] = 0.0f;
-  if (M != -__builtin_inff()) {
-    for (int p = 0; p < parts; p++) {
-      const float *s = src + p * PF;
-      const float w = __expf(s[pr_i] - M);
-      L += w * s[16 + pr_i];
+  const float *col = src + 32 + pi * HD + c0;
+#pragma unroll 4
+  for (int p = 0; p < parts; p++) {
+    const float w = wgt[p * 16 + pi];
 #pragma unroll
-      for (int c = 0; c < HD / 16; c++) o[c] += w * s[32 + pr_i * HD + c0 + 16 * c];
-    }
+    for (int c = 0; c < HD / 16; c++) o[c] += w * col[p * PF + 16 * c];
   }
-  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  uint16_t *out = (uint16_t *)a.out + pr.o;
+  const float inv = ls[pi] > 0.0f ? 1.0f / ls[pi] : 0.0f;
+  uint16_t *out = (uint16_t *)a.out + pair.o;
 #pragma unroll
   for (int c = 0; c < HD / 16; c++) out[c0 + 16 * c] = (uint16_t)bf16_packed(o[c] * inv);
 }
@@ -417,7 +442,7 @@ static int plan_attention(const bt_attention_args *a, AttnPlan *p) {
     const int nblk = (a->keys + KB - 1) / KB;
     int parts = a->parts;
     if (parts == 0) parts = std::min((2048 + kvh * p->tiles - 1) / (kvh * p->tiles), (nblk + 3) / 4);
-    p->parts = std::max(1, std::min(parts, nblk));
+    p->parts = std::max(1, std::min(std::min(parts, nblk), MAX_PARTS));
     const int pf = 32 + 16 * a->head_dim;
     if (p->parts > 1) p->scratch_bytes = (uint64_t)kvh * p->tiles * p->parts * pf * 4;
   }
