@@ -21,14 +21,39 @@ namespace bt {
 typedef short bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// The kernel arguments. What a wave reads comes first: the shape, A and the output operand sit in the first 144
+// bytes, so they arrive in the first scalar loads; the program, which only an epilogue reads, comes last.
 struct MatmulArgs {
-  bt_operand a;
   const uint8_t *b;
   int64_t b_matrix_bytes;  // bytes of one matrix of B's tiles, or 0 when every batch entry reads matrix 0
   int32_t batch, m, k, n, chunks, nruns, mtiles;
-  bt_program prog;
+  int32_t n_inst;  // prog.n_inst
+  bt_operand a;
   bt_operand out;
+  bt_program prog;
 };
+
+// Every argument but the program, read at the start of a kernel. One statement takes them all, so their scalar loads
+// are issued together and waited for once, rather than each sunk to its first use (a kernel argument first read near
+// the end is one more trip to memory there).
+struct Head {
+  const uint8_t *b;
+  int64_t b_matrix_bytes;
+  int32_t batch, m, k, n, chunks, nruns, mtiles, n_inst;
+  bt_operand a, out;
+};
+__device__ __forceinline__ Head early_head(const MatmulArgs &args) {
+  Head h;
+  h.b = args.b, h.b_matrix_bytes = args.b_matrix_bytes;
+  h.batch = args.batch, h.m = args.m, h.k = args.k, h.n = args.n;
+  h.chunks = args.chunks, h.nruns = args.nruns, h.mtiles = args.mtiles, h.n_inst = args.n_inst;
+  h.a = args.a, h.out = args.out;
+  asm volatile("" ::"s"(h.b), "s"(h.b_matrix_bytes), "s"(h.batch), "s"(h.m), "s"(h.k), "s"(h.n), "s"(h.chunks),
+               "s"(h.nruns), "s"(h.mtiles), "s"(h.n_inst), "s"(h.a.ptr), "s"(h.a.sb), "s"(h.a.sr), "s"(h.a.sc),
+               "s"(h.a.dtype), "s"(h.a.rep), "s"(h.a.cyc), "s"(h.out.ptr), "s"(h.out.sb), "s"(h.out.sr),
+               "s"(h.out.sc), "s"(h.out.dtype), "s"(h.out.rep), "s"(h.out.cyc));
+  return h;
+}
 
 template <int FMT> struct Tile;
 template <> struct Tile<BT_BF16> { static constexpr int bytes = 2048; };
@@ -152,33 +177,38 @@ __device__ __forceinline__ void load_b(Chunk &r, const uint8_t *t, int lane) {
   }
 }
 
-constexpr int GROUP_A = 12, GROUP_B = 8;  // chunks requested together (A-side, B-side)
+constexpr int GROUP_B = 8;  // chunks requested together by the B-side kernel
 
 // The epilogue of both kernels: lane holds rows 4g .. 4g+3 of the 16 x 16 tile at (mt, run), column col.
-template <int DT, bool INL = false>
-__device__ __forceinline__ void store_tile(const MatmulArgs &args, const f32x4 &acc, int b, int mt, int run, int g,
-                                           int col) {
+// ONE: a batch of one, so the output's matrix is matrix 0. PROG: 1 runs the epilogue program, 0 stores plainly, -1
+// reads which from the arguments.
+template <int DT, bool INL = false, bool ONE = false, int PROG = -1>
+__device__ __forceinline__ void store_tile(const MatmulArgs &args, const Head &h, const f32x4 &acc, int b, int mt,
+                                           int run, int g, int col) {
   const int n = run * 16 + col;
-  if (n >= args.n) return;
-  const int64_t obase = operand_matrix(args.out, b) * args.out.sb + (int64_t)n * args.out.sc;
+  if (n >= h.n) return;
+  const bt_operand &out = h.out;
+  const int m = h.m;
+  const int64_t obase = (ONE ? 0 : operand_matrix(out, b) * out.sb) + (int64_t)n * out.sc;
   // two loops, so the program's setup (its operands' fields, loop invariant) is hoisted only into the loop that needs
   // it, never onto the path of a plain store
-  if (args.prog.n_inst == 0) {
+  if (PROG == 0 || (PROG < 0 && h.n_inst == 0)) {
 #pragma unroll 1
     for (int i = 0; i < 4; i++) {
       const int mm = mt * 16 + 4 * g + i;
-      if (mm >= args.m) break;
-      store_value<DT>(args.out, obase + (int64_t)mm * args.out.sr,
-                      __float_as_uint(DT == BT_BF16 ? round_packed(acc[i]) : acc[i]));
+      if (mm >= m) break;
+      store_value<DT>(out, obase + (int64_t)mm * out.sr, __float_as_uint(DT == BT_BF16 ? round_packed(acc[i]) : acc[i]));
     }
     return;
   }
+  if constexpr (PROG != 0) {
 #pragma unroll 1
   for (int i = 0; i < 4; i++) {
     const int mm = mt * 16 + 4 * g + i;
-    if (mm >= args.m) break;
+    if (mm >= m) break;
     const uint32_t x = __float_as_uint(DT == BT_BF16 ? round_packed(acc[i]) : acc[i]);
-    store_value<DT>(args.out, obase + (int64_t)mm * args.out.sr, run_program<DT, INL>(args.prog, b, mm, n, x));
+    store_value<DT>(out, obase + (int64_t)mm * out.sr, run_program<DT, INL>(args.prog, b, mm, n, x));
+  }
   }
 }
 
@@ -188,17 +218,27 @@ struct WavePos {
   int lane, g, col, wib, run, mt, b;
   bool valid;
 };
-__device__ __forceinline__ WavePos wave_pos(const MatmulArgs &args) {
+template <bool ONE = false> __device__ __forceinline__ WavePos wave_pos(const Head &h) {
   WavePos p;
   p.lane = threadIdx.x & 63;
   p.g = p.lane >> 4;
   p.col = p.lane & 15;
   p.wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wave = blockIdx.x * 4 + p.wib;
-  p.valid = wave < args.batch * args.mtiles * args.nruns;
-  p.run = wave % args.nruns;
-  p.mt = wave / args.nruns % args.mtiles;
-  p.b = wave / args.nruns / args.mtiles;
+  const int batch = h.batch, mtiles = h.mtiles, nruns = h.nruns;
+  if (ONE) {  // one matrix of at most 16 rows: waves are runs
+    p.valid = wave < nruns;
+    p.run = wave, p.mt = 0, p.b = 0;
+    return p;
+  }
+  p.valid = wave < batch * mtiles * nruns;
+  if (batch == 1 && mtiles == 1) {  // a single GEMV: no division
+    p.run = wave, p.mt = 0, p.b = 0;
+  } else {
+    p.run = wave % nruns;
+    p.mt = wave / nruns % mtiles;
+    p.b = wave / nruns / mtiles;
+  }
   return p;
 }
 
@@ -213,59 +253,63 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer(const void *base, uint3
 // the wave's LDS slot for the chunk. Then each lane reads its A fragments from the slot, turns its B values into bf16
 // integers (bfp8) or q * 2^-9 (bfp4), and multiplies. Lanes of rows past the last read row 0 of the slot: the matrix
 // instruction keeps output rows independent, and those rows are never stored.
-template <int FMT, int DT, int ROWS>
+//
+// The loads of a group of G chunks are issued together and unconditionally: a chunk past the last falls outside the
+// tile buffer and reads zeros without touching memory, so the compiler can count the loads and let each chunk start
+// as soon as its own have landed. Weight bytes are read once, so they are loaded non-temporal (sc1 nt), which keeps
+// them from displacing cached lines on their way. ONE: a single matrix (batch of one), without broadcast arithmetic.
+// PROG: whether the epilogue runs a program; the plain kernels carry no interpreter, so their code stays small.
+constexpr int STREAM = 18;  // cache-policy bits of a buffer load: sc1 | nt
+
+template <int FMT, int DT, int ROWS, int G, bool ONE, bool PROG>
 __global__ void __launch_bounds__(256) gemv_kernel(const MatmulArgs args) {
-  constexpr int G = GROUP_A, SLOT = ROWS * 64, TB = Tile<FMT>::bytes;  // SLOT: halfwords of one chunk's scaled x
+  constexpr int SLOT = ROWS * 64, TB = Tile<FMT>::bytes;  // SLOT: halfwords of one chunk's scaled x
   __shared__ __attribute__((aligned(16))) uint16_t lds[4][G * SLOT];
-  const WavePos p = wave_pos(args);
+  const Head h = early_head(args);
+  const WavePos p = wave_pos<ONE>(h);
   if (!p.valid) return;
-  const int lane = p.lane, g = p.g, col = p.col;
-  const int rows = min(ROWS, args.m);
+  const int lane = p.lane, g = p.g, col = p.col, chunks = h.chunks;
+  const int rows = min(ROWS, h.m);
   uint16_t *slots = lds[p.wib];
-  const uint8_t *tiles = args.b + (args.b_matrix_bytes ? p.b * args.b_matrix_bytes : 0) +
-                         (int64_t)p.run * args.chunks * TB;
-  const __amdgpu_buffer_rsrc_t tr = buffer(tiles, (uint32_t)args.chunks * TB);
-  const uint16_t *abase = (const uint16_t *)args.a.ptr + operand_matrix(args.a, p.b) * args.a.sb;
+  const uint8_t *tiles = h.b + (!ONE && h.b_matrix_bytes ? p.b * h.b_matrix_bytes : 0) + (int64_t)p.run * chunks * TB;
+  const __amdgpu_buffer_rsrc_t tr = buffer(tiles, (uint32_t)chunks * TB);
+  const uint16_t *abase = (const uint16_t *)h.a.ptr + (ONE ? 0 : operand_matrix(h.a, p.b) * h.a.sb);
   __amdgpu_buffer_rsrc_t xr[ROWS];
 #pragma unroll
   for (int m = 0; m < ROWS; m++)
-    xr[m] = buffer(abase + (int64_t)min(m, rows - 1) * args.a.sr, m < rows ? (uint32_t)args.k * 2 : 0u);
+    xr[m] = buffer(abase + (int64_t)min(m, rows - 1) * h.a.sr, m < rows ? (uint32_t)h.k * 2 : 0u);
   const int kl = exp_row(lane);
   const int frag = min(col, rows - 1) * 64 + 8 * g;
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int c0 = 0; c0 < args.chunks; c0 += G) {
+  for (int c0 = 0; c0 < chunks; c0 += G) {
     uint32_t bq[G][4], ex[G], x[G][ROWS];  // B's value bytes (bfp8: 16, bfp4: 8), exponent byte, x at the lane's k
+    uint4 bhi[G];                          // bf16 B: the second 16 bytes of the lane's 32
 #pragma unroll
     for (int i = 0; i < G; i++) {
-      const int c = c0 + i;
-      if (c < args.chunks) {
-        if (FMT == BT_BFP8 || FMT == BT_BF16) {  // block-float values start after the 64 exponent bytes
-          const int at = FMT == BT_BFP8 ? 64 + 16 * lane : 32 * lane;
-          const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, at, c * TB, 0);
-          bq[i][0] = q[0]; bq[i][1] = q[1]; bq[i][2] = q[2]; bq[i][3] = q[3];
-        } else {
-          const auto q = __builtin_amdgcn_raw_buffer_load_b64(tr, 64 + 8 * lane, c * TB, 0);
-          bq[i][0] = q[0]; bq[i][1] = q[1];
-        }
-        if (FMT != BT_BF16) ex[i] = __builtin_amdgcn_raw_buffer_load_b8(tr, lane, c * TB, 0);
-#pragma unroll
-        for (int m = 0; m < ROWS; m++) x[i][m] = __builtin_amdgcn_raw_buffer_load_b16(xr[m], 2 * (c * 64 + kl), 0, 0);
+      const uint32_t at = (uint32_t)(c0 + i) * TB;
+      if (FMT == BT_BFP8 || FMT == BT_BF16) {  // block-float values start after the 64 exponent bytes
+        const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, at + (FMT == BT_BFP8 ? 64 + 16 * lane : 32 * lane),
+                                                             0, STREAM);
+        bq[i][0] = q[0]; bq[i][1] = q[1]; bq[i][2] = q[2]; bq[i][3] = q[3];
+      } else {
+        const auto q = __builtin_amdgcn_raw_buffer_load_b64(tr, at + 64 + 8 * lane, 0, STREAM);
+        bq[i][0] = q[0]; bq[i][1] = q[1];
       }
-    }
-    uint4 bhi[G];  // bf16 B: the second 16 bytes of the lane's 32
-    if (FMT == BT_BF16) {
+      if (FMT == BT_BF16) {
+        const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 32 * lane + 16, 0, STREAM);
+        bhi[i] = make_uint4(q[0], q[1], q[2], q[3]);
+      } else {
+        ex[i] = __builtin_amdgcn_raw_buffer_load_b8(tr, at + lane, 0, STREAM);
+      }
 #pragma unroll
-      for (int i = 0; i < G; i++)
-        if (c0 + i < args.chunks) {
-          const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, 32 * lane + 16, (c0 + i) * TB, 0);
-          bhi[i] = make_uint4(q[0], q[1], q[2], q[3]);
-        }
+      for (int m = 0; m < ROWS; m++)
+        x[i][m] = __builtin_amdgcn_raw_buffer_load_b16(xr[m], 2 * ((c0 + i) * 64 + kl), 0, 0);
     }
     // chunk by chunk, in load order, so each starts as soon as its own loads have landed: the scaled x into the
     // chunk's slot, then the fragments out of it
 #pragma unroll
     for (int i = 0; i < G; i++) {
-      if (c0 + i >= args.chunks) continue;
+      if (c0 + i >= chunks) continue;
       const int d = FMT == BT_BF16 ? 0 : (int)(int8_t)(ex[i] & 255u);
 #pragma unroll
       for (int m = 0; m < ROWS; m++) {
@@ -276,7 +320,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(const MatmulArgs args) {
       __builtin_amdgcn_wave_barrier();
       bf16x8 av[2], bv[2];
 #pragma unroll
-      for (int h = 0; h < 2; h++) av[h] = *(const bf16x8 *)(slots + i * SLOT + frag + 32 * h);
+      for (int hh = 0; hh < 2; hh++) av[hh] = *(const bf16x8 *)(slots + i * SLOT + frag + 32 * hh);
       if (FMT == BT_BF16) {
         const uint4 lo = make_uint4(bq[i][0], bq[i][1], bq[i][2], bq[i][3]);
         bv[0] = *(const bf16x8 *)&lo;
@@ -293,7 +337,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(const MatmulArgs args) {
     }
     __builtin_amdgcn_wave_barrier();
   }
-  store_tile<DT>(args, acc, p.b, p.mt, p.run, g, col);
+  store_tile<DT, false, ONE, PROG ? 1 : 0>(args, h, acc, p.b, p.mt, p.run, g, col);
 }
 
 // B-side scaling, for any number of rows: each lane turns its 16 B values into bf16 q * 2^d with v_ldexp_f32 and
@@ -301,32 +345,33 @@ __global__ void __launch_bounds__(256) gemv_kernel(const MatmulArgs args) {
 template <int FMT, int DT, bool VEC>
 __global__ void __launch_bounds__(256) skinny_kernel(const MatmulArgs args) {
   constexpr int G = GROUP_B;
-  const WavePos p = wave_pos(args);
+  const Head h = early_head(args);
+  const WavePos p = wave_pos(h);
   if (!p.valid) return;
-  const int lane = p.lane, g = p.g, col = p.col;
-  const int rows = min(16, args.m - p.mt * 16);
-  const uint8_t *tiles = args.b + (args.b_matrix_bytes ? p.b * args.b_matrix_bytes : 0) +
-                         (int64_t)p.run * args.chunks * Tile<FMT>::bytes;
+  const int lane = p.lane, g = p.g, col = p.col, chunks = h.chunks;
+  const int rows = min(16, h.m - p.mt * 16);
+  const uint8_t *tiles = h.b + (h.b_matrix_bytes ? p.b * h.b_matrix_bytes : 0) +
+                         (int64_t)p.run * chunks * Tile<FMT>::bytes;
   const bool row_in = col < rows;
-  const uint16_t *arow = (const uint16_t *)args.a.ptr + operand_matrix(args.a, p.b) * args.a.sb +
-                         (int64_t)(p.mt * 16 + (row_in ? col : 0)) * args.a.sr;
+  const uint16_t *arow = (const uint16_t *)h.a.ptr + operand_matrix(h.a, p.b) * h.a.sb +
+                         (int64_t)(p.mt * 16 + (row_in ? col : 0)) * h.a.sr;
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int c0 = 0; c0 < args.chunks; c0 += G) {
+  for (int c0 = 0; c0 < chunks; c0 += G) {
     Chunk r[G];
 #pragma unroll
     for (int i = 0; i < G; i++) {
       const int c = c0 + i;
-      if (c < args.chunks) {
+      if (c < chunks) {
         const uint8_t *t = tiles + (int64_t)c * Tile<FMT>::bytes;
         load_b<FMT>(r[i], t, lane);
         if (FMT != BT_BF16) r[i].ex = gload((const uint4 *)(t + 16 * g));
-        r[i].a0 = load_a<VEC>(arow, row_in, args.a.sc, c * 64 + 8 * g, args.k);
-        r[i].a1 = load_a<VEC>(arow, row_in, args.a.sc, c * 64 + 32 + 8 * g, args.k);
+        r[i].a0 = load_a<VEC>(arow, row_in, h.a.sc, c * 64 + 8 * g, h.k);
+        r[i].a1 = load_a<VEC>(arow, row_in, h.a.sc, c * 64 + 32 + 8 * g, h.k);
       }
     }
 #pragma unroll
     for (int i = 0; i < G; i++) {
-      if (c0 + i >= args.chunks) continue;
+      if (c0 + i >= chunks) continue;
       bf16x8 av[2], bv[2];
       av[0] = *(const bf16x8 *)&r[i].a0;
       av[1] = *(const bf16x8 *)&r[i].a1;
@@ -344,7 +389,7 @@ __global__ void __launch_bounds__(256) skinny_kernel(const MatmulArgs args) {
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[1], bv[1], acc, 0, 0, 0);
     }
   }
-  store_tile<DT>(args, acc, p.b, p.mt, p.run, g, col);
+  store_tile<DT>(args, h, acc, p.b, p.mt, p.run, g, col);
 }
 
 // The end of both GEMM kernels: the block's BM x BN starting values are in LDS (row stride ES bytes, ESZ bytes each:
@@ -357,7 +402,7 @@ __device__ __forceinline__ void gemm_epilogue(const MatmulArgs &args, const uint
   const int64_t obase = operand_matrix(args.out, b) * args.out.sb;
   const int osz = args.out.dtype == BT_BF16 ? 2 : 4;
   const bool same = (DT == BT_FP32 && args.out.dtype == BT_FP32) || (DT == BT_BF16 && args.out.dtype == BT_BF16);
-  const bool direct = args.prog.n_inst == 0 && same && args.out.sc == 1 && cols == BN &&
+  const bool direct = args.n_inst == 0 && same && args.out.sc == 1 && cols == BN &&
                       (args.out.ptr + (uint64_t)(obase + (int64_t)m0 * args.out.sr + n0) * osz) % 16 == 0 &&
                       (args.out.sr * osz) % 16 == 0;
   if (direct) {
@@ -385,7 +430,7 @@ __device__ __forceinline__ void gemm_epilogue(const MatmulArgs &args, const uint
       const uint8_t *src = lds + r * ES + (c0 + v) * ESZ;
       io[v] = DT == BT_FP32 ? *(const uint32_t *)src : (uint32_t)*(const uint16_t *)src << 16;
     }
-    if (args.prog.n_inst) {
+    if (args.n_inst) {
       prefile pre[SEG];
       fetch_segment<DT>(args.prog, b, m0 + r, n0 + c0, n, pre);
       eval_program<DT, SEG>(args.prog, pre, io);
@@ -729,9 +774,27 @@ int check_out(const bt_operand *out);
 template <int FMT, int DT>
 static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bool vec) {
   const bool rows_contiguous = args.a.sc == 1 && (int64_t)args.k * 2 < (1ll << 31);
-  if (args.m == 1 && rows_contiguous) gemv_kernel<FMT, DT, 1><<<blocks, 256, 0, s>>>(args);
-  else if (args.m <= 4 && rows_contiguous) gemv_kernel<FMT, DT, 4><<<blocks, 256, 0, s>>>(args);
-  else if (vec) skinny_kernel<FMT, DT, true><<<blocks, 256, 0, s>>>(args);
+  // chunks in a group: the size that leaves the fewest unused slots in the last group, the larger on a tie
+  const int group = args.chunks % 12 == 0 ? 12 : args.chunks % 9 == 0 ? 9 : args.chunks % 8 == 0 ? 8 : 12;
+  const bool one = args.batch == 1 && args.mtiles == 1;
+  const bool fits = (int64_t)(args.chunks + 12) * Tile<FMT>::bytes < (1ll << 32);  // voffsets of the last group
+  if (args.m <= 4 && rows_contiguous && fits) {
+    // with an epilogue program: one kernel for every shape; without: the group size and a batch of one specialised
+    if (args.n_inst) {
+      if (args.m == 1) gemv_kernel<FMT, DT, 1, 12, false, true><<<blocks, 256, 0, s>>>(args);
+      else gemv_kernel<FMT, DT, 4, 12, false, true><<<blocks, 256, 0, s>>>(args);
+    } else if (args.m == 1) {
+      if (!one) gemv_kernel<FMT, DT, 1, 12, false, false><<<blocks, 256, 0, s>>>(args);
+      else if (group == 9) gemv_kernel<FMT, DT, 1, 9, true, false><<<blocks, 256, 0, s>>>(args);
+      else if (group == 8) gemv_kernel<FMT, DT, 1, 8, true, false><<<blocks, 256, 0, s>>>(args);
+      else gemv_kernel<FMT, DT, 1, 12, true, false><<<blocks, 256, 0, s>>>(args);
+    } else {
+      if (!one) gemv_kernel<FMT, DT, 4, 12, false, false><<<blocks, 256, 0, s>>>(args);
+      else if (group == 9) gemv_kernel<FMT, DT, 4, 9, true, false><<<blocks, 256, 0, s>>>(args);
+      else if (group == 8) gemv_kernel<FMT, DT, 4, 8, true, false><<<blocks, 256, 0, s>>>(args);
+      else gemv_kernel<FMT, DT, 4, 12, true, false><<<blocks, 256, 0, s>>>(args);
+    }
+  } else if (vec) skinny_kernel<FMT, DT, true><<<blocks, 256, 0, s>>>(args);
   else skinny_kernel<FMT, DT, false><<<blocks, 256, 0, s>>>(args);
 }
 
@@ -833,6 +896,7 @@ extern "C" int bt_matmul(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_
     args.prog = bt_program{};
     args.prog.dtype = out->dtype == BT_FP32 ? BT_FP32 : BT_BF16;
   }
+  args.n_inst = args.prog.n_inst;
   args.out = *out;
   if (b_fmt == BT_BF16) launch_skinny<BT_BF16>(args, r->stream);
   else if (b_fmt == BT_BFP8) launch_skinny<BT_BFP8>(args, r->stream);

@@ -48,16 +48,17 @@ __global__ void fill32_kernel(uint32_t *dst, uint32_t value, uint64_t words) {
 // Reads n16 16-byte words once each, four per thread, and folds them into a word that is written only if it equals a
 // value the data never gives: the plain streaming read that a measurement compares a kernel's HBM rate against, and the
 // known-size read that calibrates the memory counters.
-__global__ void __launch_bounds__(256) stream_read_kernel(const uint4 *__restrict__ p, uint64_t n16, uint32_t *out) {
-  const uint64_t base = (uint64_t)blockIdx.x * blockDim.x * 4 + threadIdx.x;
+__global__ void __launch_bounds__(256) stream_read_kernel(const uint8_t *p, uint32_t bytes, uint32_t *out) {
+  // 16 bytes a lane, four times, through a buffer resource whose range check drops the tail; loaded non-temporal
+  // (sc1 nt), as a stream read once is
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p), (short)0, (int)bytes,
+                                                                     0x00020000);
+  const uint32_t base = (blockIdx.x * 1024u + threadIdx.x) * 16u;
   uint32_t acc = 0;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const uint64_t j = base + (uint64_t)i * blockDim.x;
-    if (j < n16) {
-      const uint4 v = p[j];
-      acc ^= v.x ^ v.y ^ v.z ^ v.w;
-    }
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, base + i * 4096u, 0, 18);
+    acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
   }
   if (acc == 0x9E3779B9u && out) out[0] = acc;
 }
@@ -74,10 +75,11 @@ int bt_stream_read(bt_runtime *rt, uint64_t src, uint64_t bytes, uint64_t scratc
   Runtime *r;
   if (int s = enter(rt, &r)) return s;
   if (src % 16 || bytes % 16) return fail(BT_EINVAL, "stream_read takes 16-byte aligned whole words");
-  const uint64_t n16 = bytes / 16, blocks = (n16 + 1023) / 1024;
+  const uint64_t blocks = (bytes + 16383) / 16384;
   if (!blocks) return BT_OK;
-  if (blocks >= (1ull << 31)) return fail(BT_EINVAL, "stream_read of %llu bytes is too large", (unsigned long long)bytes);
-  stream_read_kernel<<<(unsigned)blocks, 256, 0, r->stream>>>((const uint4 *)(uintptr_t)src, n16,
+  if (bytes > (1ull << 32) - 16384) return fail(BT_EINVAL, "stream_read of %llu bytes: at most 4 GB - 16 KB",
+                                                (unsigned long long)bytes);
+  stream_read_kernel<<<(unsigned)blocks, 256, 0, r->stream>>>((const uint8_t *)(uintptr_t)src, (uint32_t)bytes,
                                                               (uint32_t *)(uintptr_t)scratch_word);
   BT_LAUNCHED("stream_read");
   return BT_OK;

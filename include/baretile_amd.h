@@ -53,9 +53,9 @@ int bt_fill32(bt_runtime *rt, uint64_t dst, uint32_t value, uint64_t words);
 /* Runtime.wait(timeout) (runtime.py:851-880): BT_ETIMEOUT if the stream is still busy after timeout_s seconds. */
 int bt_wait(bt_runtime *rt, double timeout_s);
 /* No counterpart in the reference (a measurement aid, like probe.py's DRAM probes, probe.py:81): reads `bytes` once
- * with 16-byte loads and folds them into a word written to scratch_word only for one unlikely value. The plain
- * streaming read that bench.py sets beside a kernel of the same size, and the known-size read that calibrates the
- * HBM byte counters. */
+ * with 16-byte non-temporal loads and folds them into a word written to scratch_word only for one unlikely value
+ * (bytes: a multiple of 16, at most 4 GB - 16 KB). The plain streaming read that bench.py sets beside a kernel of the
+ * same size, and the known-size read that calibrates the HBM byte counters. */
 int bt_stream_read(bt_runtime *rt, uint64_t src, uint64_t bytes, uint64_t scratch_word);
 /* Timing for Runtime.profile (runtime.py:773-786): events on the runtime's stream. */
 int bt_event_create(bt_runtime *rt, void **ev);
