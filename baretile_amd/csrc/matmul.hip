@@ -226,9 +226,11 @@ template <bool ONE = false> __device__ __forceinline__ WavePos wave_pos(const He
   p.wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wave = blockIdx.x * 4 + p.wib;
   const int batch = h.batch, mtiles = h.mtiles, nruns = h.nruns;
-  if (ONE) {  // one matrix of at most 16 rows: waves are runs
-    p.valid = wave < nruns;
-    p.run = wave, p.mt = 0, p.b = 0;
+  if (ONE) {  // one matrix (a batch of one): waves are runs of each 16-row tile in turn
+    p.valid = wave < mtiles * nruns;
+    p.b = 0;
+    if (mtiles == 1) p.run = wave, p.mt = 0;
+    else p.run = wave % nruns, p.mt = wave / nruns;
     return p;
   }
   p.valid = wave < batch * mtiles * nruns;
@@ -248,6 +250,44 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer(const void *base, uint3
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// The place of a wave in the decode kernels' grid. There are `units` output tiles (a 16-column run of one batch entry,
+// with one group of 16-row tiles for the skinny kernel); each is split along K into `slices` (1, 2, 4 or 8) whose
+// waves sit side by side in one block, so a deep K still gives enough waves to keep every CU's loads in flight. A
+// slice is a whole number of `step` chunks; the last slices may be short or empty.
+struct SlicePos {
+  int lane, g, col, wib, unit, s, c_begin, c_end;
+  bool valid;
+};
+__device__ __forceinline__ SlicePos slice_pos(int units, int chunks, int slices, int step) {
+  SlicePos p;
+  p.lane = threadIdx.x & 63;
+  p.g = p.lane >> 4;
+  p.col = p.lane & 15;
+  p.wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wpb = slices == 8 ? 8 : 4;  // the launch's waves a block (blockDim would be a load from the packet)
+  p.unit = blockIdx.x * (wpb / slices) + p.wib / slices;
+  p.s = p.wib % slices;
+  p.valid = p.unit < units;
+  const int per = ((chunks + slices - 1) / slices + step - 1) / step * step;
+  p.c_begin = min(chunks, p.s * per);
+  p.c_end = min(chunks, p.c_begin + per);
+  return p;
+}
+
+// Adds the partial tiles of a unit's slices into its first wave, in slice order: ((slice 0 + slice 1) + slice 2) ...
+// Every wave of the block must call it: it holds a block barrier.
+template <int MT>
+__device__ __forceinline__ void sum_slices(f32x4 (&acc)[MT], const SlicePos &p, int slices, f32x4 *red) {
+  if (p.s != 0)
+#pragma unroll
+    for (int t = 0; t < MT; t++) red[(p.wib * MT + t) * 64 + p.lane] = acc[t];
+  __syncthreads();
+  if (p.s == 0)
+    for (int j = 1; j < slices; j++)
+#pragma unroll
+      for (int t = 0; t < MT; t++) acc[t] += red[((p.wib + j) * MT + t) * 64 + p.lane];
+}
+
 // A-side scaling, for up to 4 rows of A (ROWS = 1, or 4 with absent rows read as zeros) in row-major rows. Per chunk,
 // lane l owns one k of the tile (the row of exponent byte l): it scales x at that k by the run's 2^d for each row into
 // the wave's LDS slot for the chunk. Then each lane reads its A fragments from the slot, turns its B values into bf16
@@ -261,26 +301,32 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer(const void *base, uint3
 // PROG: whether the epilogue runs a program; the plain kernels carry no interpreter, so their code stays small.
 constexpr int STREAM = 18;  // cache-policy bits of a buffer load: sc1 | nt
 
-template <int FMT, int DT, int ROWS, int G, bool ONE, bool PROG>
-__global__ void __launch_bounds__(256) gemv_kernel(const MatmulArgs args) {
+template <int FMT, int DT, int ROWS, int G, bool ONE, bool PROG, bool SL>
+__global__ void __launch_bounds__(SL ? 512 : 256) gemv_kernel(const MatmulArgs args, int slices_arg) {
   constexpr int SLOT = ROWS * 64, TB = Tile<FMT>::bytes;  // SLOT: halfwords of one chunk's scaled x
-  __shared__ __attribute__((aligned(16))) uint16_t lds[4][G * SLOT];
+  // LDS, sized at launch: each wave's slots, then (with slices) each wave's partial tile
+  extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
+  const int slices = SL ? slices_arg : 1;
   const Head h = early_head(args);
-  const WavePos p = wave_pos<ONE>(h);
-  if (!p.valid) return;
-  const int lane = p.lane, g = p.g, col = p.col, chunks = h.chunks;
+  const SlicePos p = slice_pos(h.batch * h.nruns, h.chunks, slices, G);
+  f32x4 *red = (f32x4 *)(dyn + (slices == 8 ? 8 : 4) * G * SLOT * 2);
+  if (slices == 1 && !p.valid) return;
+  const int lane = p.lane, g = p.g, col = p.col;
+  const int b = ONE ? 0 : p.unit / h.nruns, run = ONE ? p.unit : p.unit % h.nruns;
+  const int chunks = p.valid ? p.c_end - p.c_begin : 0;  // this wave's slice
   const int rows = min(ROWS, h.m);
-  uint16_t *slots = lds[p.wib];
-  const uint8_t *tiles = h.b + (!ONE && h.b_matrix_bytes ? p.b * h.b_matrix_bytes : 0) + (int64_t)p.run * chunks * TB;
+  uint16_t *slots = (uint16_t *)dyn + p.wib * G * SLOT;
+  const uint8_t *tiles = h.b + (!ONE && h.b_matrix_bytes ? b * h.b_matrix_bytes : 0) +
+                         ((int64_t)run * h.chunks + p.c_begin) * TB;
   const __amdgpu_buffer_rsrc_t tr = buffer(tiles, (uint32_t)chunks * TB);
-  const uint16_t *abase = (const uint16_t *)h.a.ptr + (ONE ? 0 : operand_matrix(h.a, p.b) * h.a.sb);
+  const uint16_t *abase = (const uint16_t *)h.a.ptr + (ONE ? 0 : operand_matrix(h.a, b) * h.a.sb) + p.c_begin * 64;
+  const uint32_t xbytes = (uint32_t)max(0, h.k - p.c_begin * 64) * 2;
   __amdgpu_buffer_rsrc_t xr[ROWS];
 #pragma unroll
-  for (int m = 0; m < ROWS; m++)
-    xr[m] = buffer(abase + (int64_t)min(m, rows - 1) * h.a.sr, m < rows ? (uint32_t)h.k * 2 : 0u);
+  for (int m = 0; m < ROWS; m++) xr[m] = buffer(abase + (int64_t)min(m, rows - 1) * h.a.sr, m < rows ? xbytes : 0u);
   const int kl = exp_row(lane);
   const int frag = min(col, rows - 1) * 64 + 8 * g;
-  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4 acc[1] = {{0.0f, 0.0f, 0.0f, 0.0f}};
   for (int c0 = 0; c0 < chunks; c0 += G) {
     uint32_t bq[G][4], ex[G], x[G][ROWS];  // B's value bytes (bfp8: 16, bfp4: 8), exponent byte, x at the lane's k
     uint4 bhi[G];                          // bf16 B: the second 16 bytes of the lane's 32
@@ -332,15 +378,131 @@ __global__ void __launch_bounds__(256) gemv_kernel(const MatmulArgs args) {
         bv[0] = q4_to_bf16(bq[i][0]);
         bv[1] = q4_to_bf16(bq[i][1]);
       }
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0], bv[0], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[1], bv[1], acc, 0, 0, 0);
+      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0], bv[0], acc[0], 0, 0, 0);
+      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[1], bv[1], acc[0], 0, 0, 0);
     }
     __builtin_amdgcn_wave_barrier();
   }
-  store_tile<DT, false, ONE, PROG ? 1 : 0>(args, h, acc, p.b, p.mt, p.run, g, col);
+  if (SL && slices > 1) sum_slices<1>(acc, p, slices, red);
+  if (p.s == 0 && p.valid) store_tile<DT, false, ONE, PROG ? 1 : 0>(args, h, acc[0], b, 0, run, g, col);
 }
 
-// B-side scaling, for any number of rows: each lane turns its 16 B values into bf16 q * 2^d with v_ldexp_f32 and
+// B-side scaling with row-major, 16-byte aligned A: each lane turns its 16 B values into bf16 q * 2^d with
+// v_ldexp_f32 and reads its A fragments straight from memory. A wave takes MT 16-row tiles of A against one run, so
+// each B value is loaded and converted once for MT tiles; the waves that share a run (more tiles than MT) are
+// neighbours in the grid, so they read it at the same time. Loads go out as in gemv_kernel: a group of G chunks
+// together and unconditionally, past the last chunk (and for rows past the last) reading zeros through the buffers'
+// ranges; the weights non-temporal when a run has a single reader.
+template <int FMT, int DT, int G, bool ONE, bool PROG, int MT, bool SL>
+__global__ void __launch_bounds__(SL ? 512 : 256) skinny_vec_kernel(const MatmulArgs args, int slices_arg) {
+  constexpr int TB = Tile<FMT>::bytes;
+  extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];  // with slices: each wave's partial tiles
+  f32x4 *red = (f32x4 *)dyn;
+  const int slices = SL ? slices_arg : 1;
+  const Head h = early_head(args);
+  const int groups = (h.mtiles + MT - 1) / MT, per = h.nruns * groups;
+  const SlicePos p = slice_pos(h.batch * per, h.chunks, slices, G);
+  if (slices == 1 && !p.valid) return;
+  const int lane = p.lane, g = p.g, col = p.col;
+  const int b = ONE ? 0 : p.unit / per, rem = ONE ? p.unit : p.unit % per;
+  const int run = groups == 1 ? rem : rem / groups, mg = groups == 1 ? 0 : rem % groups;
+  const int chunks = p.valid ? p.c_end - p.c_begin : 0;  // this wave's slice
+  const int row0 = mg * MT * 16, rows = min(MT * 16, h.m - row0);  // this wave's rows of A
+  const uint8_t *tiles = h.b + (!ONE && h.b_matrix_bytes ? b * h.b_matrix_bytes : 0) +
+                         ((int64_t)run * h.chunks + p.c_begin) * TB;
+  const __amdgpu_buffer_rsrc_t tr = buffer(tiles, (uint32_t)chunks * TB);
+  // A's rows through one (uniform) buffer: each lane's row at its byte offset, a row past the last at the end of the
+  // range, so it reads zeros
+  const uint16_t *abase = (const uint16_t *)h.a.ptr + (ONE ? 0 : operand_matrix(h.a, b) * h.a.sb) +
+                          (int64_t)row0 * h.a.sr;
+  const uint32_t abytes = (uint32_t)(((int64_t)(rows - 1) * h.a.sr + h.k) * 2);
+  const __amdgpu_buffer_rsrc_t ar = buffer(abase, abytes);
+  uint32_t arow[MT];
+#pragma unroll
+  for (int t = 0; t < MT; t++)
+    arow[t] = t * 16 + col < rows ? (uint32_t)((t * 16 + col) * h.a.sr * 2 + p.c_begin * 128) : abytes;
+  const bool alone = groups == 1;
+  f32x4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; t++) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c0 = 0; c0 < chunks; c0 += G) {
+    uint4 b0[G], b1[G], ex[G], a0[G][MT], a1[G][MT];
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      const uint32_t at = (uint32_t)(c0 + i) * TB, ak = (uint32_t)(c0 + i) * 128 + 16 * g;
+      // the cache policy is an immediate: two copies of the loads, one chosen per wave
+      if (alone) {
+        if (FMT == BT_BF16) {
+          const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 32 * lane, 0, STREAM);
+          const auto u = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 32 * lane + 16, 0, STREAM);
+          b0[i] = make_uint4(q[0], q[1], q[2], q[3]);
+          b1[i] = make_uint4(u[0], u[1], u[2], u[3]);
+        } else if (FMT == BT_BFP8) {
+          const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 64 + 16 * lane, 0, STREAM);
+          b0[i] = make_uint4(q[0], q[1], q[2], q[3]);
+        } else {
+          const auto q = __builtin_amdgcn_raw_buffer_load_b64(tr, at + 64 + 8 * lane, 0, STREAM);
+          b0[i] = make_uint4(q[0], q[1], 0, 0);
+        }
+        if (FMT != BT_BF16) {
+          const auto e = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 16 * g, 0, STREAM);
+          ex[i] = make_uint4(e[0], e[1], e[2], e[3]);
+        }
+      } else {
+        if (FMT == BT_BF16) {
+          const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 32 * lane, 0, 0);
+          const auto u = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 32 * lane + 16, 0, 0);
+          b0[i] = make_uint4(q[0], q[1], q[2], q[3]);
+          b1[i] = make_uint4(u[0], u[1], u[2], u[3]);
+        } else if (FMT == BT_BFP8) {
+          const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 64 + 16 * lane, 0, 0);
+          b0[i] = make_uint4(q[0], q[1], q[2], q[3]);
+        } else {
+          const auto q = __builtin_amdgcn_raw_buffer_load_b64(tr, at + 64 + 8 * lane, 0, 0);
+          b0[i] = make_uint4(q[0], q[1], 0, 0);
+        }
+        if (FMT != BT_BF16) {
+          const auto e = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 16 * g, 0, 0);
+          ex[i] = make_uint4(e[0], e[1], e[2], e[3]);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < MT; t++) {
+        const auto x0 = __builtin_amdgcn_raw_buffer_load_b128(ar, arow[t] + ak, 0, 0);
+        const auto x1 = __builtin_amdgcn_raw_buffer_load_b128(ar, arow[t] + ak + 64, 0, 0);
+        a0[i][t] = make_uint4(x0[0], x0[1], x0[2], x0[3]);
+        a1[i][t] = make_uint4(x1[0], x1[1], x1[2], x1[3]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      if (c0 + i >= chunks) continue;
+      bf16x8 bv[2];
+      if (FMT == BT_BF16) {
+        bv[0] = *(const bf16x8 *)&b0[i];
+        bv[1] = *(const bf16x8 *)&b1[i];
+      } else if (FMT == BT_BFP8) {
+        bv[0] = q8_to_bf16<true>(make_uint2(b0[i].x, b0[i].y), make_uint2(ex[i].x, ex[i].y));
+        bv[1] = q8_to_bf16<true>(make_uint2(b0[i].z, b0[i].w), make_uint2(ex[i].z, ex[i].w));
+      } else {
+        bv[0] = q4_to_bf16_scaled(b0[i].x, make_uint2(ex[i].x, ex[i].y));
+        bv[1] = q4_to_bf16_scaled(b0[i].y, make_uint2(ex[i].z, ex[i].w));
+      }
+#pragma unroll
+      for (int t = 0; t < MT; t++) {
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)&a0[i][t], bv[0], acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)&a1[i][t], bv[1], acc[t], 0, 0, 0);
+      }
+    }
+  }
+  if (SL && slices > 1) sum_slices<MT>(acc, p, slices, red);
+  if (p.s == 0 && p.valid)
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+      store_tile<DT, false, ONE, PROG ? 1 : 0>(args, h, acc[t], b, mg * MT + t, run, g, col);
+}
+
+// B-side scaling, for A of any strides: each lane turns its 16 B values into bf16 q * 2^d with v_ldexp_f32 and
 // reads its A fragments straight from memory.
 template <int FMT, int DT, bool VEC>
 __global__ void __launch_bounds__(256) skinny_kernel(const MatmulArgs args) {
@@ -771,28 +933,72 @@ gemm2_kernel(const MatmulArgs args, int mblocks, int nblocks) {
 int validate_program(const bt_program *prog);
 int check_out(const bt_operand *out);
 
+// Slices along K for `units` output tiles: enough that the launch has about 4096 waves, when K is deep enough to give
+// each slice at least 16 chunks (a single wave would walk a deep K one group of loads after another). K of fewer than
+// 32 chunks is never sliced: such a product sums in the same order as the GEMM.
+static int choose_slices(int64_t units, int chunks) {
+  int sl = 1;
+  while (sl < 8 && units * sl < 4096 && chunks >= 32 * sl) sl *= 2;
+  return sl;
+}
+
+template <class Kernel>
+static void launch_sliced(Kernel kernel, const MatmulArgs &args, int64_t units, int slices, int slot_bytes,
+                          int tile_bytes, hipStream_t s) {
+  const int wpb = slices == 8 ? 8 : 4;
+  const unsigned blocks = (unsigned)((units * slices + wpb - 1) / wpb);
+  const size_t lds = (size_t)wpb * slot_bytes + (slices > 1 ? (size_t)wpb * tile_bytes : 0);
+  kernel<<<blocks, wpb * 64, lds, s>>>(args, slices);
+}
+
 template <int FMT, int DT>
 static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bool vec) {
   const bool rows_contiguous = args.a.sc == 1 && (int64_t)args.k * 2 < (1ll << 31);
+  const bool fits = (int64_t)(args.chunks + 12) * Tile<FMT>::bytes < (1ll << 32);  // voffsets of the last group
   // chunks in a group: the size that leaves the fewest unused slots in the last group, the larger on a tie
   const int group = args.chunks % 12 == 0 ? 12 : args.chunks % 9 == 0 ? 9 : args.chunks % 8 == 0 ? 8 : 12;
-  const bool one = args.batch == 1 && args.mtiles == 1;
-  const bool fits = (int64_t)(args.chunks + 12) * Tile<FMT>::bytes < (1ll << 32);  // voffsets of the last group
   if (args.m <= 4 && rows_contiguous && fits) {
-    // with an epilogue program: one kernel for every shape; without: the group size and a batch of one specialised
-    if (args.n_inst) {
-      if (args.m == 1) gemv_kernel<FMT, DT, 1, 12, false, true><<<blocks, 256, 0, s>>>(args);
-      else gemv_kernel<FMT, DT, 4, 12, false, true><<<blocks, 256, 0, s>>>(args);
-    } else if (args.m == 1) {
-      if (!one) gemv_kernel<FMT, DT, 1, 12, false, false><<<blocks, 256, 0, s>>>(args);
-      else if (group == 9) gemv_kernel<FMT, DT, 1, 9, true, false><<<blocks, 256, 0, s>>>(args);
-      else if (group == 8) gemv_kernel<FMT, DT, 1, 8, true, false><<<blocks, 256, 0, s>>>(args);
-      else gemv_kernel<FMT, DT, 1, 12, true, false><<<blocks, 256, 0, s>>>(args);
+    const int64_t units = (int64_t)args.batch * args.nruns;
+    const int sl = choose_slices(units, args.chunks);
+    // a plain product of one matrix, K unsliced: the lean kernels, group size fitted to K; anything else (a batch,
+    // an epilogue program, slices): one kernel with all of them, groups of 8
+    const bool lean = args.batch == 1 && !args.n_inst && sl == 1;
+    if (args.m == 1) {
+      constexpr int SB = 64 * 2;  // slot bytes a chunk
+      if (!lean) {
+        if (args.n_inst) launch_sliced(gemv_kernel<FMT, DT, 1, 8, false, true, true>, args, units, sl, 8 * SB, 1024, s);
+        else launch_sliced(gemv_kernel<FMT, DT, 1, 8, false, false, true>, args, units, sl, 8 * SB, 1024, s);
+      } else if (group == 9) launch_sliced(gemv_kernel<FMT, DT, 1, 9, true, false, false>, args, units, 1, 9 * SB, 0, s);
+      else if (group == 8) launch_sliced(gemv_kernel<FMT, DT, 1, 8, true, false, false>, args, units, 1, 8 * SB, 0, s);
+      else launch_sliced(gemv_kernel<FMT, DT, 1, 12, true, false, false>, args, units, 1, 12 * SB, 0, s);
     } else {
-      if (!one) gemv_kernel<FMT, DT, 4, 12, false, false><<<blocks, 256, 0, s>>>(args);
-      else if (group == 9) gemv_kernel<FMT, DT, 4, 9, true, false><<<blocks, 256, 0, s>>>(args);
-      else if (group == 8) gemv_kernel<FMT, DT, 4, 8, true, false><<<blocks, 256, 0, s>>>(args);
-      else gemv_kernel<FMT, DT, 4, 12, true, false><<<blocks, 256, 0, s>>>(args);
+      constexpr int SB = 4 * 64 * 2;
+      if (!lean) {
+        if (args.n_inst) launch_sliced(gemv_kernel<FMT, DT, 4, 8, false, true, true>, args, units, sl, 8 * SB, 1024, s);
+        else launch_sliced(gemv_kernel<FMT, DT, 4, 8, false, false, true>, args, units, sl, 8 * SB, 1024, s);
+      } else if (group == 9) launch_sliced(gemv_kernel<FMT, DT, 4, 9, true, false, false>, args, units, 1, 9 * SB, 0, s);
+      else if (group == 8) launch_sliced(gemv_kernel<FMT, DT, 4, 8, true, false, false>, args, units, 1, 8 * SB, 0, s);
+      else launch_sliced(gemv_kernel<FMT, DT, 4, 12, true, false, false>, args, units, 1, 12 * SB, 0, s);
+    }
+  } else if (vec && fits && ((int64_t)31 * args.a.sr + 2 * (int64_t)args.k + 1024) * 2 < (1ll << 32)) {
+    // two 16-row tiles a wave from 17 rows up; the waves of a run side by side
+    const bool two = args.m > 16;
+    const int64_t units = (int64_t)args.batch * args.nruns * (two ? (args.mtiles + 1) / 2 : args.mtiles);
+    const int sl = choose_slices(units, args.chunks);
+    const bool lean = args.batch == 1 && !args.n_inst && sl == 1 && !two;
+    if (two && args.chunks <= 2) {  // short K (a head's width): groups of 2
+      if (args.n_inst) launch_sliced(skinny_vec_kernel<FMT, DT, 2, false, true, 2, true>, args, units, sl, 0, 2048, s);
+      else launch_sliced(skinny_vec_kernel<FMT, DT, 2, false, false, 2, true>, args, units, sl, 0, 2048, s);
+    } else if (two) {
+      if (args.n_inst) launch_sliced(skinny_vec_kernel<FMT, DT, 8, false, true, 2, true>, args, units, sl, 0, 2048, s);
+      else launch_sliced(skinny_vec_kernel<FMT, DT, 8, false, false, 2, true>, args, units, sl, 0, 2048, s);
+    } else if (!lean) {
+      if (args.n_inst) launch_sliced(skinny_vec_kernel<FMT, DT, 8, false, true, 1, true>, args, units, sl, 0, 1024, s);
+      else launch_sliced(skinny_vec_kernel<FMT, DT, 8, false, false, 1, true>, args, units, sl, 0, 1024, s);
+    } else if (group == 9) {
+      launch_sliced(skinny_vec_kernel<FMT, DT, 9, true, false, 1, false>, args, units, 1, 0, 0, s);
+    } else {
+      launch_sliced(skinny_vec_kernel<FMT, DT, 8, true, false, 1, false>, args, units, 1, 0, 0, s);
     }
   } else if (vec) skinny_kernel<FMT, DT, true><<<blocks, 256, 0, s>>>(args);
   else skinny_kernel<FMT, DT, false><<<blocks, 256, 0, s>>>(args);

@@ -240,6 +240,33 @@ def graph_us(rt, fn, n):
   return ms.value * 1000 / n
 
 
+def replay_us(rt, fn, n):
+  """us per call of fn() (which realizes its result) over n calls recorded into one graph (tensor.Recording) and
+  replayed once between two events: the device time of the launches, without Python's dispatch."""
+  from baretile_amd import _lib
+  from baretile_amd.tensor import Recording
+  fn()
+  rt.wait()
+  rec = Recording(rt)
+  with rec:
+    for _ in range(n): out = fn()
+  rec.send()
+  rt.wait()
+  start, end = c_void_p(), c_void_p()
+  _lib.call("event_create", rt.handle, byref(start))
+  _lib.call("event_create", rt.handle, byref(end))
+  _lib.call("event_record", rt.handle, start)
+  rec.send()
+  _lib.call("event_record", rt.handle, end)
+  ms = c_float()
+  _lib.call("event_elapsed", start, end, byref(ms))
+  rt.wait()
+  for h in (start, end): _lib.call("event_destroy", h)
+  result = out.tobytes()
+  rec.close()
+  return ms.value * 1000 / n, result
+
+
 def bf16_bits(a):
   b = np.asarray(a, np.float32).view(np.uint32).astype(np.uint64)
   return ((b + 0x7FFF + (b >> 16 & 1)) >> 16).astype(np.uint16)
@@ -396,17 +423,18 @@ def layer_leg(check=True):
     places = Tensor.of(rt, [list(range(tokens))], "int32")
     rot = (w["cos"].gather(places), w["sin"].gather(places), w["turn"])
     column = places.reshape(1, tokens, 1)
-    run = lambda: llama.layer(x, p, c, rot, column, cache, places)
-    run().realize()
+    run = lambda: llama.layer(x, p, c, rot, column, cache, places).realize()
+    run()
     rt.wait()
     reps, t0 = 5, time.perf_counter()
-    for _ in range(reps): y = run()
+    for _ in range(reps): run()
     rt.wait()
-    us = (time.perf_counter() - t0) / reps * 1e6
+    eager = (time.perf_counter() - t0) / reps * 1e6
+    us, y = replay_us(rt, run, 5)
     flops = 2 * tokens * sum(a * b for a, b in shapes.values()) + 4 * heads * hd * tokens * (tokens + 1) // 2
     res["prefill_2048"] = {"us": round(us, 1), "TFLOP/s": round(flops / us / 1e6, 1),
                            "frac_mfma_peak": round(flops / us / 1e6 / 2500.0, 4), "flops": flops,
-                           "finite": bool(np.isfinite(np.frombuffer(y.tobytes(), np.float32)).all())}
+                           "eager_us": round(eager, 1), "finite": bool(np.isfinite(np.frombuffer(y, np.float32)).all())}
     log("layer prefill", res["prefill_2048"])
     del y, cache
     # batch-32 decode at position 4095 of each slot's cache
@@ -416,18 +444,19 @@ def layer_leg(check=True):
     at = Tensor.of(rt, [[size - 1] * slots], "int32")
     rot = (w["cos"].gather(at), w["sin"].gather(at), w["turn"])
     place = Tensor.of(rt, [[size - 1]], "int32")
-    step = lambda: llama.slots_layer(xs, p, c, rot, keys, values, place)
-    step().realize()
+    step = lambda: llama.slots_layer(xs, p, c, rot, keys, values, place).realize()
+    step()
     rt.wait()
     reps, t0 = 20, time.perf_counter()
-    for _ in range(reps): y = step()
+    for _ in range(reps): step()
     rt.wait()
-    us = (time.perf_counter() - t0) / reps * 1e6
+    eager = (time.perf_counter() - t0) / reps * 1e6
+    us, y = replay_us(rt, step, 20)
     nbytes = wbytes + slots * size * kv * hd * 2 * 2
     res["decode_B32_ctx4096"] = {"us": round(us, 1), "GB/s": round(nbytes / us / 1e3, 1),
                                  "frac_hbm_peak": round(nbytes / us / 1e3 / PEAK_GBS, 4), "bytes": nbytes,
-                                 "tok/s": round(slots / us * 1e6, 1),
-                                 "finite": bool(np.isfinite(np.frombuffer(y.tobytes(), np.float32)).all())}
+                                 "tok/s": round(slots / us * 1e6, 1), "eager_us": round(eager, 1),
+                                 "finite": bool(np.isfinite(np.frombuffer(y, np.float32)).all())}
     log("layer decode", res["decode_B32_ctx4096"])
   finally:
     rt.close()
