@@ -49,6 +49,22 @@ class AttentionArgs(ctypes.Structure):
               ("scratch_bytes", c_uint64), ("firsts", c_uint64), ("firsts_sh", c_int64)]
 
 
+ROW_PLAIN, ROW_RMS, ROW_SWIGLU = range(3)
+
+
+class RowArgs(ctypes.Structure):  # bt_row_args
+  _fields_ = [("a", c_uint64), ("norm", c_uint64), ("residual", c_uint64), ("out", c_uint64), ("b", c_uint64),
+              ("k", c_int64), ("n", c_int64), ("kind", c_int32), ("b_fmt", c_int32), ("out_dtype", c_int32),
+              ("eps", c_float)]
+
+
+class RopeArgs(ctypes.Structure):  # bt_rope_args
+  _fields_ = [("qkv", c_uint64), ("cos", c_uint64), ("sin", c_uint64), ("q", c_uint64), ("cache", c_uint64),
+              ("places", c_uint64), ("qkv_sr", c_int64), ("cs_sr", c_int64), ("q_sr", c_int64), ("cache_sh", c_int64),
+              ("cache_sr", c_int64), ("cache_rows", c_int64), ("rows", c_int32), ("heads", c_int32), ("kv", c_int32),
+              ("head_dim", c_int32)]
+
+
 RT = c_void_p
 U64, I64 = c_uint64, c_int64
 # name: argument types. Every function returns an int status.
@@ -70,6 +86,7 @@ SIGNATURES = {
   "bt_matmul": [RT, POINTER(Operand), c_int, U64, I64, I64, I64, I64, I64, POINTER(Program), POINTER(Operand)],
   "bt_attention": [RT, POINTER(AttentionArgs)],
   "bt_attention_scratch": [POINTER(AttentionArgs), POINTER(c_uint64)],
+  "bt_matmul_row": [RT, POINTER(RowArgs)], "bt_rope_put": [RT, POINTER(RopeArgs)],
   "bt_gather": [RT, c_int, U64, I64, I64, I64, U64, I64, U64, I64],
   "bt_put": [RT, c_int, U64, I64, I64, I64, I64, I64, U64, I64, U64, I64, I64],
   "bt_topk": [RT, c_int, U64, I64, I64, I64, I64, I64, c_int32, c_int32, U64, I64, I64, U64, U64],

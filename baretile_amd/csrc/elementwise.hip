@@ -428,3 +428,48 @@ int bt_put(bt_runtime *rt, int dtype, uint64_t dst, int64_t batch, int64_t dst_r
 }
 
 }  // extern "C"
+
+namespace bt {
+
+// RoPE and the cache put of a decode step: a thread per (token, head, pair j, j + d/2), both outputs of the pair from
+// the same two inputs.
+__global__ void __launch_bounds__(256) rope_put_kernel(const bt_rope_args a) {
+  const int half = a.head_dim / 2, nh = a.heads + 2 * a.kv;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (int64_t)a.rows * nh * half) return;
+  const int j = (int)(t % half), hh = (int)(t / half % nh), i = (int)(t / half / nh);
+  const uint16_t *x = (const uint16_t *)(uintptr_t)a.qkv + (int64_t)i * a.qkv_sr + (int64_t)hh * a.head_dim;
+  const uint16_t *cs = (const uint16_t *)(uintptr_t)a.cos + (int64_t)i * a.cs_sr + (int64_t)hh * a.head_dim;
+  const uint16_t *sn = (const uint16_t *)(uintptr_t)a.sin + (int64_t)i * a.cs_sr + (int64_t)hh * a.head_dim;
+  const float x1 = bf16_value(x[j]), x2 = bf16_value(x[j + half]);
+  const float y1 = x1 * bf16_value(cs[j]) - x2 * bf16_value(sn[j]);
+  const float y2 = x2 * bf16_value(cs[j + half]) + x1 * bf16_value(sn[j + half]);
+  uint16_t *dst;
+  if (hh < a.heads) {
+    dst = (uint16_t *)(uintptr_t)a.q + (int64_t)i * a.q_sr + (int64_t)hh * a.head_dim;
+  } else {
+    const int place = ((const int32_t *)(uintptr_t)a.places)[i];
+    if (place < 0 || place >= a.cache_rows) return;
+    dst = (uint16_t *)(uintptr_t)a.cache + (int64_t)(hh - a.heads) * a.cache_sh + (int64_t)place * a.cache_sr;
+  }
+  dst[j] = (uint16_t)bf16_packed(y1);
+  dst[j + half] = (uint16_t)bf16_packed(y2);
+}
+
+}  // namespace bt
+
+extern "C" int bt_rope_put(bt_runtime *rt, const bt_rope_args *args) {
+  using namespace bt;
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (!args) return fail(BT_EINVAL, "rope_put needs its arguments");
+  const bt_rope_args &a = *args;
+  if (!a.qkv || !a.cos || !a.sin || !a.q || !a.cache || !a.places) return fail(BT_EINVAL, "rope_put needs every buffer");
+  if (a.rows < 1 || a.heads < 1 || a.kv < 1 || a.head_dim < 2 || a.head_dim % 2 || a.cache_rows < 1)
+    return fail(BT_EINVAL, "rope_put shape: %d rows, %d heads, %d key heads of %d", a.rows, a.heads, a.kv, a.head_dim);
+  const int64_t threads = (int64_t)a.rows * (a.heads + 2 * a.kv) * (a.head_dim / 2);
+  if (threads >= (1ll << 31)) return fail(BT_EINVAL, "rope_put too large");
+  rope_put_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, r->stream>>>(a);
+  BT_LAUNCHED("rope_put");
+  return BT_OK;
+}

@@ -930,6 +930,159 @@ gemm2_kernel(const MatmulArgs args, int mblocks, int nblocks) {
   gemm_epilogue<DT, G::BM, G::BN, G::ES, G::ESZ>(args, lds, b, m0, n0, tid);
 }
 
+// ---- one row with its prologue and residual (bt_matmul_row) ------------------------------------------------------
+// The decode GEMV of gemv_kernel for a single row whose A is made in the kernel: the block reads the prologue's inputs
+// straight into LDS (1 KB a load) before its first group of weight loads, works out a' (the norm, or silu(g) * u)
+// into an LDS row while those loads are in flight, and each wave then takes its A values from that row. The residual
+// is added to the fp32 sum before the store.
+struct RowArgs {  // 64 bytes: one scalar load brings them all
+  const uint8_t *b;
+  const uint8_t *a;
+  const uint8_t *norm;
+  const float *res;
+  uint8_t *out;
+  int32_t chunks, nruns, k, n, out_dtype;
+  float eps;
+};
+
+// The block's inputs a 1 KB load: lane l's 16 bytes of piece p at p * 1024 + 16 l, into LDS at lds + p * 1024; the
+// buffer's range gives zeros past its end. Each wave takes every fourth piece.
+__device__ __forceinline__ int row_pieces(const i32x4 &rsrc, int pieces, uint8_t *lds, int wib, int lane) {
+  int issued = 0;
+  for (int p = wib; p < pieces; p += 4, issued++) lds_load16(rsrc, p * 1024 + 16 * lane, lds + p * 1024);
+  return issued;
+}
+
+template <int FMT, int G, int KIND>
+__global__ void __launch_bounds__(256) gemv_row_kernel(const RowArgs args) {
+  constexpr int TB = Tile<FMT>::bytes;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t dyn[];
+  const RowArgs h = args;
+  asm volatile("" ::"s"(h.b), "s"(h.a), "s"(h.norm), "s"(h.res), "s"(h.out), "s"(h.chunks), "s"(h.nruns), "s"(h.k),
+               "s"(h.n), "s"(h.out_dtype), "s"(h.eps));
+  const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
+  const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int run = blockIdx.x * 4 + wib, chunks = h.chunks, K = h.k, kpad = chunks * 64;
+  const bool valid = run < h.nruns;
+  // LDS: the inputs' pieces (raw0, raw1), the row a' (bf16, kpad values), each wave's slots, the norm's partial sums
+  const int p0 = KIND == BT_ROW_RMS ? (K * 4 + 1023) / 1024 : KIND == BT_ROW_SWIGLU ? (K * 2 + 1023) / 1024 : 0;
+  const int p1 = KIND == BT_ROW_PLAIN ? 0 : (K * 2 + 1023) / 1024;
+  const int prow = (kpad * 2 + 1023) / 1024;
+  uint8_t *raw0 = dyn, *raw1 = dyn + p0 * 1024;
+  uint16_t *arow = (uint16_t *)(raw1 + p1 * 1024);
+  uint16_t *slots = arow + prow * 512 + wib * G * 64;
+  float *red = (float *)(arow + prow * 512 + 4 * G * 64);
+  // 1. the prologue's inputs into LDS
+  if (KIND == BT_ROW_PLAIN) {
+    row_pieces(buffer_words(h.a, (uint32_t)K * 2), prow, (uint8_t *)arow, wib, lane);
+  } else if (KIND == BT_ROW_RMS) {
+    row_pieces(buffer_words(h.a, (uint32_t)K * 4), p0, raw0, wib, lane);
+    row_pieces(buffer_words(h.norm, (uint32_t)K * 2), p1, raw1, wib, lane);
+  } else {
+    row_pieces(buffer_words(h.a, (uint32_t)K * 2), p0, raw0, wib, lane);
+    row_pieces(buffer_words(h.a + (int64_t)K * 2, (uint32_t)K * 2), p1, raw1, wib, lane);
+  }
+  // 2. the first group's weights (every wave issues 2 G loads; a wave past the last run reads nothing)
+  const uint8_t *tiles = h.b + (int64_t)(valid ? run : 0) * chunks * TB;
+  const __amdgpu_buffer_rsrc_t tr = buffer(tiles, valid ? (uint32_t)chunks * TB : 0u);
+  const int kl = exp_row(lane), frag = 8 * g;
+  uint32_t bq[G][4], ex[G];
+  uint4 bhi[G];
+  auto load_group = [&](int c0) {
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      const uint32_t at = (uint32_t)(c0 + i) * TB;
+      if (FMT == BT_BFP8 || FMT == BT_BF16) {
+        const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, at + (FMT == BT_BFP8 ? 64 + 16 * lane : 32 * lane),
+                                                             0, STREAM);
+        bq[i][0] = q[0]; bq[i][1] = q[1]; bq[i][2] = q[2]; bq[i][3] = q[3];
+      } else {
+        const auto q = __builtin_amdgcn_raw_buffer_load_b64(tr, at + 64 + 8 * lane, 0, STREAM);
+        bq[i][0] = q[0]; bq[i][1] = q[1];
+      }
+      if (FMT == BT_BF16) {
+        const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 32 * lane + 16, 0, STREAM);
+        bhi[i] = make_uint4(q[0], q[1], q[2], q[3]);
+      } else {
+        ex[i] = __builtin_amdgcn_raw_buffer_load_b8(tr, at + lane, 0, STREAM);
+      }
+    }
+  };
+  load_group(0);
+  // 3. the inputs have landed once at most the 2 G weight loads are outstanding; then the block's
+  wait_vm<2 * G>();
+  __syncthreads();
+  // 4. the row a', each wave a quarter of it
+  if (KIND == BT_ROW_RMS) {
+    const float *x = (const float *)raw0;
+    const uint16_t *w = (const uint16_t *)raw1;
+    float ss = 0.0f;
+    for (int k = wib * 64 + lane; k < K; k += 256) {
+      const float v = round_packed(x[k]);
+      ss += v * v;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (lane == 0) red[wib] = ss;
+    __syncthreads();
+    const float total = ((red[0] + red[1]) + red[2]) + red[3];
+    const float r = 1.0f / sqrtf(total / (float)K + h.eps);
+    for (int k = wib * 64 + lane; k < kpad; k += 256)
+      arow[k] = k < K ? (uint16_t)bf16_packed(round_packed(x[k]) * r * bf16_value(w[k])) : (uint16_t)0;
+    __syncthreads();
+  } else if (KIND == BT_ROW_SWIGLU) {
+    const uint16_t *gate = (const uint16_t *)raw0, *up = (const uint16_t *)raw1;
+    for (int k = wib * 64 + lane; k < kpad; k += 256) {
+      uint16_t v = 0;
+      if (k < K) {
+        const float gv = bf16_value(gate[k]);
+        v = (uint16_t)bf16_packed(gv / (1.0f + expf(-gv)) * bf16_value(up[k]));
+      }
+      arow[k] = v;
+    }
+    __syncthreads();
+  }
+  if (!valid) return;
+  // 5. the product, chunk by chunk as gemv_kernel's
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c0 = 0; c0 < chunks; c0 += G) {
+    if (c0 > 0) load_group(c0);
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      if (c0 + i >= chunks) continue;
+      const int d = FMT == BT_BF16 ? 0 : (int)(int8_t)(ex[i] & 255u);
+      uint32_t v = arow[(c0 + i) * 64 + kl];
+      if (FMT != BT_BF16) v = __float_as_uint(ldexpf(__uint_as_float(v << 16), d)) >> 16;
+      slots[i * 64 + kl] = (uint16_t)v;
+      __builtin_amdgcn_wave_barrier();
+      bf16x8 av[2], bv[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; hh++) av[hh] = *(const bf16x8 *)(slots + i * 64 + frag + 32 * hh);
+      if (FMT == BT_BF16) {
+        const uint4 lo = make_uint4(bq[i][0], bq[i][1], bq[i][2], bq[i][3]);
+        bv[0] = *(const bf16x8 *)&lo;
+        bv[1] = *(const bf16x8 *)&bhi[i];
+      } else if (FMT == BT_BFP8) {
+        bv[0] = q8_to_bf16<false>(make_uint2(bq[i][0], bq[i][1]), make_uint2(0, 0));
+        bv[1] = q8_to_bf16<false>(make_uint2(bq[i][2], bq[i][3]), make_uint2(0, 0));
+      } else {
+        bv[0] = q4_to_bf16(bq[i][0]);
+        bv[1] = q4_to_bf16(bq[i][1]);
+      }
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0], bv[0], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[1], bv[1], acc, 0, 0, 0);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  // 6. row 0 of the tile: lanes 0..15, one column each
+  const int n = run * 16 + col;
+  if (g != 0 || n >= h.n) return;
+  float v = acc[0];
+  if (h.res) v += h.res[n];
+  if (h.out_dtype == BT_BF16) ((uint16_t *)h.out)[n] = (uint16_t)bf16_packed(v);
+  else ((float *)h.out)[n] = v;
+}
+
 int validate_program(const bt_program *prog);
 int check_out(const bt_operand *out);
 
@@ -965,17 +1118,23 @@ static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bo
     const bool lean = args.batch == 1 && !args.n_inst && sl == 1;
     if (args.m == 1) {
       constexpr int SB = 64 * 2;  // slot bytes a chunk
-      if (!lean) {
+      if (!lean && sl > 1) {
         if (args.n_inst) launch_sliced(gemv_kernel<FMT, DT, 1, 8, false, true, true>, args, units, sl, 8 * SB, 1024, s);
         else launch_sliced(gemv_kernel<FMT, DT, 1, 8, false, false, true>, args, units, sl, 8 * SB, 1024, s);
+      } else if (!lean) {
+        if (args.n_inst) launch_sliced(gemv_kernel<FMT, DT, 1, 12, false, true, false>, args, units, 1, 12 * SB, 0, s);
+        else launch_sliced(gemv_kernel<FMT, DT, 1, 12, false, false, false>, args, units, 1, 12 * SB, 0, s);
       } else if (group == 9) launch_sliced(gemv_kernel<FMT, DT, 1, 9, true, false, false>, args, units, 1, 9 * SB, 0, s);
       else if (group == 8) launch_sliced(gemv_kernel<FMT, DT, 1, 8, true, false, false>, args, units, 1, 8 * SB, 0, s);
       else launch_sliced(gemv_kernel<FMT, DT, 1, 12, true, false, false>, args, units, 1, 12 * SB, 0, s);
     } else {
       constexpr int SB = 4 * 64 * 2;
-      if (!lean) {
+      if (!lean && sl > 1) {
         if (args.n_inst) launch_sliced(gemv_kernel<FMT, DT, 4, 8, false, true, true>, args, units, sl, 8 * SB, 1024, s);
         else launch_sliced(gemv_kernel<FMT, DT, 4, 8, false, false, true>, args, units, sl, 8 * SB, 1024, s);
+      } else if (!lean) {
+        if (args.n_inst) launch_sliced(gemv_kernel<FMT, DT, 4, 12, false, true, false>, args, units, 1, 12 * SB, 0, s);
+        else launch_sliced(gemv_kernel<FMT, DT, 4, 12, false, false, false>, args, units, 1, 12 * SB, 0, s);
       } else if (group == 9) launch_sliced(gemv_kernel<FMT, DT, 4, 9, true, false, false>, args, units, 1, 9 * SB, 0, s);
       else if (group == 8) launch_sliced(gemv_kernel<FMT, DT, 4, 8, true, false, false>, args, units, 1, 8 * SB, 0, s);
       else launch_sliced(gemv_kernel<FMT, DT, 4, 12, true, false, false>, args, units, 1, 12 * SB, 0, s);
@@ -1108,5 +1267,59 @@ extern "C" int bt_matmul(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_
   else if (b_fmt == BT_BFP8) launch_skinny<BT_BFP8>(args, r->stream);
   else launch_skinny<BT_BFP4>(args, r->stream);
   BT_LAUNCHED("matmul");
+  return BT_OK;
+}
+
+template <int FMT, int G>
+static void launch_row_g(const RowArgs &ra, int kind, size_t lds, hipStream_t s) {
+  const unsigned blocks = (unsigned)((ra.nruns + 3) / 4);
+  if (kind == BT_ROW_RMS) gemv_row_kernel<FMT, G, BT_ROW_RMS><<<blocks, 256, lds, s>>>(ra);
+  else if (kind == BT_ROW_SWIGLU) gemv_row_kernel<FMT, G, BT_ROW_SWIGLU><<<blocks, 256, lds, s>>>(ra);
+  else gemv_row_kernel<FMT, G, BT_ROW_PLAIN><<<blocks, 256, lds, s>>>(ra);
+}
+
+template <int FMT>
+static void launch_row(const RowArgs &ra, int kind, hipStream_t s) {
+  const int c = ra.chunks, g = c % 12 == 0 ? 12 : c % 9 == 0 ? 9 : c % 8 == 0 ? 8 : 12;
+  const int k = ra.k, p0 = kind == BT_ROW_RMS ? (k * 4 + 1023) / 1024 : kind == BT_ROW_SWIGLU ? (k * 2 + 1023) / 1024 : 0;
+  const int p1 = kind == BT_ROW_PLAIN ? 0 : (k * 2 + 1023) / 1024, prow = (c * 128 + 1023) / 1024;
+  const size_t lds = (size_t)(p0 + p1 + prow) * 1024 + 4 * g * 128 + 16;
+  if (g == 9) launch_row_g<FMT, 9>(ra, kind, lds, s);
+  else if (g == 8) launch_row_g<FMT, 8>(ra, kind, lds, s);
+  else launch_row_g<FMT, 12>(ra, kind, lds, s);
+}
+
+extern "C" int bt_matmul_row(bt_runtime *rt, const bt_row_args *args) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (!args) return fail(BT_EINVAL, "matmul_row needs its arguments");
+  const bt_row_args &x = *args;
+  if (x.kind != BT_ROW_PLAIN && x.kind != BT_ROW_RMS && x.kind != BT_ROW_SWIGLU)
+    return fail(BT_EINVAL, "matmul_row prologue %d", x.kind);
+  if (x.b_fmt != BT_BF16 && x.b_fmt != BT_BFP8 && x.b_fmt != BT_BFP4) return fail(BT_EINVAL, "B format %d", x.b_fmt);
+  if (x.out_dtype != BT_BF16 && x.out_dtype != BT_FP32) return fail(BT_EINVAL, "matmul_row writes bf16 or fp32");
+  if (x.k < 1 || x.k > 4096 || x.n < 1 || x.n >= (1 << 30))
+    return fail(BT_EINVAL, "matmul_row shape k=%lld (1..4096), n=%lld", (long long)x.k, (long long)x.n);
+  if (!x.a || !x.out || !x.b || (x.kind == BT_ROW_RMS && !x.norm))
+    return fail(BT_EINVAL, "matmul_row needs a, out, B and (for the norm) its weights");
+  if (x.a % 16 || x.norm % 16 || x.b % 16 || (x.kind == BT_ROW_SWIGLU && x.k % 8))
+    return fail(BT_EINVAL, "matmul_row reads its inputs 16 bytes at a time: a, norm and B 16-byte aligned%s",
+                x.kind == BT_ROW_SWIGLU ? ", k a multiple of 8" : "");
+  RowArgs ra;
+  ra.b = (const uint8_t *)(uintptr_t)x.b;
+  ra.a = (const uint8_t *)(uintptr_t)x.a;
+  ra.norm = (const uint8_t *)(uintptr_t)x.norm;
+  ra.res = (const float *)(uintptr_t)x.residual;
+  ra.out = (uint8_t *)(uintptr_t)x.out;
+  ra.chunks = (int32_t)((x.k + 63) / 64);
+  ra.nruns = (int32_t)((x.n + 15) / 16);
+  ra.k = (int32_t)x.k;
+  ra.n = (int32_t)x.n;
+  ra.out_dtype = x.out_dtype;
+  ra.eps = x.eps;
+  if (x.b_fmt == BT_BF16) launch_row<BT_BF16>(ra, x.kind, r->stream);
+  else if (x.b_fmt == BT_BFP8) launch_row<BT_BFP8>(ra, x.kind, r->stream);
+  else launch_row<BT_BFP4>(ra, x.kind, r->stream);
+  BT_LAUNCHED("matmul_row");
   return BT_OK;
 }

@@ -171,6 +171,30 @@ def layer(x, p, c, rot, places, cache, rows, firsts=None):
   return (x + mlp(rms(x, p["post_attention_layernorm"], c), p)).realize()
 
 
+def row_fits(w, c):
+  """Whether one-token steps can take the fused row kernels (row_layer): the widths bt_matmul_row takes, heads
+  attend() takes, bf16 norms, matrices by columns."""
+  hd, ffn = head(c), c.ffn or 4 * c.dim
+  widths = (c.dim, c.heads * hd, ffn)
+  return (all(k <= 4096 and k % 8 == 0 for k in widths) and hd in (64, 128) and w["norm"].dtype == "bf16" and
+          all(w[f"layers.{l}.{n}"].layout == "columns" for l in range(c.layers)
+              for n in ("qkv_proj", "o_proj", "gate_up_proj", "down_proj")) and w["embed.T"].layout == "columns")
+
+
+def row_layer(x, p, c, rot, places, cache, rows):
+  """One block for a single token, as layer() computes it, in six kernels: the norm inside the qkv and gate_up
+  products, RoPE with the cache put, attention, the residual adds inside the o and down products, and silu(gate) * up
+  inside the down product (bt_matmul_row, bt_rope_put). Each fused step rounds once, in fp32, where the lazy graph
+  rounds each operation to bf16."""
+  rep = c.heads // c.kv
+  qkv = x.matmul_row(p["qkv_proj"], "bf16", norm=p["input_layernorm"], eps=c.eps)
+  q = qkv.rope_put(rot[0], rot[1], cache, rows, c.heads, c.kv).split(c.heads)
+  o = q.attend(cache[:c.kv, :, :].repeat_interleave(rep), cache[c.kv:, :, :].repeat_interleave(rep), places)
+  x = o.matmul_row(p["o_proj"], "fp32", residual=x)
+  gate_up = x.matmul_row(p["gate_up_proj"], "bf16", norm=p["post_attention_layernorm"], eps=c.eps)
+  return gate_up.matmul_row(p["down_proj"], "fp32", swiglu=True, residual=x)
+
+
 def slots_layer(x, p, c, rot, keys, values, place):
   """One block for a batch of slots, each with its own cache and one new token, all at one place: the batched decode
   of llama.forward(slots=...) (llama.py:293-354). x is (1, S, dim), the stream of the S slots; keys and values are
@@ -221,6 +245,10 @@ def forward(ids, places, w, c, caches, every=False, slots=None):
     column = (first + places * (places < part - 1)).realize().reshape(1, n, 1)  # a free slot's token: its first row
     firsts = first.reshape(1, n, 1)
   blocks = [block(w, l) for l in range(c.layers)]
+  if n == 1 and not slots and w.setdefault("row_fits", row_fits(w, c)):  # one token: the fused row kernels
+    x = x.reshape(1, c.dim)
+    for l in range(c.layers): x = row_layer(x, blocks[l], c, rot, column, caches[l], rows)
+    return x.matmul_row(w["embed.T"], "fp32", norm=w["norm"], eps=c.eps).reshape(1, 1, w["embed.T"].cols)
   for l in range(c.layers): x = layer(x, blocks[l], c, rot, column, caches[l], rows, firsts)
   h = rms(x, w["norm"], c)
   if not (every or slots) and n > 1: h = h[:, n - 1:n, :]  # the last token's row

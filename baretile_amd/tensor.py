@@ -646,6 +646,62 @@ class Tensor:
     a = self.cast("bf16") if self.dtype in BFP else self
     return a._new("matmul", (a, x), (max(a.batch, x.batch), a.rows, x.cols), dtype)
 
+  def matmul_row(self, w, dtype="bf16", norm=None, eps=1e-5, swiglu=False, residual=None):
+    """The product of one row with w (by columns) in one kernel, with the operation before it fused (the decode step
+    of llama.py's layer at batch 1, llama.py:106-130; bt_matmul_row): with norm, the RMSNorm of self (an fp32 row,
+    rounded to bf16 first) scaled by norm (bf16); with swiglu, silu(gate) * up of self (a bf16 row holding the gate
+    then the up half); else self (bf16). residual, an fp32 row, is added to the fp32 sum. The row may be any tensor
+    whose values lie contiguous in memory (an attention output of one row, say). Returns a (1, n) row of dtype."""
+    if dtype not in ("bf16", "fp32"): raise ValueError(f"matmul_row writes bf16 or fp32, not {dtype}")
+    if not isinstance(w, Tensor) or w.rt is not self.rt or w.layout != "columns" or w.batch != 1:
+      raise ValueError("matmul_row needs w laid out by columns, batch 1, on the same runtime")
+    a = self.realize()
+    kind = _lib.ROW_RMS if norm is not None else _lib.ROW_SWIGLU if swiglu else _lib.ROW_PLAIN
+    size = a.batch * a.rows * a.cols
+    k = size // 2 if swiglu else size
+    want = "fp32" if norm is not None else "bf16"
+    flat = a._contiguous() or (a.rows == 1 and a.sc == 1 and a.sb == a.cols and a.rep == 1 and a.cyc == 0)
+    if not (a.dtype == want and flat and a.layout == "plain" and k == w.rows and (not swiglu or size == 2 * k)):
+      raise ValueError(f"matmul_row needs a contiguous {want} row of {w.rows} values{' (twice, gate then up)' if swiglu else ''}: "
+                       f"{a.shape} {a.dtype}")
+    nw = None
+    if norm is not None:
+      nw = norm.realize()
+      if not (nw.dtype == "bf16" and nw._contiguous() and nw.batch * nw.rows * nw.cols == k):
+        raise ValueError(f"matmul_row's norm weights must be a contiguous bf16 row of {k}: {nw.shape} {nw.dtype}")
+    res = None
+    if residual is not None:
+      res = residual.realize()
+      if not (res.dtype == "fp32" and res._contiguous() and res.batch * res.rows * res.cols == w.cols):
+        raise ValueError(f"matmul_row's residual must be a contiguous fp32 row of {w.cols}: {res.shape} {res.dtype}")
+    out = Tensor(self.rt, 1, w.cols, dtype=dtype)
+    args = _lib.RowArgs(a.addr, nw.addr if nw is not None else 0, res.addr if res is not None else 0, out.addr,
+                        w.storage.addr, k, w.cols, kind, _lib.DTYPES[w.dtype], _lib.DTYPES[dtype], eps)
+    self.rt.run("matmul_row", "matmul_row", ctypes.byref(args))
+    return out
+
+  def rope_put(self, cos, sin, cache, places, heads, kv):
+    """RoPE of each head of self (bf16 rows of heads + 2 kv heads) in fp32, the query heads returned as a
+    (rows, heads * d) tensor and the key and value heads put into cache (2 kv, size, d) at places (an int32 row),
+    in one kernel (llama.py:132-160; bt_rope_put). cos and sin are bf16 rows laid out as self; the tables turn x
+    into x cos + (-x2, x1) sin, which leaves the value heads (cos 1, sin 0) as they are."""
+    x, c, sn, cc, pl = self.realize(), cos.realize(), sin.realize(), cache.realize(), places.realize()
+    nh = heads + 2 * kv
+    if not (x.dtype == c.dtype == sn.dtype == cc.dtype == "bf16" and x.batch == 1 and x.cols % nh == 0 and x.sc == 1):
+      raise ValueError(f"rope_put needs bf16 rows of {nh} heads and bf16 tables: {x.shape} {x.dtype}")
+    d = x.cols // nh
+    if not (c.shape[-2:] == sn.shape[-2:] == (x.rows, x.cols) and c.sc == 1 and sn.sc == 1 and c.sr == sn.sr):
+      raise ValueError(f"rope_put needs cos and sin laid out as the rows: {c.shape} {sn.shape} for {x.shape}")
+    if not (cc.batch == 2 * kv and cc.cols == d and cc.sc == 1 and cc.rep == 1 and not cc.cyc and cc.layout == "plain"):
+      raise ValueError(f"rope_put needs a plain ({2 * kv}, size, {d}) cache: {cc.shape}")
+    if not (pl.dtype == "int32" and pl.batch * pl.rows == 1 and pl.cols == x.rows and pl.sc == 1):
+      raise ValueError("rope_put needs places as an int32 row, one for each row")
+    q = Tensor(self.rt, x.rows, heads * d)
+    args = _lib.RopeArgs(x.addr, c.addr, sn.addr, q.addr, cc.addr, pl.addr, x.sr, c.sr, q.sr, cc.sb, cc.sr, cc.rows,
+                         x.rows, heads, kv, d)
+    self.rt.run("rope_put", "rope_put", ctypes.byref(args))
+    return q
+
   # ---- attention, rows in and out
   def attend(self, k, v, places, window=0, fidelity=None, parts=None, firsts=None):
     """softmax(self @ k^T + mask) @ v, with the mask from each query row's place (and window), in one kernel

@@ -174,6 +174,45 @@ int bt_reduce(bt_runtime *rt, const bt_program *prog, int kind, int axis, int64_
 int bt_matmul(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_t b, int64_t b_batch, int64_t batch, int64_t m,
               int64_t k, int64_t n, const bt_program *epilogue, const bt_operand *out);
 
+/* ---- one-row products with their neighbours fused: the decode step of models/llama.py at batch 1 (its layer,
+ * llama.py:106-130: rms then qkv, rms then gate_up, silu(gate) * up then down, each product then the residual add),
+ * where fused_kernel would run the norm, the activation and the add as the matmul's prologue and epilogue
+ * (kernels.py:41-727) ----------------------------------------------------------------------------------------------
+ *
+ * out[n] = (residual ? residual[n] : 0) + sum_k a'[k] * B[k, n] for n < N, where a' is
+ *   BT_ROW_PLAIN:  a, bf16, k values;
+ *   BT_ROW_RMS:    bf16(x[k] * r * norm[k]), x = bf16(a[k]) (rounded half up) for a an fp32 row of k values,
+ *                  norm bf16, r = 1 / sqrt(mean over k of x^2 + eps), all in fp32;
+ *   BT_ROW_SWIGLU: bf16(silu(g) * u) with g = a[k], u = a[k + K] (a: bf16, the gate then the up half, 2K values),
+ *                  silu(g) = g / (1 + exp(-g)) in fp32.
+ * B is in columns layout (bf16, bfp8 or bfp4) and is multiplied as bt_matmul does; residual is 0 or fp32, n values;
+ * out is bf16 (rounded half up) or fp32. k <= 4096. */
+#define BT_ROW_PLAIN 0
+#define BT_ROW_RMS 1
+#define BT_ROW_SWIGLU 2
+typedef struct {
+  uint64_t a, norm, residual, out, b;
+  int64_t k, n;
+  int32_t kind, b_fmt, out_dtype;
+  float eps;
+} bt_row_args;
+int bt_matmul_row(bt_runtime *rt, const bt_row_args *args);
+
+/* RoPE and the cache put of a decode step (llama.py:132-160: rope, then the key and value heads put at the tokens'
+ * places). For each token i < rows and head h < heads + 2 kv of qkv (bf16, element (i, h, j) at
+ * i * qkv_sr + h * head_dim + j):
+ *   y = bf16(x[j] * cos[j] + t[j] * sin[j]), t[j] = -x[j + d/2] for j < d/2 and x[j - d/2] after (d = head_dim),
+ * in fp32, with cos and sin bf16 rows laid out as qkv (row stride cs_sr). Query heads are written to q (as qkv, row
+ * stride q_sr); key and value heads to cache[h - heads, places[i], :] (bf16, element strides cache_sh, cache_sr),
+ * a place outside [0, cache_rows) skipped. RoPE's tables carry the query scale, and cos 1, sin 0 for the value
+ * heads, so a value head is stored as it is. */
+typedef struct {
+  uint64_t qkv, cos, sin, q, cache, places;
+  int64_t qkv_sr, cs_sr, q_sr, cache_sh, cache_sr, cache_rows;
+  int32_t rows, heads, kv, head_dim;
+} bt_rope_args;
+int bt_rope_put(bt_runtime *rt, const bt_rope_args *args);
+
 /* ---- attention: replaces attention_kernel and its division/combine launches (kernels.py:794-1005,
  * tensor.py:797-841) -------------------------------------------------------------------------------------------
  *

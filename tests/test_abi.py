@@ -48,7 +48,7 @@ def test_struct_sizes_match_the_header(tmp_path):
   cc = shutil.which("gcc") or shutil.which("cc")
   if cc is None: pytest.skip("no C compiler")
   structs = {"bt_operand": _lib.Operand, "bt_inst": _lib.Inst, "bt_program": _lib.Program,
-             "bt_attention_args": _lib.AttentionArgs}
+             "bt_attention_args": _lib.AttentionArgs, "bt_row_args": _lib.RowArgs, "bt_rope_args": _lib.RopeArgs}
   cname = {("bt_program", "inputs"): "in"}  # Python can't name a field `in`
   lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "baretile_amd.h"', "int main(void) {"]
   for name, cls in structs.items():
