@@ -935,7 +935,7 @@ gemm2_kernel(const MatmulArgs args, int mblocks, int nblocks) {
 // straight into LDS (1 KB a load) before its first group of weight loads, works out a' (the norm, or silu(g) * u)
 // into an LDS row while those loads are in flight, and each wave then takes its A values from that row. The residual
 // is added to the fp32 sum before the store.
-struct RowArgs {  // 64 bytes: one scalar load brings them all
+struct RowArgs {  // 68 bytes: brought by the kernel's first round of scalar loads
   const uint8_t *b;
   const uint8_t *a;
   const uint8_t *norm;
@@ -943,6 +943,7 @@ struct RowArgs {  // 64 bytes: one scalar load brings them all
   uint8_t *out;
   int32_t chunks, nruns, k, n, out_dtype;
   float eps;
+  int32_t slices;  // waves a run (1, 2 or 4), each a slice of K, summed in slice order
 };
 
 // The block's inputs a 1 KB load: lane l's 16 bytes of piece p at p * 1024 + 16 l, into LDS at lds + p * 1024; the
@@ -956,14 +957,19 @@ __device__ __forceinline__ int row_pieces(const i32x4 &rsrc, int pieces, uint8_t
 template <int FMT, int G, int KIND>
 __global__ void __launch_bounds__(256) gemv_row_kernel(const RowArgs args) {
   constexpr int TB = Tile<FMT>::bytes;
+  // weights loaded with the default cache policy: a decode step reads the same matrices every token, and a small
+  // model's stay in the 256 MB Infinity Cache between steps
+  constexpr int KEEP = 0;
   extern __shared__ __attribute__((aligned(1024))) uint8_t dyn[];
   const RowArgs h = args;
   asm volatile("" ::"s"(h.b), "s"(h.a), "s"(h.norm), "s"(h.res), "s"(h.out), "s"(h.chunks), "s"(h.nruns), "s"(h.k),
-               "s"(h.n), "s"(h.out_dtype), "s"(h.eps));
+               "s"(h.n), "s"(h.out_dtype), "s"(h.eps), "s"(h.slices));
   const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
   const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int run = blockIdx.x * 4 + wib, chunks = h.chunks, K = h.k, kpad = chunks * 64;
+  const int S = h.slices, sl = wib % S, run = blockIdx.x * (4 / S) + wib / S;
+  const int chunks = h.chunks, K = h.k, kpad = chunks * 64;
   const bool valid = run < h.nruns;
+  const int per = (chunks + S - 1) / S, c_begin = min(chunks, sl * per), mine = min(chunks, c_begin + per) - c_begin;
   // LDS: the inputs' pieces (raw0, raw1), the row a' (bf16, kpad values), each wave's slots, the norm's partial sums
   const int p0 = KIND == BT_ROW_RMS ? (K * 4 + 1023) / 1024 : KIND == BT_ROW_SWIGLU ? (K * 2 + 1023) / 1024 : 0;
   const int p1 = KIND == BT_ROW_PLAIN ? 0 : (K * 2 + 1023) / 1024;
@@ -972,6 +978,7 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(const RowArgs args) {
   uint16_t *arow = (uint16_t *)(raw1 + p1 * 1024);
   uint16_t *slots = arow + prow * 512 + wib * G * 64;
   float *red = (float *)(arow + prow * 512 + 4 * G * 64);
+  f32x4 *part = (f32x4 *)(red + 4);  // the slices' partial tiles
   // 1. the prologue's inputs into LDS
   if (KIND == BT_ROW_PLAIN) {
     row_pieces(buffer_words(h.a, (uint32_t)K * 2), prow, (uint8_t *)arow, wib, lane);
@@ -983,8 +990,8 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(const RowArgs args) {
     row_pieces(buffer_words(h.a + (int64_t)K * 2, (uint32_t)K * 2), p1, raw1, wib, lane);
   }
   // 2. the first group's weights (every wave issues 2 G loads; a wave past the last run reads nothing)
-  const uint8_t *tiles = h.b + (int64_t)(valid ? run : 0) * chunks * TB;
-  const __amdgpu_buffer_rsrc_t tr = buffer(tiles, valid ? (uint32_t)chunks * TB : 0u);
+  const uint8_t *tiles = h.b + ((int64_t)(valid ? run : 0) * chunks + c_begin) * TB;
+  const __amdgpu_buffer_rsrc_t tr = buffer(tiles, valid ? (uint32_t)mine * TB : 0u);
   const int kl = exp_row(lane), frag = 8 * g;
   uint32_t bq[G][4], ex[G];
   uint4 bhi[G];
@@ -994,17 +1001,17 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(const RowArgs args) {
       const uint32_t at = (uint32_t)(c0 + i) * TB;
       if (FMT == BT_BFP8 || FMT == BT_BF16) {
         const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, at + (FMT == BT_BFP8 ? 64 + 16 * lane : 32 * lane),
-                                                             0, STREAM);
+                                                             0, KEEP);
         bq[i][0] = q[0]; bq[i][1] = q[1]; bq[i][2] = q[2]; bq[i][3] = q[3];
       } else {
-        const auto q = __builtin_amdgcn_raw_buffer_load_b64(tr, at + 64 + 8 * lane, 0, STREAM);
+        const auto q = __builtin_amdgcn_raw_buffer_load_b64(tr, at + 64 + 8 * lane, 0, KEEP);
         bq[i][0] = q[0]; bq[i][1] = q[1];
       }
       if (FMT == BT_BF16) {
-        const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 32 * lane + 16, 0, STREAM);
+        const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 32 * lane + 16, 0, KEEP);
         bhi[i] = make_uint4(q[0], q[1], q[2], q[3]);
       } else {
-        ex[i] = __builtin_amdgcn_raw_buffer_load_b8(tr, at + lane, 0, STREAM);
+        ex[i] = __builtin_amdgcn_raw_buffer_load_b8(tr, at + lane, 0, KEEP);
       }
     }
   };
@@ -1042,16 +1049,16 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(const RowArgs args) {
     }
     __syncthreads();
   }
-  if (!valid) return;
-  // 5. the product, chunk by chunk as gemv_kernel's
+  if (!valid && S == 1) return;
+  // 5. the product over this wave's slice, chunk by chunk as gemv_kernel's
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int c0 = 0; c0 < chunks; c0 += G) {
+  for (int c0 = 0; c0 < mine; c0 += G) {
     if (c0 > 0) load_group(c0);
 #pragma unroll
     for (int i = 0; i < G; i++) {
-      if (c0 + i >= chunks) continue;
+      if (c0 + i >= mine) continue;
       const int d = FMT == BT_BF16 ? 0 : (int)(int8_t)(ex[i] & 255u);
-      uint32_t v = arow[(c0 + i) * 64 + kl];
+      uint32_t v = arow[(c_begin + c0 + i) * 64 + kl];
       if (FMT != BT_BF16) v = __float_as_uint(ldexpf(__uint_as_float(v << 16), d)) >> 16;
       slots[i * 64 + kl] = (uint16_t)v;
       __builtin_amdgcn_wave_barrier();
@@ -1074,7 +1081,13 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(const RowArgs args) {
     }
     __builtin_amdgcn_wave_barrier();
   }
-  // 6. row 0 of the tile: lanes 0..15, one column each
+  // 6. the slices added in order into the first; row 0 of the tile: lanes 0..15, one column each
+  if (S > 1) {
+    if (sl != 0) part[wib * 64 + lane] = acc;
+    __syncthreads();
+    if (sl != 0 || !valid) return;
+    for (int j = 1; j < S; j++) acc += part[(wib + j) * 64 + lane];
+  }
   const int n = run * 16 + col;
   if (g != 0 || n >= h.n) return;
   float v = acc[0];
@@ -1271,22 +1284,28 @@ extern "C" int bt_matmul(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_
 }
 
 template <int FMT, int G>
-static void launch_row_g(const RowArgs &ra, int kind, size_t lds, hipStream_t s) {
-  const unsigned blocks = (unsigned)((ra.nruns + 3) / 4);
+static void launch_row_g(const RowArgs &ra, int kind, size_t lds, unsigned blocks, hipStream_t s) {
   if (kind == BT_ROW_RMS) gemv_row_kernel<FMT, G, BT_ROW_RMS><<<blocks, 256, lds, s>>>(ra);
   else if (kind == BT_ROW_SWIGLU) gemv_row_kernel<FMT, G, BT_ROW_SWIGLU><<<blocks, 256, lds, s>>>(ra);
   else gemv_row_kernel<FMT, G, BT_ROW_PLAIN><<<blocks, 256, lds, s>>>(ra);
 }
 
 template <int FMT>
-static void launch_row(const RowArgs &ra, int kind, hipStream_t s) {
-  const int c = ra.chunks, g = c % 12 == 0 ? 12 : c % 9 == 0 ? 9 : c % 8 == 0 ? 8 : 12;
+static void launch_row(RowArgs ra, int kind, hipStream_t s) {
+  // slices: up to 4 a run while each keeps 6 chunks or more and the launch stays under 1024 waves
+  int sl = 1;
+  while (sl < 4 && ra.chunks / (2 * sl) >= 6 && (int64_t)ra.nruns * sl < 1024) sl *= 2;
+  ra.slices = sl;
+  const int c = (ra.chunks + sl - 1) / sl;  // chunks a slice
+  const int g = c <= 6 ? 6 : c % 12 == 0 ? 12 : c % 9 == 0 ? 9 : c % 8 == 0 ? 8 : 12;
   const int k = ra.k, p0 = kind == BT_ROW_RMS ? (k * 4 + 1023) / 1024 : kind == BT_ROW_SWIGLU ? (k * 2 + 1023) / 1024 : 0;
-  const int p1 = kind == BT_ROW_PLAIN ? 0 : (k * 2 + 1023) / 1024, prow = (c * 128 + 1023) / 1024;
-  const size_t lds = (size_t)(p0 + p1 + prow) * 1024 + 4 * g * 128 + 16;
-  if (g == 9) launch_row_g<FMT, 9>(ra, kind, lds, s);
-  else if (g == 8) launch_row_g<FMT, 8>(ra, kind, lds, s);
-  else launch_row_g<FMT, 12>(ra, kind, lds, s);
+  const int p1 = kind == BT_ROW_PLAIN ? 0 : (k * 2 + 1023) / 1024, prow = (ra.chunks * 128 + 1023) / 1024;
+  const size_t lds = (size_t)(p0 + p1 + prow) * 1024 + 4 * g * 128 + 16 + 4 * 1024;
+  const unsigned blocks = (unsigned)(((int64_t)ra.nruns * sl + 3) / 4);
+  if (g == 9) launch_row_g<FMT, 9>(ra, kind, lds, blocks, s);
+  else if (g == 8) launch_row_g<FMT, 8>(ra, kind, lds, blocks, s);
+  else if (g == 6) launch_row_g<FMT, 6>(ra, kind, lds, blocks, s);
+  else launch_row_g<FMT, 12>(ra, kind, lds, blocks, s);
 }
 
 extern "C" int bt_matmul_row(bt_runtime *rt, const bt_row_args *args) {
@@ -1317,6 +1336,7 @@ extern "C" int bt_matmul_row(bt_runtime *rt, const bt_row_args *args) {
   ra.n = (int32_t)x.n;
   ra.out_dtype = x.out_dtype;
   ra.eps = x.eps;
+  ra.slices = 1;
   if (x.b_fmt == BT_BF16) launch_row<BT_BF16>(ra, x.kind, r->stream);
   else if (x.b_fmt == BT_BFP8) launch_row<BT_BFP8>(ra, x.kind, r->stream);
   else launch_row<BT_BFP4>(ra, x.kind, r->stream);

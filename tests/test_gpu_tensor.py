@@ -251,3 +251,85 @@ def test_topk(rt):
     assert np.array_equal(np.array(values.tolist(), np.float32), np.take_along_axis(x, want, -1))
   with pytest.raises(ValueError): Tensor.of(rt, x, "fp32").topk(65)
   with pytest.raises(ValueError): Tensor.of(rt, x, "fp32").topk(4, parts=3)
+
+
+def _weights(rt, k, n, fmt, seed):
+  w = np.random.default_rng(seed).normal(0, 0.05, (k, n)).astype(np.float32)
+  t = Tensor.of(rt, w)
+  t = (t.cast(fmt) if fmt != "bf16" else t).columns()
+  if fmt == "bf16": return t, B.bf16(w).astype(np.float64)
+  pad = -n % 16  # the oracle takes whole runs of 16; the padding columns' runs don't touch the real ones
+  return t, B.bfp(np.pad(w, ((0, 0), (0, pad))), fmt)[:, :n]
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bfp4"])
+@pytest.mark.parametrize("kind,k,n", [("plain", 576, 960), ("rms", 576, 3072), ("rms", 4096, 200),
+                                      ("swiglu", 1536, 576), ("swiglu", 64, 40)])
+def test_matmul_row(rt, fmt, kind, k, n):
+  # One row times w with its prologue and residual in one kernel (bt_matmul_row), against NumPy on the documented
+  # formula: the prologue's row a' exactly as bf16 of the fp32 computation (a bf16 rounding may flip where the
+  # device's fp32 sum or exp differs in the last bit), the product within the reference's bound of a' @ w.
+  rng = np.random.default_rng(k + n)
+  wt, wq = _weights(rt, k, n, fmt, k * n)
+  res = rng.normal(0, 1, n).astype(np.float32)
+  if kind == "rms":
+    x = (rng.normal(0, 2, k)).astype(np.float32)
+    norm = B.bf16(rng.normal(1, 0.1, k).astype(np.float32)).astype(np.float32)
+    xb = packed(x).astype(np.float32)
+    r = np.float32(1) / np.sqrt(np.float32(np.mean(xb.astype(np.float64) ** 2)) + np.float32(1e-5))
+    a = packed(xb * r * norm)
+    got = Tensor.of(rt, x[None], "fp32").matmul_row(wt, "fp32", norm=Tensor.of(rt, norm[None]), eps=1e-5,
+                                                     residual=Tensor.of(rt, res[None], "fp32"))
+  elif kind == "swiglu":
+    gu = B.bf16(rng.normal(0, 2, 2 * k).astype(np.float32)).astype(np.float32)
+    g, u = gu[:k], gu[k:]
+    a = packed(g / (np.float32(1) + np.exp(-g)) * u)
+    got = Tensor.of(rt, gu[None]).matmul_row(wt, "fp32", swiglu=True, residual=Tensor.of(rt, res[None], "fp32"))
+  else:
+    a = B.bf16(rng.normal(0, 1, k).astype(np.float32)).astype(np.float64)
+    got = Tensor.of(rt, a[None].astype(np.float32)).matmul_row(wt, "fp32", residual=Tensor.of(rt, res[None], "fp32"))
+  want = a @ wq + res
+  bound = ops.matmul_bound(a, wq) * 2 + 1e-6 * np.abs(want)
+  assert got.shape[-2:] == (1, n)
+  assert np.all(np.abs(value(got).reshape(n) - want) <= bound)
+  # bf16 output: the fp32 result rounded half up
+  if kind == "plain":
+    g16 = Tensor.of(rt, a[None].astype(np.float32)).matmul_row(wt, "bf16")
+    assert np.all(np.abs(value(g16).reshape(n) - a @ wq) <= ops.matmul_bound(a, wq) + 2.0 ** -8 * np.abs(a @ wq))
+
+
+def test_matmul_row_rejects_bad_inputs(rt):
+  wt, _ = _weights(rt, 64, 32, "bfp8", 0)
+  with pytest.raises(ValueError, match="contiguous bf16 row of 64"):
+    Tensor.of(rt, np.ones((1, 32), np.float32)).matmul_row(wt)
+  with pytest.raises(ValueError, match="fp32 row"):
+    Tensor.of(rt, np.ones((1, 64), np.float32)).matmul_row(wt, norm=Tensor.of(rt, np.ones((1, 64), np.float32)))
+  with pytest.raises(ValueError, match="columns"):
+    Tensor.of(rt, np.ones((1, 64), np.float32)).matmul_row(Tensor.of(rt, np.ones((64, 32), np.float32)))
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_rope_put(rt, hd):
+  # RoPE of every head with the key and value heads put into the cache (bt_rope_put), against x cos + (x @ turn) sin
+  # in float64 on the same bf16 inputs, to a bf16 rounding; value heads (cos 1, sin 0) stored exactly.
+  from baretile_amd.models import llama
+  heads, kv, rows, size = 4, 2, 3, 16
+  c = llama.model(dim=heads * hd, heads=heads, kv=kv, layers=1, eps=1e-5, theta=10000.0, head_dim=hd)
+  cos, sin, turn = llama.rotary(c, size)
+  rng = np.random.default_rng(hd)
+  nh = heads + 2 * kv
+  x = B.bf16(rng.normal(0, 1, (rows, nh * hd)).astype(np.float32)).astype(np.float64)
+  places = [5, 0, 15]
+  cache = Tensor.zeros(rt, size, hd, batch=2 * kv)
+  q = Tensor.of(rt, x.astype(np.float32)).rope_put(Tensor.of(rt, cos[places]), Tensor.of(rt, sin[places]), cache,
+                                                     Tensor.of(rt, [places], "int32"), heads, kv)
+  xs = x.reshape(rows, nh, hd)
+  want = xs * cos[places].reshape(rows, nh, hd) + (xs @ turn) * sin[places].reshape(rows, nh, hd)
+  got_q = value(q).reshape(rows, heads, hd)
+  assert np.all(np.abs(got_q - want[:, :heads]) <= 2.0 ** -8 * np.abs(want[:, :heads]) + 1e-30)
+  got_c = value(cache).reshape(2 * kv, size, hd)
+  for i, p in enumerate(places):
+    assert np.all(np.abs(got_c[:kv, p] - want[i, heads:heads + kv]) <= 2.0 ** -8 * np.abs(want[i, heads:heads + kv]) + 1e-30)
+    assert np.array_equal(got_c[kv:, p], xs[i, heads + kv:])
+  others = [r for r in range(size) if r not in places]
+  assert not np.any(got_c[:, others])
