@@ -5,6 +5,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdarg>
+#include <vector>
 #include "../../include/baretile_amd.h"
 
 namespace bt {
@@ -33,7 +34,17 @@ struct Runtime {
   hipStream_t stream = nullptr;
   hipStream_t capture_origin = nullptr;  // non-null while bt_graph_begin has the stream in capture
   int closed = 0;
+  // Working memory of the library's own kernels (a matmul's B unpacked to bf16), used in stream order. It only
+  // grows, outside a capture; a smaller one it replaces is kept until the runtime closes, as a recorded graph may
+  // still use it.
+  void *scratch = nullptr;
+  size_t scratch_bytes = 0;
+  std::vector<void *> retired;
 };
+
+// The runtime's scratch of at least `bytes`, or null: inside a capture when it would have to grow (the caller then
+// takes a way that needs none), or when the device is out of memory.
+void *runtime_scratch(Runtime *r, size_t bytes);
 
 // Checks a runtime handle and makes its device current.
 int enter(bt_runtime *rt, Runtime **out);

@@ -557,7 +557,7 @@ __global__ void __launch_bounds__(256) skinny_kernel(const MatmulArgs args) {
 // The end of both GEMM kernels: the block's BM x BN starting values are in LDS (row stride ES bytes, ESZ bytes each:
 // bf16-rounded for a bf16 epilogue, fp32 otherwise). Without a program, and with rows of the output contiguous and
 // 16-byte aligned, each lane copies 16 bytes at a time; otherwise each value goes through the program and is stored.
-template <int DT, int BM, int BN, int ES, int ESZ>
+template <int DT, int BM, int BN, int ES, int ESZ, int NT = 256>
 __device__ __forceinline__ void gemm_epilogue(const MatmulArgs &args, const uint8_t *lds, int b, int m0, int n0,
                                               int tid) {
   const int rows = min(BM, args.m - m0), cols = min(BN, args.n - n0);
@@ -571,7 +571,7 @@ __device__ __forceinline__ void gemm_epilogue(const MatmulArgs &args, const uint
     constexpr int PER_ROW = BN * ESZ / 16;  // 16-byte pieces of a row
     uint8_t *out = (uint8_t *)args.out.ptr + (obase + (int64_t)m0 * args.out.sr + n0) * osz;
 #pragma unroll 1
-    for (int e = tid; e < rows * PER_ROW; e += 256) {
+    for (int e = tid; e < rows * PER_ROW; e += NT) {
       const int r = e / PER_ROW, piece = e % PER_ROW;
       *(uint4 *)(out + (int64_t)r * args.out.sr * osz + piece * 16) = *(const uint4 *)(lds + r * ES + piece * 16);
     }
@@ -582,7 +582,7 @@ __device__ __forceinline__ void gemm_epilogue(const MatmulArgs &args, const uint
   (void)obase;
   constexpr int GS = BN / SEG;
 #pragma unroll 1
-  for (int e = tid; e < rows * GS; e += 256) {
+  for (int e = tid; e < rows * GS; e += NT) {
     const int r = e / GS, c0 = e % GS * SEG;
     if (c0 >= cols) continue;
     const int n = min(SEG, cols - c0);
@@ -930,6 +930,136 @@ gemm2_kernel(const MatmulArgs args, int mblocks, int nblocks) {
   gemm_epilogue<DT, G::BM, G::BN, G::ES, G::ESZ>(args, lds, b, m0, n0, tid);
 }
 
+// ---- the prefill GEMM for bf16 B, K in steps of 32 ----------------------------------------------------------------
+// 256 x 256 blocks of 8 waves (2 x 4, 128 x 64 each), two waves a SIMD, so one wave's LDS reads run under the other's
+// matrix instructions. A step of 32 along K stages A (256 rows of 64 bytes, each row's four 16-byte columns at
+// c ^ ((r >> 1) & 3), so a fragment's 16 rows meet different banks) and B (16 tiles' half, 1 KB each in operand order)
+// in LDS through direct loads, S steps deep. One barrier a step: after it a wave issues its loads of step t + S - 1
+// into the stage that step t - 1 used, reads its fragments of step t and multiplies. The sums run in the order of the
+// other kernels (chunk by chunk, its lower 32 rows then its upper), so the result is the same bits. Needs K a multiple
+// of 32.
+template <int DT, int S>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks) {
+  constexpr int BM = 256, BN = 256, STAGE = 32768, A_BYTES = 16384, WM = 8, WN = 4;
+  constexpr int ESZ = DT == BT_FP32 ? 4 : 2, ES = BN * ESZ + 16, HALF = DT == BT_FP32 ? 128 : 256;
+  constexpr int LDS = S * STAGE > HALF * ES ? S * STAGE : HALF * ES;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS];
+  const Head h = early_head(args);
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, col = lane & 15;
+  const int wib = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wib >> 2, wn = wib & 3;
+  const int per = mblocks * nblocks, total = per * h.batch, full = total / 8 * 8;
+  int pid = blockIdx.x;
+  if (pid < full) pid = (pid % 8) * (full / 8) + pid / 8;  // neighbouring blocks on one XCD
+  const int b = pid / per;
+  pid %= per;
+  constexpr int GROUP = 8;  // blocks of a column of 8 block rows run together, sharing B's tiles in L2
+  const int width = GROUP * nblocks, first = pid / width * GROUP, gsz = min(mblocks - first, GROUP);
+  const int bm = first + pid % width % gsz, bn = pid % width / gsz;
+  const int m0 = bm * BM, n0 = bn * BN;
+
+  const uint16_t *abase = (const uint16_t *)h.a.ptr + operand_matrix(h.a, b) * h.a.sb;
+  const i32x4 ar = buffer_words(abase, (uint32_t)(((int64_t)(h.m - 1) * h.a.sr + h.k) * 2));
+  const uint8_t *bbase = h.b + (h.b_matrix_bytes ? b * h.b_matrix_bytes : 0);
+  const i32x4 br = buffer_words(bbase, (uint32_t)((int64_t)h.nruns * h.chunks * 2048));
+  constexpr uint32_t NOWHERE = 0xFFFFFFF0u;  // an offset past every buffer: the load writes zeros
+  // each lane's source for the wave's 2 A and 2 B loads of step 0 (a step adds 64 bytes to A's; B's move by half a
+  // tile, then to the next chunk)
+  uint32_t asrc[2], bsrc[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int li = wib + 8 * j;  // rows 16 li .. 16 li + 15 of A, tile li of B
+    const int r = 16 * li + lane / 4, c = (lane & 3) ^ ((r >> 1) & 3);
+    asrc[j] = m0 + r < h.m ? (uint32_t)(((int64_t)(m0 + r) * h.a.sr + 8 * c) * 2) : NOWHERE;
+    const int run = n0 / 16 + li;
+    bsrc[j] = run < h.nruns ? (uint32_t)((int64_t)run * h.chunks * 2048 + 32 * lane) : NOWHERE;
+  }
+  auto issue = [&](int t) {  // step t's loads into stage t % S
+    uint8_t *st = lds + (t % S) * STAGE;
+    const uint32_t ao = (uint32_t)t * 64, bo = (uint32_t)(t >> 1) * 2048 + (t & 1) * 16;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int li = wib + 8 * j;
+      lds_load16(ar, asrc[j] == NOWHERE ? NOWHERE : asrc[j] + ao, st + li * 1024);
+      lds_load16(br, bsrc[j] == NOWHERE ? NOWHERE : bsrc[j] + bo, st + A_BYTES + li * 1024);
+    }
+  };
+  f32x4 acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; i++)
+#pragma unroll
+    for (int j = 0; j < WN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int steps = h.k / 32;
+#pragma unroll
+  for (int t = 0; t < S - 1; t++)
+    if (t < steps) issue(t);
+  for (int t = 0; t < steps; t++) {
+    // step t landed once at most the later steps' loads are outstanding (fewer near the end)
+    if (t + S - 2 < steps) wait_vm<4 * (S - 2)>();
+    else wait_vm<0>();
+    __syncthreads();
+    if (t + S - 1 < steps) issue(t + S - 1);  // into the stage step t - 1 used
+    const uint8_t *st = lds + (t % S) * STAGE;
+    bf16x8 fa[WM], fb[WN];
+#pragma unroll
+    for (int i = 0; i < WM; i++) {
+      const int r = wm * 128 + 16 * i + col;
+      fa[i] = *(const bf16x8 *)(st + r * 64 + 16 * (g ^ ((r >> 1) & 3)));
+    }
+#pragma unroll
+    for (int j = 0; j < WN; j++) fb[j] = *(const bf16x8 *)(st + A_BYTES + (wn * 4 + j) * 1024 + lane * 16);
+#pragma unroll
+    for (int i = 0; i < WM; i++)
+#pragma unroll
+      for (int j = 0; j < WN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+  }
+  __syncthreads();  // every wave is done with the stages
+  // the tile through LDS to the epilogue: 256 rows (bf16) or 128 at a time (fp32)
+#pragma unroll
+  for (int half = 0; half < BM / HALF; half++) {
+    if (BM == HALF || wm == half) {
+#pragma unroll
+      for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int j = 0; j < WN; j++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            uint8_t *at = lds + ((BM == HALF ? wm * 128 : 0) + 16 * i + 4 * g + r) * ES + (wn * 64 + 16 * j + col) * ESZ;
+            if (DT == BT_FP32) *(float *)at = acc[i][j][r];
+            else *(uint16_t *)at = (uint16_t)bf16_packed(acc[i][j][r]);
+          }
+    }
+    __syncthreads();
+    gemm_epilogue<DT, HALF, BN, ES, ESZ, 512>(args, lds, b, m0 + half * HALF, n0, tid);
+    if (BM != HALF) __syncthreads();
+  }
+}
+
+// Block-float columns tiles -> bf16 columns tiles of the same values (the conversion gemm2 does in LDS), a thread a
+// lane of a tile: for the prefill GEMM, which takes bf16 B.
+template <int FMT>
+__global__ void __launch_bounds__(256) tiles_bf16_kernel(const uint8_t *src, uint8_t *dst, int64_t tiles) {
+  constexpr int TB = Tile<FMT>::bytes;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (t >= tiles) return;
+  const uint8_t *s = src + t * TB;
+  const uint4 ex = *(const uint4 *)(s + 16 * (lane >> 4));
+  bf16x8 h0, h1;
+  if (FMT == BT_BFP8) {
+    const uint4 q = *(const uint4 *)(s + 64 + 16 * lane);
+    h0 = q8_to_bf16<true>(make_uint2(q.x, q.y), make_uint2(ex.x, ex.y));
+    h1 = q8_to_bf16<true>(make_uint2(q.z, q.w), make_uint2(ex.z, ex.w));
+  } else {
+    const uint2 q = *(const uint2 *)(s + 64 + 8 * lane);
+    h0 = q4_to_bf16_scaled(q.x, make_uint2(ex.x, ex.y));
+    h1 = q4_to_bf16_scaled(q.y, make_uint2(ex.z, ex.w));
+  }
+  uint8_t *d = dst + t * 2048 + 32 * lane;
+  *(bf16x8 *)d = h0;
+  *(bf16x8 *)(d + 16) = h1;
+}
+
 // ---- one row with its prologue and residual (bt_matmul_row) ------------------------------------------------------
 // The decode GEMV of gemv_kernel for a single row whose A is made in the kernel: the block reads the prologue's inputs
 // straight into LDS (1 KB a load) before its first group of weight loads, works out a' (the norm, or silu(g) * u)
@@ -1203,12 +1333,20 @@ static void launch_gemm_dt(const MatmulArgs &args, hipStream_t s) {
   int best = 0;
   double score = -1.0;
   for (int o = 0; o < 3; o++) {
-    if (o < 2 && (args.m <= 128 || args.k % 64)) continue;  // K past whole chunks: the register-staged 128 x 128 kernel
-    if (o == 0 && DT == BT_FP32) continue;  // its fp32 epilogue values would not fit in LDS
+    const bool steps = FMT == BT_BF16 && DT == BT_BF16 && args.k % 32 == 0;  // gemm3: bf16 B and out, K in 32s
+    if (o < 2 && (args.m <= 128 || (args.k % 64 && !(o == 0 && steps)))) continue;  // else the register-staged kernel
+    if (o == 0 && DT == BT_FP32 && !steps) continue;  // gemm2's fp32 epilogue values would not fit in LDS
     const int64_t blocks = (int64_t)args.batch * ((args.m + opts[o].bm - 1) / opts[o].bm) * ((args.n + opts[o].bn - 1) / opts[o].bn);
     const int64_t rounds = (blocks + 255) / 256;
     const double sc = opts[o].eff * (double)blocks / (double)(rounds * 256);
     if (sc > score + 1e-9) score = sc, best = o;
+  }
+  if constexpr (FMT == BT_BF16 && DT == BT_BF16) {
+    if (best == 0 && args.k % 32 == 0) {
+      const int mb = (args.m + 255) / 256, nb = (args.n + 255) / 256;
+      gemm3_kernel<DT, 4><<<(unsigned)((int64_t)mb * nb * args.batch), 512, 0, s>>>(args, mb, nb);
+      return;
+    }
   }
   if constexpr (DT != BT_FP32) {
     if (best == 0) return launch_gemm<FMT, DT, 8, 8>(args, s);
@@ -1276,6 +1414,22 @@ extern "C" int bt_matmul(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_
   }
   args.n_inst = args.prog.n_inst;
   args.out = *out;
+  // A prefill-sized product with block-float B and bf16 out: B unpacked once into bf16 tiles in the runtime's scratch
+  // (the same values bit for bit), then the bf16 GEMM, whose pipeline the in-LDS conversion would stall
+  if (b_fmt != BT_BF16 && out->dtype == BT_BF16 && (!epilogue || epilogue->dtype != BT_FP32) && m >= 512 &&
+      k % 32 == 0 && a->sc == 1 && (int64_t)args.chunks * args.nruns * 2048 < (1ll << 32)) {
+    const int64_t tiles = (int64_t)args.chunks * args.nruns * (b_batch > 1 ? b_batch : 1);
+    void *bt16 = runtime_scratch(r, (size_t)tiles * 2048);
+    if (bt16) {
+      const unsigned blocks = (unsigned)((tiles + 3) / 4);
+      if (b_fmt == BT_BFP8) tiles_bf16_kernel<BT_BFP8><<<blocks, 256, 0, r->stream>>>(args.b, (uint8_t *)bt16, tiles);
+      else tiles_bf16_kernel<BT_BFP4><<<blocks, 256, 0, r->stream>>>(args.b, (uint8_t *)bt16, tiles);
+      BT_LAUNCHED("matmul");
+      args.b = (const uint8_t *)bt16;
+      args.b_matrix_bytes = b_batch > 1 ? (int64_t)args.chunks * args.nruns * 2048 : 0;
+      b_fmt = BT_BF16;
+    }
+  }
   if (b_fmt == BT_BF16) launch_skinny<BT_BF16>(args, r->stream);
   else if (b_fmt == BT_BFP8) launch_skinny<BT_BFP8>(args, r->stream);
   else launch_skinny<BT_BFP4>(args, r->stream);

@@ -122,10 +122,32 @@ int bt_close(bt_runtime *rt) {
   if (r->capture_origin) return fail(BT_ESTATE, "close a runtime after ending its graph capture");
   BT_HIP(hipStreamSynchronize(r->stream));
   BT_HIP(hipStreamDestroy(r->stream));
+  for (void *p : r->retired) (void)hipFree(p);
+  if (r->scratch) (void)hipFree(r->scratch);
   r->closed = 1;
   delete r;
   return BT_OK;
 }
+
+}  // extern "C"
+
+namespace bt {
+void *runtime_scratch(Runtime *r, size_t bytes) {
+  if (bytes <= r->scratch_bytes) return r->scratch;
+  if (r->capture_origin) return nullptr;
+  const size_t n = (bytes + (1u << 20) - 1) / (1u << 20) * (1u << 20);
+  void *p = nullptr;
+  if (hipMalloc(&p, n) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (r->scratch) r->retired.push_back(r->scratch);
+  r->scratch = p, r->scratch_bytes = n;
+  return p;
+}
+}  // namespace bt
+
+extern "C" {
 
 int bt_alloc(bt_runtime *rt, uint64_t bytes, uint64_t *addr) {
   Runtime *r;

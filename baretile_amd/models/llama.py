@@ -140,15 +140,15 @@ def rope(x, cos, sin, turn):
 
 
 def attention(h, p, c, rot, places, cache, rows, firsts=None):
-  """One block's attention over its cache (llama.py:132-172): qkv, RoPE written straight into the heads' row layout,
-  the new keys and values put into the cache at rows, then one attention kernel from each token's place (and, with
-  slots, from its slot's first row)."""
-  hd, rep, nh = head(c), c.heads // c.kv, c.heads + 2 * c.kv
+  """One block's attention over its cache (llama.py:132-172): qkv, then RoPE with the new keys and values put into
+  the cache at rows in one kernel (x cos + (x @ turn) sin, worked out in fp32 from the turn's pairs), then one
+  attention kernel from each token's place (and, with slots, from its slot's first row)."""
+  rep = c.heads // c.kv
   qkv = h.matmul(p["qkv_proj"])
-  qkv = rope(qkv.split(nh), rot[0].split(nh), rot[1].split(nh), rot[2]).merge()
-  heads = qkv.split(nh)
-  cache.put(rows, heads[c.heads:c.heads + 2 * c.kv, :, :])
-  q, k, v = heads[:c.heads, :, :], cache[:c.kv, :, :], cache[c.kv:, :, :]
+  n = qkv.rows
+  q = qkv.reshape(n, qkv.cols).rope_put(rot[0].reshape(n, rot[0].cols), rot[1].reshape(n, rot[1].cols),
+                                         cache, rows, c.heads, c.kv).split(c.heads)
+  k, v = cache[:c.kv, :, :], cache[c.kv:, :, :]
   o = q.attend(k.repeat_interleave(rep), v.repeat_interleave(rep), places, firsts=firsts)
   return o.merge().matmul(p["o_proj"], "fp32")
 
