@@ -473,3 +473,41 @@ extern "C" int bt_rope_put(bt_runtime *rt, const bt_rope_args *args) {
   BT_LAUNCHED("rope_put");
   return BT_OK;
 }
+
+namespace bt {
+
+// RMSNorm of rows: a block a row, two passes over it (the second from cache).
+__global__ void __launch_bounds__(256) rms_rows_kernel(const float *x, int64_t k, int64_t x_sr, const uint16_t *w,
+                                                       float eps, uint16_t *out, int64_t out_sr) {
+  __shared__ float part[4];
+  const int tid = threadIdx.x, lane = tid & 63, wib = tid >> 6;
+  const float *xr = x + (int64_t)blockIdx.x * x_sr;
+  uint16_t *o = out + (int64_t)blockIdx.x * out_sr;
+  float ss = 0.0f;
+  for (int64_t c = tid; c < k; c += 256) {
+    const float v = round_packed(xr[c]);
+    ss += v * v;
+  }
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) ss += __shfl_xor(ss, s, 64);
+  if (lane == 0) part[wib] = ss;
+  __syncthreads();
+  const float total = ((part[0] + part[1]) + part[2]) + part[3];
+  const float r = 1.0f / sqrtf(total / (float)k + eps);
+  for (int64_t c = tid; c < k; c += 256) o[c] = (uint16_t)bf16_packed(round_packed(xr[c]) * r * bf16_value(w[c]));
+}
+
+}  // namespace bt
+
+extern "C" int bt_rms_rows(bt_runtime *rt, uint64_t x, int64_t rows, int64_t k, int64_t x_sr, uint64_t w, float eps,
+                           uint64_t out, int64_t out_sr) {
+  using namespace bt;
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (!x || !w || !out) return fail(BT_EINVAL, "rms_rows needs x, w and out");
+  if (rows < 1 || rows >= (1ll << 31) || k < 1) return fail(BT_EINVAL, "rms_rows shape %lld x %lld", (long long)rows, (long long)k);
+  rms_rows_kernel<<<(unsigned)rows, 256, 0, r->stream>>>((const float *)(uintptr_t)x, k, x_sr, (const uint16_t *)(uintptr_t)w,
+                                                          eps, (uint16_t *)(uintptr_t)out, out_sr);
+  BT_LAUNCHED("rms_rows");
+  return BT_OK;
+}

@@ -938,12 +938,19 @@ gemm2_kernel(const MatmulArgs args, int mblocks, int nblocks) {
 // into the stage that step t - 1 used, reads its fragments of step t and multiplies. The sums run in the order of the
 // other kernels (chunk by chunk, its lower 32 rows then its upper), so the result is the same bits. Needs K a multiple
 // of 32.
-template <int DT, int S>
+// MODE 1 (RES): fp32 out written straight from the accumulators, plus (if res.ptr) the fp32 operand res at the same
+// element: the residual add that a program `out = value + x` asks for, without staging the tile.
+// MODE 2 (SWIGLU): B holds gate then up side by side (n = 2 f columns); a block takes 128 columns of each, at the
+// same place in both halves, and writes silu(gate) * up for those 128 columns (out: m x f, bf16): the gate and up
+// values rounded to bf16 as stored, silu(g) = g / (1 + exp(-g)) and the product in fp32, rounded once.
+constexpr int GEMM_PLAIN = 0, GEMM_RES = 1, GEMM_SWIGLU = 2;
+template <int DT, int S, int MODE = GEMM_PLAIN>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks) {
+gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand res) {
+  constexpr bool RES = MODE == GEMM_RES;
   constexpr int BM = 256, BN = 256, STAGE = 32768, A_BYTES = 16384, WM = 8, WN = 4;
   constexpr int ESZ = DT == BT_FP32 ? 4 : 2, ES = BN * ESZ + 16, HALF = DT == BT_FP32 ? 128 : 256;
-  constexpr int LDS = S * STAGE > HALF * ES ? S * STAGE : HALF * ES;
+  constexpr int LDS = RES ? S * STAGE : S * STAGE > HALF * ES ? S * STAGE : HALF * ES;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS];
   const Head h = early_head(args);
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, col = lane & 15;
@@ -971,8 +978,14 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks) {
     const int li = wib + 8 * j;  // rows 16 li .. 16 li + 15 of A, tile li of B
     const int r = 16 * li + lane / 4, c = (lane & 3) ^ ((r >> 1) & 3);
     asrc[j] = m0 + r < h.m ? (uint32_t)(((int64_t)(m0 + r) * h.a.sr + 8 * c) * 2) : NOWHERE;
-    const int run = n0 / 16 + li;
-    bsrc[j] = run < h.nruns ? (uint32_t)((int64_t)run * h.chunks * 2048 + 32 * lane) : NOWHERE;
+    int run = n0 / 16 + li;
+    bool in = run < h.nruns;
+    if (MODE == GEMM_SWIGLU) {  // tiles 0..7: gate columns from 128 bn, 8..15: the same up columns
+      const int f = h.n / 2, c0 = bn * 128 + 16 * (li & 7);
+      run = ((li < 8 ? 0 : f) + c0) / 16;
+      in = c0 < f;
+    }
+    bsrc[j] = in ? (uint32_t)((int64_t)run * h.chunks * 2048 + 32 * lane) : NOWHERE;
   }
   auto issue = [&](int t) {  // step t's loads into stage t % S
     uint8_t *st = lds + (t % S) * STAGE;
@@ -1013,6 +1026,26 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks) {
 #pragma unroll
       for (int j = 0; j < WN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
   }
+  if constexpr (RES) {
+    // lanes 0..15 of a row group write 16 neighbouring columns: 64 bytes
+    const int64_t ob = operand_matrix(h.out, b) * h.out.sb, rb = res.ptr ? operand_matrix(res, b) * res.sb : 0;
+#pragma unroll
+    for (int i = 0; i < WM; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int m = m0 + wm * 128 + 16 * i + 4 * g + r;
+        if (m >= h.m) continue;
+#pragma unroll
+        for (int j = 0; j < WN; j++) {
+          const int n = n0 + wn * 64 + 16 * j + col;
+          if (n >= h.n) continue;
+          float v = acc[i][j][r];
+          if (res.ptr) v += ((const float *)res.ptr)[rb + (int64_t)m * res.sr + (int64_t)n * res.sc];
+          ((float *)h.out.ptr)[ob + (int64_t)m * h.out.sr + (int64_t)n * h.out.sc] = v;
+        }
+      }
+    return;
+  }
   __syncthreads();  // every wave is done with the stages
   // the tile through LDS to the epilogue: 256 rows (bf16) or 128 at a time (fp32)
 #pragma unroll
@@ -1030,7 +1063,32 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks) {
           }
     }
     __syncthreads();
-    gemm_epilogue<DT, HALF, BN, ES, ESZ, 512>(args, lds, b, m0 + half * HALF, n0, tid);
+    if constexpr (MODE == GEMM_SWIGLU) {
+      // a thread 8 neighbouring columns of a row at a time: gate at column c of the tile, up at c + 128
+      const int f = h.n / 2, rows = min(BM, h.m - m0), c0 = bn * 128;
+      const int64_t ob = operand_matrix(h.out, b) * h.out.sb;
+#pragma unroll 1
+      for (int e = tid; e < rows * 16; e += 512) {
+        const int r = e >> 4, c = (e & 15) * 8;
+        if (c0 + c >= f) continue;
+        const uint4 gw = *(const uint4 *)(lds + r * ES + c * 2), uw = *(const uint4 *)(lds + r * ES + (128 + c) * 2);
+        const uint32_t gs[4] = {gw.x, gw.y, gw.z, gw.w}, us[4] = {uw.x, uw.y, uw.z, uw.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+          uint32_t w = 0;
+#pragma unroll
+          for (int hf = 0; hf < 2; hf++) {
+            const float gv = bf16_value(gs[v] >> (16 * hf) & 0xFFFFu), uv = bf16_value(us[v] >> (16 * hf) & 0xFFFFu);
+            w |= bf16_packed(gv / (1.0f + expf(-gv)) * uv) << (16 * hf);
+          }
+          o[v] = w;
+        }
+        *(uint4 *)((uint16_t *)h.out.ptr + ob + (int64_t)(m0 + r) * h.out.sr + c0 + c) = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    } else {
+      gemm_epilogue<DT, HALF, BN, ES, ESZ, 512>(args, lds, b, m0 + half * HALF, n0, tid);
+    }
     if (BM != HALF) __syncthreads();
   }
 }
@@ -1325,6 +1383,23 @@ static void launch_gemm(const MatmulArgs &args, hipStream_t s) {
   }
 }
 
+// Whether the product's epilogue is nothing or a residual add, out = value + x with x an fp32 operand, as gemm3's
+// direct fp32 store does it (the same fp32 add, so the same bits); res gets x (ptr 0 for none).
+static bool residual_program(const MatmulArgs &args, bt_operand *res) {
+  const bt_program &p = args.prog;
+  if (args.out.dtype != BT_FP32 || p.dtype != BT_FP32) return false;
+  if (p.n_inst == 0) {
+    if (res) *res = bt_operand{};
+    return true;
+  }
+  if (p.n_inst != 2 || p.n_inputs != 1 || p.in[0].dtype != BT_FP32) return false;
+  const bt_inst &ld = p.inst[0], &add = p.inst[1];
+  if (ld.op != BT_OP_LOAD || ld.a != 0 || ld.dst == 0 || add.op != BT_OP_ADD || p.result != add.dst) return false;
+  if (!((add.a == 0 && add.b == ld.dst) || (add.a == ld.dst && add.b == 0))) return false;
+  if (res) *res = p.in[0];
+  return true;
+}
+
 // The block shape for a GEMM: the largest tile whose grid still keeps the chip's 256 CUs busy through its last round.
 template <int FMT, int DT>
 static void launch_gemm_dt(const MatmulArgs &args, hipStream_t s) {
@@ -1333,7 +1408,8 @@ static void launch_gemm_dt(const MatmulArgs &args, hipStream_t s) {
   int best = 0;
   double score = -1.0;
   for (int o = 0; o < 3; o++) {
-    const bool steps = FMT == BT_BF16 && DT == BT_BF16 && args.k % 32 == 0;  // gemm3: bf16 B and out, K in 32s
+    // gemm3: bf16 B, K in 32s, bf16 out or fp32 out with at most a residual add
+    const bool steps = FMT == BT_BF16 && args.k % 32 == 0 && (DT == BT_BF16 || residual_program(args, nullptr));
     if (o < 2 && (args.m <= 128 || (args.k % 64 && !(o == 0 && steps)))) continue;  // else the register-staged kernel
     if (o == 0 && DT == BT_FP32 && !steps) continue;  // gemm2's fp32 epilogue values would not fit in LDS
     const int64_t blocks = (int64_t)args.batch * ((args.m + opts[o].bm - 1) / opts[o].bm) * ((args.n + opts[o].bn - 1) / opts[o].bn);
@@ -1341,11 +1417,20 @@ static void launch_gemm_dt(const MatmulArgs &args, hipStream_t s) {
     const double sc = opts[o].eff * (double)blocks / (double)(rounds * 256);
     if (sc > score + 1e-9) score = sc, best = o;
   }
-  if constexpr (FMT == BT_BF16 && DT == BT_BF16) {
+  if constexpr (FMT == BT_BF16) {
     if (best == 0 && args.k % 32 == 0) {
       const int mb = (args.m + 255) / 256, nb = (args.n + 255) / 256;
-      gemm3_kernel<DT, 4><<<(unsigned)((int64_t)mb * nb * args.batch), 512, 0, s>>>(args, mb, nb);
-      return;
+      const unsigned blocks = (unsigned)((int64_t)mb * nb * args.batch);
+      if constexpr (DT == BT_BF16) {
+        gemm3_kernel<DT, 4><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
+        return;
+      } else {
+        bt_operand res{};
+        if (residual_program(args, &res)) {
+          gemm3_kernel<DT, 4, GEMM_RES><<<blocks, 512, 0, s>>>(args, mb, nb, res);
+          return;
+        }
+      }
     }
   }
   if constexpr (DT != BT_FP32) {
@@ -1416,7 +1501,8 @@ extern "C" int bt_matmul(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_
   args.out = *out;
   // A prefill-sized product with block-float B and bf16 out: B unpacked once into bf16 tiles in the runtime's scratch
   // (the same values bit for bit), then the bf16 GEMM, whose pipeline the in-LDS conversion would stall
-  if (b_fmt != BT_BF16 && out->dtype == BT_BF16 && (!epilogue || epilogue->dtype != BT_FP32) && m >= 512 &&
+  const bool bf16_out = out->dtype == BT_BF16 && (!epilogue || epilogue->dtype != BT_FP32);
+  if (b_fmt != BT_BF16 && (bf16_out || residual_program(args, nullptr)) && m >= 512 &&
       k % 32 == 0 && a->sc == 1 && (int64_t)args.chunks * args.nruns * 2048 < (1ll << 32)) {
     const int64_t tiles = (int64_t)args.chunks * args.nruns * (b_batch > 1 ? b_batch : 1);
     void *bt16 = runtime_scratch(r, (size_t)tiles * 2048);
@@ -1495,5 +1581,48 @@ extern "C" int bt_matmul_row(bt_runtime *rt, const bt_row_args *args) {
   else if (x.b_fmt == BT_BFP8) launch_row<BT_BFP8>(ra, x.kind, r->stream);
   else launch_row<BT_BFP4>(ra, x.kind, r->stream);
   BT_LAUNCHED("matmul_row");
+  return BT_OK;
+}
+
+extern "C" int bt_matmul_swiglu(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_t b, int64_t m, int64_t k,
+                                int64_t n, const bt_operand *out) {
+  Runtime *r;
+  if (int st = enter(rt, &r)) return st;
+  if (!a || !a->ptr || !b || !out || !out->ptr) return fail(BT_EINVAL, "matmul_swiglu needs A, B and out");
+  if (b_fmt != BT_BF16 && b_fmt != BT_BFP8 && b_fmt != BT_BFP4) return fail(BT_EINVAL, "B format %d", b_fmt);
+  if (m < 1 || k < 32 || k % 32 || n < 32 || n % 32 || m >= (1 << 30) || k >= (1 << 30) || n >= (1 << 30))
+    return fail(BT_EINVAL, "matmul_swiglu shape %lld x %lld x %lld: k a multiple of 32, n of 32", (long long)m,
+                (long long)k, (long long)n);
+  if (a->dtype != BT_BF16 || a->sc != 1 || a->rep != 1 || a->cyc != 0 || a->ptr % 2)
+    return fail(BT_EINVAL, "matmul_swiglu's A is bf16 with contiguous rows");
+  if (out->dtype != BT_BF16 || out->sc != 1 || out->ptr % 16 || out->sr % 8 || out->rep != 1 || out->cyc != 0)
+    return fail(BT_EINVAL, "matmul_swiglu's out is bf16, 16-byte aligned contiguous rows");
+  if (b % 16) return fail(BT_EINVAL, "B's tiles must be 16-byte aligned");
+  if (((m - 1) * a->sr + k) * 2 >= (1ll << 32)) return fail(BT_EINVAL, "matmul_swiglu's A must lie within 4 GB");
+  MatmulArgs args;
+  args.a = *a;
+  args.b = (const uint8_t *)b;
+  args.b_matrix_bytes = 0;
+  args.batch = 1;
+  args.m = (int32_t)m, args.k = (int32_t)k, args.n = (int32_t)n;
+  args.chunks = (int32_t)((k + 63) / 64), args.nruns = (int32_t)(n / 16), args.mtiles = (int32_t)((m + 15) / 16);
+  args.prog = bt_program{};
+  args.prog.dtype = BT_BF16;
+  args.n_inst = 0;
+  args.out = *out;
+  if ((int64_t)args.chunks * args.nruns * 2048 >= (1ll << 32)) return fail(BT_EINVAL, "matmul_swiglu's B is too large");
+  if (b_fmt != BT_BF16) {  // unpacked once into bf16 tiles in the runtime's scratch
+    const int64_t tiles = (int64_t)args.chunks * args.nruns;
+    void *bt16 = runtime_scratch(r, (size_t)tiles * 2048);
+    if (!bt16) return fail(BT_ESTATE, "matmul_swiglu: no scratch for B's bf16 tiles (inside a capture, or out of memory)");
+    const unsigned blocks = (unsigned)((tiles + 3) / 4);
+    if (b_fmt == BT_BFP8) tiles_bf16_kernel<BT_BFP8><<<blocks, 256, 0, r->stream>>>(args.b, (uint8_t *)bt16, tiles);
+    else tiles_bf16_kernel<BT_BFP4><<<blocks, 256, 0, r->stream>>>(args.b, (uint8_t *)bt16, tiles);
+    BT_LAUNCHED("matmul_swiglu");
+    args.b = (const uint8_t *)bt16;
+  }
+  const int mb = (int)((m + 255) / 256), nb = (int)((n / 2 + 127) / 128);
+  gemm3_kernel<BT_BF16, 4, GEMM_SWIGLU><<<(unsigned)((int64_t)mb * nb), 512, 0, r->stream>>>(args, mb, nb, bt_operand{});
+  BT_LAUNCHED("matmul_swiglu");
   return BT_OK;
 }

@@ -129,7 +129,10 @@ def kv_cache(rt, c, size):
 
 
 def rms(x, w, c):
-  """RMSNorm of the stream rounded to bf16, scaled by w (llama.py:88-95)."""
+  """RMSNorm of the stream rounded to bf16, scaled by w (llama.py:88-95): for fp32 rows of one matrix, one kernel
+  (Tensor.rms_rows, in fp32, rounded once); otherwise the lazy graph, which rounds each step in bf16."""
+  if x.dtype == "fp32" and x.batch == 1 and w.dtype == "bf16" and len(x.shape) <= 3:
+    return x.rms_rows(w, c.eps)
   x = x.bfloat16()
   return x * ((x * x).mean(2) + c.eps).rsqrt() * w
 
@@ -149,13 +152,15 @@ def attention(h, p, c, rot, places, cache, rows, firsts=None):
   q = qkv.reshape(n, qkv.cols).rope_put(rot[0].reshape(n, rot[0].cols), rot[1].reshape(n, rot[1].cols),
                                          cache, rows, c.heads, c.kv).split(c.heads)
   k, v = cache[:c.kv, :, :], cache[c.kv:, :, :]
-  o = q.attend(k.repeat_interleave(rep), v.repeat_interleave(rep), places, firsts=firsts)
-  return o.merge().matmul(p["o_proj"], "fp32")
+  o = q.attend(k.repeat_interleave(rep), v.repeat_interleave(rep), places, firsts=firsts, merged=True)
+  return o.matmul(p["o_proj"], "fp32")
 
 
 def mlp(h, p):
   """SwiGLU: silu(h @ gate) * (h @ up), then down, with gate and up side by side (llama.py:174-183)."""
   m = p["down_proj"].rows
+  if h.rows >= 256 and h.batch == 1 and m % 16 == 0 and h.cols % 32 == 0:  # a block of tokens: SiLU-mul as the epilogue
+    return h.matmul_swiglu(p["gate_up_proj"]).matmul(p["down_proj"], "fp32")
   gate_up = h.matmul(p["gate_up_proj"])
   return (gate_up[:, :m].silu() * gate_up[:, m:]).matmul(p["down_proj"], "fp32")
 

@@ -680,6 +680,35 @@ class Tensor:
     self.rt.run("matmul_row", "matmul_row", ctypes.byref(args))
     return out
 
+  def rms_rows(self, w, eps=1e-5):
+    """RMSNorm of each row of self (fp32, a batch of one) scaled by w (bf16), in one kernel a row apart
+    (llama.py:88-95; bt_rms_rows): x rounded to bf16, then x / sqrt(mean(x^2) + eps) * w in fp32, rounded once."""
+    x, wt = self.realize(), w.realize()
+    if not (x.dtype == "fp32" and x.batch == 1 and x.sc == 1 and x.rep == 1 and not x.cyc and x.layout == "plain"):
+      raise ValueError(f"rms_rows needs fp32 rows of one matrix: {x.shape} {x.dtype}")
+    if not (wt.dtype == "bf16" and wt._contiguous() and wt.batch * wt.rows * wt.cols == x.cols):
+      raise ValueError(f"rms_rows needs bf16 weights, one for each column: {wt.shape} {wt.dtype}")
+    out = Tensor(self.rt, x.rows, x.cols)
+    out.lead = self.lead
+    self.rt.run("rms_rows", "rms_rows", x.addr, x.rows, x.cols, x.sr, wt.addr, eps, out.addr, out.sr)
+    return out
+
+  def matmul_swiglu(self, w):
+    """silu(self @ gate) * (self @ up) for w holding gate then up side by side (llama.py:174-183), in one kernel: the
+    SiLU-mul runs as the product's epilogue (bt_matmul_swiglu). self is bf16 rows of one matrix; returns bf16
+    (rows, w.cols / 2)."""
+    if not isinstance(w, Tensor) or w.rt is not self.rt or w.layout != "columns" or w.batch != 1:
+      raise ValueError("matmul_swiglu needs w laid out by columns, batch 1, on the same runtime")
+    a = self.realize()
+    if not (a.dtype == "bf16" and a.batch == 1 and a.sc == 1 and a.rep == 1 and not a.cyc and a.cols == w.rows):
+      raise ValueError(f"matmul_swiglu needs bf16 rows of one matrix, {w.rows} wide: {a.shape} {a.dtype}")
+    out = Tensor(self.rt, a.rows, w.cols // 2)
+    out.lead = self.lead
+    self.rt.run("matmul_swiglu", "matmul_swiglu", ctypes.byref(_lib.operand(a.addr, "bf16", 0, a.sr)),
+                _lib.DTYPES[w.dtype], w.storage.addr, a.rows, a.cols, w.cols,
+                ctypes.byref(_lib.operand(out.addr, "bf16", 0, out.sr)))
+    return out
+
   def rope_put(self, cos, sin, cache, places, heads, kv):
     """RoPE of each head of self (bf16 rows of heads + 2 kv heads) in fp32, the query heads returned as a
     (rows, heads * d) tensor and the key and value heads put into cache (2 kv, size, d) at places (an int32 row),
@@ -703,11 +732,11 @@ class Tensor:
     return q
 
   # ---- attention, rows in and out
-  def attend(self, k, v, places, window=0, fidelity=None, parts=None, firsts=None):
+  def attend(self, k, v, places, window=0, fidelity=None, parts=None, firsts=None, merged=False):
     """softmax(self @ k^T + mask) @ v, with the mask from each query row's place (and window), in one kernel
     (tensor.py:797-841). k and v may be repeat views (grouped-query attention). RoPE scales q beforehand. firsts, an
     int32 column like places, raises each row's first visible key: sequences that share one cache in regions of their
-    own (llama.py:293-318's slots)."""
+    own (llama.py:293-318's slots). merged writes the result as merge() of it, (rows, heads * width)."""
     if len(self.shape) > 3: raise ValueError(f"attend takes three dimensions, not {self.shape}")
     if window < 0 or parts is not None and parts <= 0: raise ValueError("attention needs a nonnegative window and positive parts")
     if not (self.dtype == "bf16" and k.dtype == v.dtype == "bf16" and self.batch == k.batch == v.batch):
@@ -724,10 +753,15 @@ class Tensor:
     if k.sc != 1: k = k.contiguous()
     if v.sc != 1: v = v.contiguous()
     if not places._contiguous(): places = places.contiguous()
-    out = Tensor(self.rt, q.rows, q.cols, batch=q.batch)
-    out.lead = self.lead
+    if merged:  # the heads side by side in each row, as merge() would give them
+      out = Tensor(self.rt, q.rows, q.batch * q.cols)
+      osh, osr = q.cols, out.sr
+    else:
+      out = Tensor(self.rt, q.rows, q.cols, batch=q.batch)
+      out.lead = self.lead
+      osh, osr = out.sb, out.sr
     args = _lib.AttentionArgs(q.addr, k.addr, v.addr, out.addr, places.addr, q.sb, q.sr, k.sb, k.sr, v.sb, v.sr,
-                              out.sb, out.sr, q.rows if places.batch > 1 else 0, q.batch, rep, q.rows, k.rows, q.cols,
+                              osh, osr, q.rows if places.batch > 1 else 0, q.batch, rep, q.rows, k.rows, q.cols,
                               window, parts or 0, 0, 0, 0)
     if firsts is not None:
       if not (firsts.rows == self.rows and firsts.batch in (1, self.batch) and firsts.cols == 1 and firsts.dtype == "int32"):

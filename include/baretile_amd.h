@@ -198,6 +198,19 @@ typedef struct {
 } bt_row_args;
 int bt_matmul_row(bt_runtime *rt, const bt_row_args *args);
 
+/* The MLP's first product for a block of tokens with silu(gate) * up as its epilogue (llama.py:174-183; the fused
+ * SiLU-mul epilogue fused_kernel gives the prefill's gate_up): B holds gate then up side by side (n = 2 f columns,
+ * n a multiple of 32) and out[i, j] = bf16(silu(g) * u) for j < f, with g, u the products at columns j and f + j
+ * rounded to bf16 as stored, silu(g) = g / (1 + exp(-g)), in fp32. A is bf16 with contiguous rows, k a multiple of
+ * 32; out is bf16 with contiguous, 16-byte aligned rows. A block-float B is unpacked to bf16 in the runtime's scratch
+ * first (BT_ESTATE inside a capture when that scratch would have to grow). */
+int bt_matmul_swiglu(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_t b, int64_t m, int64_t k, int64_t n,
+                     const bt_operand *out);
+/* RMSNorm of a block of token rows (llama.py:88-95): out[r, c] = bf16(x * s * w[c]) with x = bf16(x[r, c]) (half
+ * up), s = 1 / sqrt(mean over c of x^2 + eps), in fp32; x fp32, w and out bf16, row strides in elements. */
+int bt_rms_rows(bt_runtime *rt, uint64_t x, int64_t rows, int64_t k, int64_t x_sr, uint64_t w, float eps, uint64_t out,
+                int64_t out_sr);
+
 /* RoPE and the cache put of a decode step (llama.py:132-160: rope, then the key and value heads put at the tokens'
  * places). For each token i < rows and head h < heads + 2 kv of qkv (bf16, element (i, h, j) at
  * i * qkv_sr + h * head_dim + j):

@@ -333,3 +333,44 @@ def test_rope_put(rt, hd):
     assert np.array_equal(got_c[kv:, p], xs[i, heads + kv:])
   others = [r for r in range(size) if r not in places]
   assert not np.any(got_c[:, others])
+
+
+def test_rms_rows(rt):
+  # RMSNorm of rows in one kernel (bt_rms_rows) against NumPy on the documented formula, to a bf16 rounding
+  rng = np.random.default_rng(7)
+  x = rng.normal(0, 3, (37, 1000)).astype(np.float32)
+  w = B.bf16(rng.normal(1, 0.1, 1000).astype(np.float32)).astype(np.float32)
+  xb = packed(x).astype(np.float32)
+  r = np.float32(1) / np.sqrt(np.mean(xb.astype(np.float64) ** 2, 1, keepdims=True).astype(np.float32) + np.float32(1e-5))
+  want = xb * r * w
+  got = value(Tensor.of(rt, x, "fp32").rms_rows(Tensor.of(rt, w[None]), 1e-5)).reshape(37, 1000)
+  assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-30)
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bfp4"])
+def test_matmul_swiglu(rt, fmt):
+  # silu(x @ gate) * (x @ up) with the SiLU-mul as the product's epilogue (bt_matmul_swiglu): against the unfused
+  # product's gate and up values (bit for bit the same sums) put through the documented formula, to a bf16 rounding
+  m, k, f = 300, 256, 272
+  rng = np.random.default_rng(11)
+  x = Tensor.of(rt, rng.normal(0, 1, (m, k)).astype(np.float32))
+  wt, _ = _weights(rt, k, 2 * f, fmt, 3)
+  gu = value(x.matmul(wt)).reshape(m, 2 * f)  # bf16, rounded as stored
+  g, u = gu[:, :f].astype(np.float32), gu[:, f:].astype(np.float32)
+  want = g / (np.float32(1) + np.exp(-g)) * u
+  out = x.matmul_swiglu(wt)
+  assert out.shape[-2:] == (m, f)
+  got = value(out).reshape(m, f)
+  assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-30)
+
+
+def test_attend_merged_equals_merge(rt):
+  rng = np.random.default_rng(5)
+  q = Tensor.of(rt, rng.normal(0, 1, (4, 3, 64)).astype(np.float32))
+  k = Tensor.of(rt, rng.normal(0, 1, (2, 8, 64)).astype(np.float32))
+  v = Tensor.of(rt, rng.normal(0, 1, (2, 8, 64)).astype(np.float32))
+  places = Tensor.of(rt, [[2], [5], [7]], "int32")
+  a = q.attend(k.repeat_interleave(2), v.repeat_interleave(2), places).merge()
+  b = q.attend(k.repeat_interleave(2), v.repeat_interleave(2), places, merged=True)
+  assert a.shape[-2:] == b.shape[-2:] == (3, 256)
+  assert a.tobytes() == b.tobytes()
