@@ -336,80 +336,302 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(const bt_attenti
   for (int c = 0; c < HD / 16; c++) out[c0 + 16 * c] = (uint16_t)bf16_packed(o[c] * inv);
 }
 
-// Prefill: block (kvh, 4 consecutive tiles); wave w takes tile 4 * blockIdx + w. Each block of 64 keys and values is
-// loaded once by the whole block into LDS (two buffers), then every wave whose tile sees part of it folds it in.
+// Prefill. A block is 4 waves and 128 consecutive pairs of one key head; wave w takes pairs 32w .. 32w + 31 of them as
+// two groups of 16 (the 16-pair tile of the scheme above), so every K and V fragment it reads from LDS feeds two
+// matrix instructions. The block's keys come through LDS 64 at a time, double-buffered, one barrier a step: K as it is
+// stored (row-major), V transposed (V^T[dim][key]) so that P V's value operand, 8 keys of one column, is two 8-byte
+// reads. The row sums come from the matrix cores too: P times a column of ones, accumulated and rescaled like O.
+// Masks are applied only on blocks of keys that some pair of the wave sees in part, and the running output is
+// rescaled only when some pair's maximum moved. p is rounded to bf16 to nearest even (v_cvt_pk_bf16_f32).
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_rne(float lo, float hi) {
+  const bf16x2 r = __builtin_convertvector((f32x2){lo, hi}, bf16x2);
+  return *(const uint32_t *)&r;
+}
+
+template <int HD> struct Group {
+  f32x4 o[HD / 16];  // lane (g, n): pairs 4g + i, columns 16c + n
+  f32x4 l;           // row sums of the same pairs (every column holds them)
+  float m;           // pair n's reference maximum, in log2 units: p = 2^(s log2(e) - m)
+};
+
+// The reference maximum moves only when a block's maximum passes it by more than 2^8 (then O and l are rescaled), so
+// p stays below 256 and most blocks need no rescale; O / l is the same for any reference.
+constexpr float LAZY = 8.0f;
+
+// mask: some pair of the wave sees only part of the block (wave-uniform). A block no pair sees leaves the state as
+// it was (every p is 0). mid() runs once the scores are made: the caller's loads of a later block, issued where fewer
+// registers are live.
+template <int HD, typename Mid>
+__device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf)[2][HD / 32], const uint16_t *kl,
+                                           const uint16_t *vt, int kb, const int (&lo)[2], const int (&hi)[2],
+                                           int lane, bool mask, Mid mid) {
+  constexpr int KS = HD + 8, VT = KB + 8;
+  constexpr float L2E = 1.4426950408889634f;
+  const int g = lane >> 4, n = lane & 15;
+  f32x4 s[2][4];
+  bf16x8 kf[2][HD / 32];  // two key tiles' K fragments, the next read while the current one is multiplied
+#pragma unroll
+  for (int kk = 0; kk < HD / 32; kk++) kf[0][kk] = *(const bf16x8 *)(kl + n * KS + 32 * kk + 8 * g);
+#pragma unroll
+  for (int kt = 0; kt < 4; kt++) {
+    if (kt < 3) {
+#pragma unroll
+      for (int kk = 0; kk < HD / 32; kk++)
+        kf[(kt + 1) & 1][kk] = *(const bf16x8 *)(kl + (16 * (kt + 1) + n) * KS + 32 * kk + 8 * g);
+    }
+    s[0][kt] = s[1][kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kk = 0; kk < HD / 32; kk++) {
+      s[0][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kt & 1][kk], qf[0][kk], s[0][kt], 0, 0, 0);
+      s[1][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kt & 1][kk], qf[1][kk], s[1][kt], 0, 0, 0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  mid();
+  __builtin_amdgcn_sched_barrier(0);
+  uint32_t pb[2][4][2];  // [group][key tile][pair of keys]: packed p
+  bool need = false;
+  float mnew[2];
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    if (mask) {
+#pragma unroll
+      for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int j = kb + 16 * kt + 4 * g + i;
+          if (j < lo[q] || j > hi[q]) s[q][kt][i] = -__builtin_inff();
+        }
+    }
+    float mx = s[q][0][0];
+#pragma unroll
+    for (int e = 1; e < 16; e += 2) mx = fmaxf(fmaxf(mx, s[q][e / 4][e % 4]), s[q][(e + 1) / 4 % 4][(e + 1) % 4]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m2 = mx * L2E;
+    const bool up = m2 > gr[q].m + LAZY;  // false for a pair with no visible key in the block
+    need |= up;
+    mnew[q] = up ? m2 : gr[q].m;
+  }
+  if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+      // 1 where the reference stays (also -inf to -inf), 0 from no reference to the first
+      const float scale = mnew[q] == gr[q].m ? 1.0f : __builtin_amdgcn_exp2f(gr[q].m - mnew[q]);
+      gr[q].m = mnew[q];
+      float sc[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) sc[i] = __shfl(scale, 4 * g + i, 64);
+#pragma unroll
+      for (int c = 0; c < HD / 16; c++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) gr[q].o[c][i] *= sc[i];
+#pragma unroll
+      for (int i = 0; i < 4; i++) gr[q].l[i] *= sc[i];
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const float nb = gr[q].m == -__builtin_inff() ? 0.0f : -gr[q].m;  // no key seen yet: every s is -inf, p 0
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++) {
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[q][kt][i], L2E, nb));
+      pb[q][kt][0] = pack_rne(p[0], p[1]);
+      pb[q][kt][1] = pack_rne(p[2], p[3]);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const bf16x8 ones = as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++) {
+    bf16x8 pa[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++)
+      pa[q] = as_bf16x8(pb[q][2 * ks][0], pb[q][2 * ks][1], pb[q][2 * ks + 1][0], pb[q][2 * ks + 1][1]);
+    const uint16_t *col = vt + n * VT + 32 * ks + 4 * g;
+#pragma unroll
+    for (int c = 0; c < HD / 16; c++) {
+      const uint2 a0 = *(const uint2 *)(col + 16 * c * VT);       // keys 4g .. 4g + 3 of the step
+      const uint2 a1 = *(const uint2 *)(col + 16 * c * VT + 16);  // keys 16 + 4g .. 16 + 4g + 3
+      const bf16x8 vf = as_bf16x8(a0.x, a0.y, a1.x, a1.y);
+      gr[0].o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], vf, gr[0].o[c], 0, 0, 0);
+      gr[1].o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], vf, gr[1].o[c], 0, 0, 0);
+    }
+    gr[0].l = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], ones, gr[0].l, 0, 0, 0);
+    gr[1].l = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], ones, gr[1].l, 0, 0, 0);
+  }
+}
+
+// Prefill. A block is 8 waves and 128 consecutive pairs of one key head. Waves w and w + 4 take the same 32 pairs,
+// as two groups of 16 (the tile of the scheme above), so every K and V fragment a wave reads from LDS feeds two matrix
+// instructions; the two halves of the block (waves 0-3, 4-7) split the keys, half h folding blocks 2t + h of 64 keys,
+// each half with its own double-buffered LDS stage, one barrier a step. K is staged as stored (row-major), V transposed
+// (V^T[dim][key]) so that P V's value operand, 8 keys of one column, is two 8-byte reads. The row sums come from the
+// matrix cores too: P times a column of ones, accumulated and rescaled like O. At the end half 1 hands its state to
+// half 0 through LDS, which joins the two (rescaling both to the larger maximum) and stores the output.
+//
+// Blocks go heaviest first (the last rows of the causal triangle see the most keys): block u takes key head u % kvhs
+// and row block rblocks - 1 - u / kvhs.
 template <int HD>
-__global__ void __launch_bounds__(256) attention_prefill_kernel(const bt_attention_args a, int tiles) {
-  constexpr int VS = HD + 8, BUF = KB * VS;  // halfwords of one 64-row block
-  constexpr int PER = KB * HD / 8 / 256;      // 16-byte words of K (and of V) each thread moves per block
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][BUF];  // [buffer][K, V]
+__global__ void __launch_bounds__(512, 1) attention_prefill_kernel(const bt_attention_args a, int rblocks, int kvhs) {
+  constexpr int KS = HD + 8, VT = KB + 8, KBUF = KB * KS, STG = KBUF + HD * VT;  // halfwords of one stage
+  constexpr int KW = KB * HD / 8 / 256;  // 16-byte words of K each thread of a half moves per block
+  constexpr int KPT = HD / 32;           // keys of V each thread of a half moves per block (8 columns of each)
+  constexpr int NKG = KB / KPT;          // threads along the keys of V
+  constexpr int XF = 2 * (HD / 4 + 8);   // floats per lane a wave hands over: O, l and the maxima of both groups
+  static_assert(4 * XF * 64 * 4 <= 4 * STG * 2, "the hand-over fits in the stages");
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][STG];  // [half][stage]
   __shared__ int range[4][2];
-  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-  const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int blocks4 = (tiles + 3) / 4;
-  const int kvh = blockIdx.x / blocks4, t = (blockIdx.x % blocks4) * 4 + wib;
-  const Pair pr = pair_of(a, kvh, 16 * t + n);
-  bf16x8 qf[HD / 32];
-  load_q<HD>(a, pr, lane, qf);
-  int lo, hi;
-  tile_range(pr, lo, hi);
-  if (lane == 0) range[wib][0] = lo, range[wib][1] = hi;
+  const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+  const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), wq = wib & 3, hf = wib >> 2;
+  const int th = threadIdx.x & 255;
+  const int u = blockIdx.x, kvh = u % kvhs, rb = rblocks - 1 - u / kvhs;
+  const int base = 128 * rb + 32 * wq;
+  Pair pr[2];
+  bf16x8 qf[2][HD / 32];
+  int lo[2], hi[2];
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    pr[q] = pair_of(a, kvh, base + 16 * q + n);
+    load_q<HD>(a, pr[q], lane, qf[q]);
+    lo[q] = pr[q].lo, hi[q] = pr[q].hi;
+  }
+  // the wave's range (union over its pairs) and the keys every valid pair sees (intersection)
+  int wlo = 0x7FFFFFFF, whi = -1, alo = -1, ahi = 0x7FFFFFFF;
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    if (pr[q].lo <= pr[q].hi) wlo = min(wlo, pr[q].lo), whi = max(whi, pr[q].hi);
+    if (pr[q].valid) alo = max(alo, pr[q].lo), ahi = min(ahi, pr[q].hi);
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) {
+    wlo = min(wlo, __shfl_xor(wlo, o, 64)), whi = max(whi, __shfl_xor(whi, o, 64));
+    alo = max(alo, __shfl_xor(alo, o, 64)), ahi = min(ahi, __shfl_xor(ahi, o, 64));
+  }
+  wlo = __builtin_amdgcn_readfirstlane(wlo), whi = __builtin_amdgcn_readfirstlane(whi);
+  alo = __builtin_amdgcn_readfirstlane(alo), ahi = __builtin_amdgcn_readfirstlane(ahi);
+  if (lane == 0 && hf == 0) range[wq][0] = wlo, range[wq][1] = whi;
   __syncthreads();
   int blo = 0x7FFFFFFF, bhi = -1;
 #pragma unroll
   for (int w = 0; w < 4; w++) blo = min(blo, range[w][0]), bhi = max(bhi, range[w][1]);
-  State<HD> st;
-  st.m = -__builtin_inff(), st.l = 0.0f;
+  blo = __builtin_amdgcn_readfirstlane(blo), bhi = __builtin_amdgcn_readfirstlane(bhi);
+  Group<HD> gr[2];
 #pragma unroll
-  for (int c = 0; c < HD / 16; c++) st.o[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  const uint32_t kbytes = (uint32_t)(((int64_t)(a.keys - 1) * a.k_sr + HD) * 2);
-  const uint32_t vbytes = (uint32_t)(((int64_t)(a.keys - 1) * a.v_sr + HD) * 2);
+  for (int q = 0; q < 2; q++) {
+    gr[q].m = -__builtin_inff();
+    gr[q].l = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < HD / 16; c++) gr[q].o[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  // rows past the block's last visible key read as zeros (they are masked, and may never have been written): the
+  // buffers end there
+  const uint32_t kbytes = bhi < 0 ? 0 : (uint32_t)(((int64_t)bhi * a.k_sr + HD) * 2);
+  const uint32_t vbytes = bhi < 0 ? 0 : (uint32_t)(((int64_t)bhi * a.v_sr + HD) * 2);
   const __amdgpu_buffer_rsrc_t kr = attn_rsrc((const uint16_t *)a.k + (int64_t)kvh * a.k_sh, kbytes);
   const __amdgpu_buffer_rsrc_t vr = attn_rsrc((const uint16_t *)a.v + (int64_t)kvh * a.v_sh, vbytes);
-  // thread's words: row (tid / (HD / 8)) + (256 * 8 / HD) * i, column (tid % (HD / 8)) * 8
-  const int tr = threadIdx.x / (HD / 8), tc = threadIdx.x % (HD / 8) * 8;
-  constexpr int RSTEP = 256 * 8 / HD;
-  uint4 kreg[PER], vreg[PER];
+  // K: thread's words at row kr0 + (256 / (HD / 8)) i, column kc; V: keys KPT kg .. + KPT - 1, columns 8 dg .. + 7.
+  const int kr0 = th / (HD / 8), kc = th % (HD / 8) * 8;
+  constexpr int KSTEP = 256 / (HD / 8);
+  const int kg = th % NKG, dg = th / NKG;
+  // byte offsets from a block's first row: the thread's first word, then uniform steps
+  const uint32_t koff = (uint32_t)(((int64_t)kr0 * a.k_sr + kc) * 2), voff = (uint32_t)(((int64_t)KPT * kg * a.v_sr + 8 * dg) * 2);
+  const uint32_t kstep = (uint32_t)(KSTEP * a.k_sr * 2), vstep = (uint32_t)(a.v_sr * 2);
+  uint4 kreg[KW], vreg[KPT];
   auto fetch = [&](int kb) {
+    const uint32_t kbo = (uint32_t)((int64_t)kb * a.k_sr * 2), vbo = (uint32_t)((int64_t)kb * a.v_sr * 2);
 #pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const auto k = __builtin_amdgcn_raw_buffer_load_b128(kr, (uint32_t)(((int64_t)(kb + tr + RSTEP * i) * a.k_sr + tc) * 2), 0, 0);
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(vr, (uint32_t)(((int64_t)(kb + tr + RSTEP * i) * a.v_sr + tc) * 2), 0, 0);
-      kreg[i] = make_uint4(k[0], k[1], k[2], k[3]);
+    for (int i = 0; i < KW; i++) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(kr, koff + (kbo + i * kstep), 0, 0);
+      kreg[i] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+#pragma unroll
+    for (int i = 0; i < KPT; i++) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(vr, voff + (vbo + i * vstep), 0, 0);
       vreg[i] = make_uint4(v[0], v[1], v[2], v[3]);
     }
   };
-  const int first = blo & ~(KB - 1);
-  if (first <= bhi) fetch(first);
-  int buf = 0;
-  for (int kb = first; kb <= bhi; kb += KB, buf ^= 1) {
-    uint16_t *kl = lds[buf][0], *vl = lds[buf][1];
+  auto stash = [&](uint16_t *stage) {
+    uint16_t *kl = stage, *vt = stage + KBUF;
 #pragma unroll
-    for (int i = 0; i < PER; i++) {
-      *(uint4 *)(kl + (tr + RSTEP * i) * VS + tc) = kreg[i];
-      *(uint4 *)(vl + (tr + RSTEP * i) * VS + tc) = vreg[i];
+    for (int i = 0; i < KW; i++) *(uint4 *)(kl + (kr0 + KSTEP * i) * KS + kc) = kreg[i];
+#pragma unroll
+    for (int d = 0; d < 8; d++) {
+      uint32_t w[KPT / 2];
+#pragma unroll
+      for (int i = 0; i < KPT; i += 2) {
+        const uint32_t x = ((const uint32_t *)&vreg[i])[d / 2], y = ((const uint32_t *)&vreg[i + 1])[d / 2];
+        w[i / 2] = d & 1 ? (x >> 16) | (y & 0xFFFF0000u) : (x & 0xFFFFu) | (y << 16);
+      }
+      uint16_t *at = vt + (8 * dg + d) * VT + KPT * kg;
+      if constexpr (KPT == 4) *(uint2 *)at = make_uint2(w[0], w[1]);
+      else *(uint32_t *)at = w[0];
     }
+  };
+  // half hf folds blocks first + 64 (2t + hf), t < steps, the same count for both halves (a block past the last
+  // visible key reads as zeros and is masked whole)
+  const int first = blo & ~(KB - 1);
+  const int nblk = bhi >= first ? (bhi - first) / KB + 1 : 0, steps = (nblk + 1) / 2;
+  uint16_t *const st0 = lds[hf][0], *const st1 = lds[hf][1];
+  if (steps > 0) {
+    fetch(first + KB * hf);
+    stash(st0);
+  }
+  __syncthreads();
+  auto step = [&](int t, uint16_t *cur, uint16_t *nxt) {
+    const int kb = first + KB * (2 * t + hf);
+    const bool more = t + 1 < steps, mask = kb < alo || kb + KB - 1 > ahi;
+    fold_pairs<HD>(gr, qf, cur, cur + KBUF, kb, lo, hi, lane, mask, [&] {
+      if (more) fetch(kb + 2 * KB);
+    });
+    if (more) stash(nxt);
     __syncthreads();
-    if (kb + KB <= bhi) fetch(kb + KB);
-    if (kb <= hi && kb + KB - 1 >= lo) {
-      bf16x8 kf[4][HD / 32];
+  };
+  for (int t = 0; t < steps; t++) step(t, t & 1 ? st1 : st0, t & 1 ? st0 : st1);
+  // half 1 hands over O, l and its maxima (row i's, for the rows this lane holds); half 0 joins and stores
+  float *xs = (float *)&lds[0][0][0] + wq * XF * 64 + lane;
+  float md[2][4];
 #pragma unroll
-      for (int kt = 0; kt < 4; kt++)
+  for (int q = 0; q < 2; q++)
 #pragma unroll
-        for (int kk = 0; kk < HD / 32; kk++) kf[kt][kk] = *(const bf16x8 *)(kl + (16 * kt + n) * VS + 32 * kk + 8 * g);
-      fold_block<HD, VS>(st, kf, qf, vl, kb, pr, lane);
+    for (int i = 0; i < 4; i++) md[q][i] = __shfl(gr[q].m, 4 * g + i, 64);
+  if (hf == 1) {
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+      float *x = xs + q * (HD / 4 + 8) * 64;
+#pragma unroll
+      for (int c = 0; c < HD / 16; c++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) x[(4 * c + i) * 64] = gr[q].o[c][i];
+#pragma unroll
+      for (int i = 0; i < 4; i++) x[(HD / 4 + i) * 64] = gr[q].l[i], x[(HD / 4 + 4 + i) * 64] = md[q][i];
     }
   }
-  // the wave's own tile is complete: normalize and store its valid pairs (lane l: pairs 4g + i, column 16c + n)
-  const float inv_n = st.l > 0.0f ? 1.0f / st.l : 0.0f;
+  __syncthreads();
+  if (hf == 1) return;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const float inv = __shfl(inv_n, 4 * g + i, 64);
-    const Pair pi = pair_of(a, kvh, 16 * t + 4 * g + i);
-    if (!pi.valid) continue;
-    uint16_t *out = (uint16_t *)a.out + pi.o;
+  for (int q = 0; q < 2; q++) {
+    const float *x = xs + q * (HD / 4 + 8) * 64;
 #pragma unroll
-    for (int c = 0; c < HD / 16; c++) out[16 * c + n] = (uint16_t)bf16_packed(st.o[c][i] * inv);
+    for (int i = 0; i < 4; i++) {
+      const int p = base + 16 * q + 4 * g + i;
+      if (p >= a.rep * a.rows) continue;
+      const float m1 = x[(HD / 4 + 4 + i) * 64], m0 = md[q][i], M = fmaxf(m0, m1);
+      const float w0 = m0 == M ? 1.0f : __builtin_amdgcn_exp2f(m0 - M);
+      const float w1 = m1 == M ? 1.0f : __builtin_amdgcn_exp2f(m1 - M);
+      const float l = gr[q].l[i] * w0 + x[(HD / 4 + i) * 64] * w1;
+      const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+      const int h = p % a.rep, r = p / a.rep, e = kvh * a.rep + h;
+      uint16_t *out = (uint16_t *)a.out + (int64_t)e * a.o_sh + (int64_t)r * a.o_sr;
+#pragma unroll
+      for (int c = 0; c < HD / 16; c++)
+        out[16 * c + n] = (uint16_t)bf16_packed((gr[q].o[c][i] * w0 + x[(4 * c + i) * 64] * w1) * inv);
+    }
   }
 }
 
@@ -430,8 +652,8 @@ static int plan_attention(const bt_attention_args *a, AttnPlan *p) {
       a->v_sh % 8)
     return fail(BT_EINVAL, "attention needs q, k and v rows on 16-byte boundaries");
   if (a->places_sh != 0 && a->places_sh != a->rows) return fail(BT_EINVAL, "places' head stride is 0 or rows");
-  if (((int64_t)(a->keys - 1) * std::max(a->k_sr, a->v_sr) + a->head_dim) * 2 >= (1ll << 32))
-    return fail(BT_EINVAL, "a key head's rows must span less than 4 GiB");
+  if (((int64_t)(a->keys + KB) * std::max(a->k_sr, a->v_sr) + a->head_dim) * 2 >= (1ll << 32))
+    return fail(BT_EINVAL, "a key head's rows (and 64 more) must span less than 4 GiB");
   if (a->firsts && a->firsts % 4) return fail(BT_EINVAL, "attention's firsts must be int32-aligned");
   if (a->firsts && a->firsts_sh != 0 && a->firsts_sh != a->rows) return fail(BT_EINVAL, "firsts' head stride is 0 or rows");
   const int kvh = a->heads / a->rep, np = a->rep * a->rows;
@@ -485,9 +707,10 @@ int bt_attention(bt_runtime *rt, const bt_attention_args *a) {
       BT_LAUNCHED("attention combine");
     }
   } else {
-    const unsigned blocks = (unsigned)(kvh * ((p.tiles + 3) / 4));
-    if (a->head_dim == 64) attention_prefill_kernel<64><<<blocks, 256, 0, r->stream>>>(*a, p.tiles);
-    else attention_prefill_kernel<128><<<blocks, 256, 0, r->stream>>>(*a, p.tiles);
+    const int rblocks = (a->rep * a->rows + 127) / 128;
+    const unsigned blocks = (unsigned)(kvh * rblocks);
+    if (a->head_dim == 64) attention_prefill_kernel<64><<<blocks, 512, 0, r->stream>>>(*a, rblocks, kvh);
+    else attention_prefill_kernel<128><<<blocks, 512, 0, r->stream>>>(*a, rblocks, kvh);
     BT_LAUNCHED("attention");
   }
   return BT_OK;
