@@ -1341,12 +1341,20 @@ static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bo
       else launch_sliced(gemv_kernel<FMT, DT, 4, 12, true, false, false>, args, units, 1, 12 * SB, 0, s);
     }
   } else if (vec && fits && ((int64_t)31 * args.a.sr + 2 * (int64_t)args.k + 1024) * 2 < (1ll << 32)) {
-    // two 16-row tiles a wave from 17 rows up; the waves of a run side by side
-    const bool two = args.m > 16;
+    // two 16-row tiles a wave from 17 rows up; the waves of a run side by side. A short K (3-12 chunks) with many
+    // rows: one tile a wave and all of K in one group of loads, so each wave makes one trip to memory.
+    const bool one_trip = args.m > 16 && args.chunks > 2 && args.chunks <= 12;
+    const bool two = args.m > 16 && !one_trip;
     const int64_t units = (int64_t)args.batch * args.nruns * (two ? (args.mtiles + 1) / 2 : args.mtiles);
-    const int sl = choose_slices(units, args.chunks);
-    const bool lean = args.batch == 1 && !args.n_inst && sl == 1 && !two;
-    if (two && args.chunks <= 2) {  // short K (a head's width): groups of 2
+    const int sl = one_trip ? 1 : choose_slices(units, args.chunks);
+    const bool lean = args.batch == 1 && !args.n_inst && sl == 1 && !two && !one_trip;
+    if (one_trip && args.chunks % 9 == 0) {
+      if (args.n_inst) launch_sliced(skinny_vec_kernel<FMT, DT, 9, false, true, 1, false>, args, units, 1, 0, 0, s);
+      else launch_sliced(skinny_vec_kernel<FMT, DT, 9, false, false, 1, false>, args, units, 1, 0, 0, s);
+    } else if (one_trip) {
+      if (args.n_inst) launch_sliced(skinny_vec_kernel<FMT, DT, 12, false, true, 1, false>, args, units, 1, 0, 0, s);
+      else launch_sliced(skinny_vec_kernel<FMT, DT, 12, false, false, 1, false>, args, units, 1, 0, 0, s);
+    } else if (two && args.chunks <= 2) {  // short K (a head's width): groups of 2
       if (args.n_inst) launch_sliced(skinny_vec_kernel<FMT, DT, 2, false, true, 2, true>, args, units, sl, 0, 2048, s);
       else launch_sliced(skinny_vec_kernel<FMT, DT, 2, false, false, 2, true>, args, units, sl, 0, 2048, s);
     } else if (two) {
@@ -1446,8 +1454,13 @@ static void launch_skinny(const MatmulArgs &args, hipStream_t s) {
   const unsigned blocks = (unsigned)((waves + 3) / 4);
   const bt_operand &a = args.a;
   const bool vec = a.sc == 1 && a.sr % 8 == 0 && a.ptr % 16 == 0 && a.sb % 8 == 0 && args.k % 8 == 0;
-  // many rows: the tiled GEMM, when A's rows are contiguous, aligned and within reach of one buffer resource
-  const bool gemm = vec && args.m > 64 && ((int64_t)(args.m - 1) * a.sr + args.k) * 2 < (1ll << 32);
+  // many rows: the tiled GEMM, when A's rows are contiguous, aligned and within reach of one buffer resource. Up to
+  // 256 rows, a product whose 128 x 128 blocks would fill fewer than half the CUs stays on the skinny kernel: its
+  // waves (32 rows by one 16-column run each) spread the work over many more CUs, and the extra reads of B (one per
+  // 32 rows) come from L2.
+  const int64_t gemm_blocks = (int64_t)args.batch * ((args.m + 127) / 128) * ((args.n + 127) / 128);
+  const bool gemm = vec && args.m > 64 && !(args.m <= 256 && gemm_blocks < 128) &&
+                    ((int64_t)(args.m - 1) * a.sr + args.k) * 2 < (1ll << 32);
   if (gemm) {
     if (args.prog.dtype == BT_FP32) launch_gemm_dt<FMT, BT_FP32>(args, s);
     else launch_gemm_dt<FMT, BT_BF16>(args, s);
