@@ -62,7 +62,8 @@ class RopeArgs(ctypes.Structure):  # bt_rope_args
   _fields_ = [("qkv", c_uint64), ("cos", c_uint64), ("sin", c_uint64), ("q", c_uint64), ("cache", c_uint64),
               ("places", c_uint64), ("qkv_sr", c_int64), ("cs_sr", c_int64), ("q_sr", c_int64), ("cache_sh", c_int64),
               ("cache_sr", c_int64), ("cache_rows", c_int64), ("rows", c_int32), ("heads", c_int32), ("kv", c_int32),
-              ("head_dim", c_int32)]
+              ("head_dim", c_int32), ("vcache", c_uint64), ("cache_tsh", c_int64), ("one_place", c_int32),
+              ("pad_", c_int32)]
 
 
 RT = c_void_p

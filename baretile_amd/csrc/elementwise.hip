@@ -448,9 +448,12 @@ __global__ void __launch_bounds__(256) rope_put_kernel(const bt_rope_args a) {
   if (hh < a.heads) {
     dst = (uint16_t *)(uintptr_t)a.q + (int64_t)i * a.q_sr + (int64_t)hh * a.head_dim;
   } else {
-    const int place = ((const int32_t *)(uintptr_t)a.places)[i];
+    const int place = ((const int32_t *)(uintptr_t)a.places)[a.one_place ? 0 : i];
     if (place < 0 || place >= a.cache_rows) return;
-    dst = (uint16_t *)(uintptr_t)a.cache + (int64_t)(hh - a.heads) * a.cache_sh + (int64_t)place * a.cache_sr;
+    const int hk = hh - a.heads;
+    const bool own = a.vcache && hk >= a.kv;  // a value head with a cache of its own
+    dst = (uint16_t *)(uintptr_t)(own ? a.vcache : a.cache) + (int64_t)(own ? hk - a.kv : hk) * a.cache_sh +
+          (int64_t)i * a.cache_tsh + (int64_t)place * a.cache_sr;
   }
   dst[j] = (uint16_t)bf16_packed(y1);
   dst[j + half] = (uint16_t)bf16_packed(y2);

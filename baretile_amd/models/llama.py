@@ -204,16 +204,13 @@ def slots_layer(x, p, c, rot, keys, values, place):
   """One block for a batch of slots, each with its own cache and one new token, all at one place: the batched decode
   of llama.forward(slots=...) (llama.py:293-354). x is (1, S, dim), the stream of the S slots; keys and values are
   (S * kv, size, head) bf16, slot s's key heads at s * kv .. s * kv + kv - 1; rot holds the tables at the place for
-  each slot's row; place is a (1, 1) int32 row. The slots' query heads become S * heads attention heads of one row."""
-  S, hd, nh, rep = x.rows, head(c), c.heads + 2 * c.kv, c.heads // c.kv
+  each slot's row; place is a (1, 1) int32 row. The slots' query heads become S * heads attention heads of one row.
+  RoPE and the cache puts run as one kernel (bt_rope_put), in fp32 with one rounding."""
+  S, hd, rep = x.rows, head(c), c.heads // c.kv
   h = rms(x, p["input_layernorm"], c)
-  qkv = rope(h.matmul(p["qkv_proj"]).split(nh), rot[0].split(nh), rot[1].split(nh), rot[2]).merge()
-  q = qkv[:, :, :c.heads * hd].contiguous().reshape(S * c.heads, 1, hd)
-  k = qkv[:, :, c.heads * hd:(c.heads + c.kv) * hd].contiguous().reshape(S * c.kv, 1, hd)
-  v = qkv[:, :, (c.heads + c.kv) * hd:].contiguous().reshape(S * c.kv, 1, hd)
-  keys.put(place, k)
-  values.put(place, v)
-  o = q.attend(keys.repeat_interleave(rep), values.repeat_interleave(rep), place.reshape(1, 1, 1))
+  q = h.matmul(p["qkv_proj"]).rope_put(rot[0], rot[1], keys, place, c.heads, c.kv, values=values)
+  o = q.reshape(S * c.heads, 1, hd).attend(keys.repeat_interleave(rep), values.repeat_interleave(rep),
+                                           place.reshape(1, 1, 1))
   x = (x + o.reshape(1, S, c.heads * hd).matmul(p["o_proj"], "fp32")).realize()
   return (x + mlp(rms(x, p["post_attention_layernorm"], c), p)).realize()
 

@@ -709,25 +709,33 @@ class Tensor:
                 ctypes.byref(_lib.operand(out.addr, "bf16", 0, out.sr)))
     return out
 
-  def rope_put(self, cos, sin, cache, places, heads, kv):
+  def rope_put(self, cos, sin, cache, places, heads, kv, values=None):
     """RoPE of each head of self (bf16 rows of heads + 2 kv heads) in fp32, the query heads returned as a
-    (rows, heads * d) tensor and the key and value heads put into cache (2 kv, size, d) at places (an int32 row),
-    in one kernel (llama.py:132-160; bt_rope_put). cos and sin are bf16 rows laid out as self; the tables turn x
+    (rows, heads * d) tensor and the key and value heads put into cache (2 kv, size, d) at places (an int32 row, one
+    place for each row or one for all), in one kernel (llama.py:132-160; bt_rope_put). With values, cache and values
+    are separate key and value caches of rows * kv heads, row i's at i * kv .. i * kv + kv - 1 (the slots of
+    llama.py:293-354, each with a cache of its own). cos and sin are bf16 rows laid out as self; the tables turn x
     into x cos + (-x2, x1) sin, which leaves the value heads (cos 1, sin 0) as they are."""
     x, c, sn, cc, pl = self.realize(), cos.realize(), sin.realize(), cache.realize(), places.realize()
+    vc = values.realize() if values is not None else None
     nh = heads + 2 * kv
     if not (x.dtype == c.dtype == sn.dtype == cc.dtype == "bf16" and x.batch == 1 and x.cols % nh == 0 and x.sc == 1):
       raise ValueError(f"rope_put needs bf16 rows of {nh} heads and bf16 tables: {x.shape} {x.dtype}")
     d = x.cols // nh
     if not (c.shape[-2:] == sn.shape[-2:] == (x.rows, x.cols) and c.sc == 1 and sn.sc == 1 and c.sr == sn.sr):
       raise ValueError(f"rope_put needs cos and sin laid out as the rows: {c.shape} {sn.shape} for {x.shape}")
-    if not (cc.batch == 2 * kv and cc.cols == d and cc.sc == 1 and cc.rep == 1 and not cc.cyc and cc.layout == "plain"):
+    plain = lambda t: t.cols == d and t.sc == 1 and t.rep == 1 and not t.cyc and t.layout == "plain"
+    if vc is None and not (cc.batch == 2 * kv and plain(cc)):
       raise ValueError(f"rope_put needs a plain ({2 * kv}, size, {d}) cache: {cc.shape}")
-    if not (pl.dtype == "int32" and pl.batch * pl.rows == 1 and pl.cols == x.rows and pl.sc == 1):
-      raise ValueError("rope_put needs places as an int32 row, one for each row")
+    if vc is not None and not (cc.batch == vc.batch == x.rows * kv and vc.dtype == "bf16" and plain(cc) and plain(vc)
+                               and cc.rows == vc.rows and cc.sb == vc.sb and cc.sr == vc.sr):
+      raise ValueError(f"rope_put needs plain ({x.rows * kv}, size, {d}) key and value caches: {cc.shape}")
+    if not (pl.dtype == "int32" and pl.batch * pl.rows == 1 and pl.cols in (1, x.rows) and pl.sc == 1):
+      raise ValueError("rope_put needs places as an int32 row, one for each row or one for all")
     q = Tensor(self.rt, x.rows, heads * d)
     args = _lib.RopeArgs(x.addr, c.addr, sn.addr, q.addr, cc.addr, pl.addr, x.sr, c.sr, q.sr, cc.sb, cc.sr, cc.rows,
-                         x.rows, heads, kv, d)
+                         x.rows, heads, kv, d, vc.addr if vc is not None else 0, kv * cc.sb if vc is not None else 0,
+                         int(pl.cols == 1 and x.rows > 1), 0)
     self.rt.run("rope_put", "rope_put", ctypes.byref(args))
     return q
 

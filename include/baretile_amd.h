@@ -216,13 +216,19 @@ int bt_rms_rows(bt_runtime *rt, uint64_t x, int64_t rows, int64_t k, int64_t x_s
  * i * qkv_sr + h * head_dim + j):
  *   y = bf16(x[j] * cos[j] + t[j] * sin[j]), t[j] = -x[j + d/2] for j < d/2 and x[j - d/2] after (d = head_dim),
  * in fp32, with cos and sin bf16 rows laid out as qkv (row stride cs_sr). Query heads are written to q (as qkv, row
- * stride q_sr); key and value heads to cache[h - heads, places[i], :] (bf16, element strides cache_sh, cache_sr),
- * a place outside [0, cache_rows) skipped. RoPE's tables carry the query scale, and cos 1, sin 0 for the value
- * heads, so a value head is stored as it is. */
+ * stride q_sr); key and value heads to cache[h - heads, place, :] (bf16, element strides cache_sh, cache_sr),
+ * place = places[i] (places[0] for every token when one_place is nonzero), a place outside [0, cache_rows) skipped.
+ * With vcache nonzero the value heads go to vcache[h - heads - kv, place, :] instead (laid out as cache), and
+ * cache_tsh adds i * cache_tsh elements to token i's rows in both caches: a batch of sequences with caches of their
+ * own side by side (the slots of llama.py:293-354, slot i's key heads at i * kv). RoPE's tables carry the query
+ * scale, and cos 1, sin 0 for the value heads, so a value head is stored as it is. */
 typedef struct {
   uint64_t qkv, cos, sin, q, cache, places;
   int64_t qkv_sr, cs_sr, q_sr, cache_sh, cache_sr, cache_rows;
   int32_t rows, heads, kv, head_dim;
+  uint64_t vcache;     /* 0: value heads at cache heads kv .. 2 kv - 1 */
+  int64_t cache_tsh;   /* elements between tokens' caches, or 0 */
+  int32_t one_place, pad_;
 } bt_rope_args;
 int bt_rope_put(bt_runtime *rt, const bt_rope_args *args);
 

@@ -101,6 +101,8 @@ def test_slots_layer_matches_each_slot_in_numpy(rt):
     want = L.layer(x[s:s + 1], L.block(ref, 0), c, (ref["cos"][[place]], ref["sin"][[place]], ref["turn"]), mask,
                    cache, [place])[0]
     assert np.abs(got[s] - want).max() <= 0.03 * np.abs(want - x[s]).max(), (s, np.abs(got[s] - want).max())
-  # the new keys landed in each slot's rows of the caches
-  new_k = np.array(keys.tolist()).reshape(S * kv, size, hd)[:, place]
-  assert np.abs(new_k).max() > 0
+    # the slot's new key and value rows, as the NumPy block put them into its cache
+    new_k = np.array(keys.tolist()).reshape(S * kv, size, hd)[s * kv:(s + 1) * kv, place]
+    new_v = np.array(values.tolist()).reshape(S * kv, size, hd)[s * kv:(s + 1) * kv, place]
+    for got_r, want_r in ((new_k, cache[:kv, place]), (new_v, cache[kv:, place])):
+      assert np.abs(got_r - want_r).max() <= 0.03 * np.abs(want_r).max(), (s, np.abs(got_r - want_r).max())

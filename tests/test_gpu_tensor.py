@@ -335,6 +335,32 @@ def test_rope_put(rt, hd):
   assert not np.any(got_c[:, others])
 
 
+def test_rope_put_slots(rt):
+  # the slots' layout: separate key and value caches of rows * kv heads, row i's heads at i * kv, one place for all
+  # rows (llama.slots_layer); against the same float64 RoPE, and nothing else written
+  from baretile_amd.models import llama
+  heads, kv, rows, size, hd = 4, 2, 5, 12, 64
+  c = llama.model(dim=heads * hd, heads=heads, kv=kv, layers=1, eps=1e-5, theta=10000.0, head_dim=hd)
+  cos, sin, turn = llama.rotary(c, size)
+  rng = np.random.default_rng(11)
+  nh, place = heads + 2 * kv, 7
+  x = B.bf16(rng.normal(0, 1, (rows, nh * hd)).astype(np.float32)).astype(np.float64)
+  keys, vals = Tensor.zeros(rt, size, hd, batch=rows * kv), Tensor.zeros(rt, size, hd, batch=rows * kv)
+  q = Tensor.of(rt, x.astype(np.float32)).rope_put(Tensor.of(rt, cos[[place] * rows]), Tensor.of(rt, sin[[place] * rows]),
+                                                     keys, Tensor.of(rt, [[place]], "int32"), heads, kv, values=vals)
+  xs = x.reshape(rows, nh, hd)
+  cs, sn = cos[[place] * rows].reshape(rows, nh, hd), sin[[place] * rows].reshape(rows, nh, hd)
+  want = xs * cs + (xs @ turn) * sn
+  assert np.all(np.abs(value(q).reshape(rows, heads, hd) - want[:, :heads]) <= 2.0 ** -8 * np.abs(want[:, :heads]) + 1e-30)
+  got_k, got_v = value(keys).reshape(rows * kv, size, hd), value(vals).reshape(rows * kv, size, hd)
+  for i in range(rows):
+    wk = want[i, heads:heads + kv]
+    assert np.all(np.abs(got_k[i * kv:(i + 1) * kv, place] - wk) <= 2.0 ** -8 * np.abs(wk) + 1e-30)
+    assert np.array_equal(got_v[i * kv:(i + 1) * kv, place], xs[i, heads + kv:])
+  others = [r for r in range(size) if r != place]
+  assert not np.any(got_k[:, others]) and not np.any(got_v[:, others])
+
+
 def test_rms_rows(rt):
   # RMSNorm of rows in one kernel (bt_rms_rows) against NumPy on the documented formula, to a bf16 rounding
   rng = np.random.default_rng(7)
