@@ -442,8 +442,9 @@ __global__ void __launch_bounds__(256) rope_put_kernel(const bt_rope_args a) {
   const uint16_t *cs = (const uint16_t *)(uintptr_t)a.cos + (int64_t)i * a.cs_sr + (int64_t)hh * a.head_dim;
   const uint16_t *sn = (const uint16_t *)(uintptr_t)a.sin + (int64_t)i * a.cs_sr + (int64_t)hh * a.head_dim;
   const float x1 = bf16_value(x[j]), x2 = bf16_value(x[j + half]);
-  const float y1 = x1 * bf16_value(cs[j]) - x2 * bf16_value(sn[j]);
-  const float y2 = x2 * bf16_value(cs[j + half]) + x1 * bf16_value(sn[j + half]);
+  // products and sums rounded one by one (no fused multiply-add), as the qkv product's fused RoPE computes them
+  const float y1 = __fsub_rn(__fmul_rn(x1, bf16_value(cs[j])), __fmul_rn(x2, bf16_value(sn[j])));
+  const float y2 = __fadd_rn(__fmul_rn(x2, bf16_value(cs[j + half])), __fmul_rn(x1, bf16_value(sn[j + half])));
   uint16_t *dst;
   if (hh < a.heads) {
     dst = (uint16_t *)(uintptr_t)a.q + (int64_t)i * a.q_sr + (int64_t)hh * a.head_dim;

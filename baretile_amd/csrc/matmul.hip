@@ -789,6 +789,15 @@ __device__ __forceinline__ void lds_load16(const i32x4 &rsrc, uint32_t voff, con
                : "memory", "m0");
 }
 
+// 4 bytes a lane from the buffer at voff into LDS at lds + 4 * lane, as lds_load16.
+__device__ __forceinline__ void lds_load4(const i32x4 &rsrc, uint32_t voff, const void *lds) {
+  const uint32_t at = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds;
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(at)
+               : "memory", "m0");
+}
+
 // Waits until at most N vector memory loads of this wave are outstanding. Assembly too: the compiler would drop a
 // wait for loads it doesn't know of.
 template <int N> __device__ __forceinline__ void wait_vm() {
@@ -1123,7 +1132,7 @@ __global__ void __launch_bounds__(256) tiles_bf16_kernel(const uint8_t *src, uin
 // straight into LDS (1 KB a load) before its first group of weight loads, works out a' (the norm, or silu(g) * u)
 // into an LDS row while those loads are in flight, and each wave then takes its A values from that row. The residual
 // is added to the fp32 sum before the store.
-struct RowArgs {  // 68 bytes: brought by the kernel's first round of scalar loads
+struct RowArgs {  // 72 bytes: brought by the kernel's first round of scalar loads
   const uint8_t *b;
   const uint8_t *a;
   const uint8_t *norm;
@@ -1131,8 +1140,19 @@ struct RowArgs {  // 68 bytes: brought by the kernel's first round of scalar loa
   uint8_t *out;
   int32_t chunks, nruns, k, n, out_dtype;
   float eps;
-  int32_t slices;  // waves a run (1, 2 or 4), each a slice of K, summed in slice order
+  int32_t slices;     // waves a run (1, 2 or 4), each a slice of K, summed in slice order
+  int32_t half_runs;  // with RoPE: 16-column runs in half a head
 };
+
+// RoPE of the product and the cache put (bt_rope_put's fields, read in the epilogue only).
+struct RopeTail {
+  const uint16_t *cos, *sin;
+  const int32_t *places;
+  uint16_t *q, *cache, *vcache;
+  int64_t cache_sh, cache_sr, cache_tsh, cache_rows;
+  int32_t heads, kv, head_dim;
+};
+
 
 // The block's inputs a 1 KB load: lane l's 16 bytes of piece p at p * 1024 + 16 l, into LDS at lds + p * 1024; the
 // buffer's range gives zeros past its end. Each wave takes every fourth piece.
@@ -1142,8 +1162,12 @@ __device__ __forceinline__ int row_pieces(const i32x4 &rsrc, int pieces, uint8_t
   return issued;
 }
 
-template <int FMT, int G, int KIND>
-__global__ void __launch_bounds__(256) gemv_row_kernel(const RowArgs args) {
+//
+// With ROPE the product is rounded to bf16 (as bt_matmul_row stores it) and goes through RoPE and the cache put as
+// bt_rope_put does, in one kernel: a block's waves take the runs of RoPE's partner columns (j and j + d/2 of a head)
+// side by side and swap their values through LDS.
+template <int FMT, int G, int KIND, bool ROPE>
+__global__ void __launch_bounds__(256) gemv_row_kernel(const RowArgs args, const RopeTail rp) {
   constexpr int TB = Tile<FMT>::bytes;
   // weights loaded with the default cache policy: a decode step reads the same matrices every token, and a small
   // model's stay in the 256 MB Infinity Cache between steps
@@ -1151,10 +1175,17 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(const RowArgs args) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t dyn[];
   const RowArgs h = args;
   asm volatile("" ::"s"(h.b), "s"(h.a), "s"(h.norm), "s"(h.res), "s"(h.out), "s"(h.chunks), "s"(h.nruns), "s"(h.k),
-               "s"(h.n), "s"(h.out_dtype), "s"(h.eps), "s"(h.slices));
+               "s"(h.n), "s"(h.out_dtype), "s"(h.eps), "s"(h.slices), "s"(h.half_runs));
   const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
   const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int S = h.slices, sl = wib % S, run = blockIdx.x * (4 / S) + wib / S;
+  const int S = h.slices, sl = wib % S, lr = wib / S;  // lr: the wave's run among the block's 4 / S
+  // with RoPE, runs u and u + half_runs of a head side by side: block run i is of pair blockIdx.x * (2 / S) + i / 2
+  auto run_of = [&](int i) -> int {
+    if (!ROPE) return (int)blockIdx.x * (4 / S) + i;
+    const int pair = blockIdx.x * (2 / S) + i / 2, hr = h.half_runs;
+    return pair / hr * 2 * hr + pair % hr + (i & 1) * hr;
+  };
+  const int run = run_of(lr);
   const int chunks = h.chunks, K = h.k, kpad = chunks * 64;
   const bool valid = run < h.nruns;
   const int per = (chunks + S - 1) / S, c_begin = min(chunks, sl * per), mine = min(chunks, c_begin + per) - c_begin;
@@ -1167,6 +1198,17 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(const RowArgs args) {
   uint16_t *slots = arow + prow * 512 + wib * G * 64;
   float *red = (float *)(arow + prow * 512 + 4 * G * 64);
   f32x4 *part = (f32x4 *)(red + 4);  // the slices' partial tiles
+  float *xch = (float *)(part + 256);  // with RoPE: each run's 16 values, as stored (bf16)
+  uint8_t *rtab = (uint8_t *)(xch + 64);  // with RoPE: cos and sin of the block's runs (1 KB each), the place
+  // 0. RoPE's tables for the block's runs and the token's place: lane i of wave 0 (cos) or 1 (sin) brings columns
+  // 8 (i % 2) .. + 7 of block run i / 2; lane 0 of wave 2 the place
+  if (ROPE && wib < 2) {
+    const int i = lane / 2, rn = run_of(i);
+    const uint32_t off = lane < 2 * (4 / S) && rn < h.nruns ? (uint32_t)(rn * 16 + (lane & 1) * 8) * 2 : 0xFFFFFFF0u;
+    lds_load16(buffer_words(wib == 0 ? rp.cos : rp.sin, (uint32_t)h.n * 2), off, rtab + wib * 1024);
+  } else if (ROPE && wib == 2) {
+    lds_load4(buffer_words(rp.places, 4), lane == 0 ? 0u : 0xFFFFFFF0u, rtab + 2048);
+  }
   // 1. the prologue's inputs into LDS
   if (KIND == BT_ROW_PLAIN) {
     row_pieces(buffer_words(h.a, (uint32_t)K * 2), prow, (uint8_t *)arow, wib, lane);
@@ -1237,7 +1279,7 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(const RowArgs args) {
     }
     __syncthreads();
   }
-  if (!valid && S == 1) return;
+  if (!ROPE && !valid && S == 1) return;  // with RoPE every wave reaches the swap's barrier (an invalid one sums zeros)
   // 5. the product over this wave's slice, chunk by chunk as gemv_kernel's
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int c0 = 0; c0 < mine; c0 += G) {
@@ -1273,8 +1315,31 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(const RowArgs args) {
   if (S > 1) {
     if (sl != 0) part[wib * 64 + lane] = acc;
     __syncthreads();
-    if (sl != 0 || !valid) return;
-    for (int j = 1; j < S; j++) acc += part[(wib + j) * 64 + lane];
+    if (!ROPE && (sl != 0 || !valid)) return;
+    if (sl == 0)
+      for (int j = 1; j < S; j++) acc += part[(wib + j) * 64 + lane];
+  }
+  if (ROPE) {
+    if (sl == 0 && g == 0) xch[lr * 16 + col] = round_packed(acc[0]);
+    __syncthreads();
+    const int n = run * 16 + col;
+    if (sl != 0 || g != 0 || !valid) return;
+    const float x = xch[lr * 16 + col], xp = xch[(lr ^ 1) * 16 + col];
+    const float cs = bf16_value(((const uint16_t *)rtab)[lr * 16 + col]);
+    const float sn = bf16_value(((const uint16_t *)rtab)[512 + lr * 16 + col]);
+    const float y = lr & 1 ? __fadd_rn(__fmul_rn(x, cs), __fmul_rn(xp, sn)) : __fsub_rn(__fmul_rn(x, cs), __fmul_rn(xp, sn));
+    const int head = n / rp.head_dim, j = n % rp.head_dim;
+    if (head < rp.heads) {
+      rp.q[n] = (uint16_t)bf16_packed(y);
+    } else {
+      const int place = *(const int32_t *)(rtab + 2048), hk = head - rp.heads;
+      if (place < 0 || place >= rp.cache_rows) return;
+      const bool own = rp.vcache && hk >= rp.kv;
+      uint16_t *dst = (own ? rp.vcache : rp.cache) + (int64_t)(own ? hk - rp.kv : hk) * rp.cache_sh +
+                      (int64_t)place * rp.cache_sr;
+      dst[j] = (uint16_t)bf16_packed(y);
+    }
+    return;
   }
   const int n = run * 16 + col;
   if (g != 0 || n >= h.n) return;
@@ -1537,33 +1602,33 @@ extern "C" int bt_matmul(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_
 }
 
 template <int FMT, int G>
-static void launch_row_g(const RowArgs &ra, int kind, size_t lds, unsigned blocks, hipStream_t s) {
-  if (kind == BT_ROW_RMS) gemv_row_kernel<FMT, G, BT_ROW_RMS><<<blocks, 256, lds, s>>>(ra);
-  else if (kind == BT_ROW_SWIGLU) gemv_row_kernel<FMT, G, BT_ROW_SWIGLU><<<blocks, 256, lds, s>>>(ra);
-  else gemv_row_kernel<FMT, G, BT_ROW_PLAIN><<<blocks, 256, lds, s>>>(ra);
+static void launch_row_g(const RowArgs &ra, const RopeTail *rope, int kind, size_t lds, unsigned blocks, hipStream_t s) {
+  if (rope) gemv_row_kernel<FMT, G, BT_ROW_RMS, true><<<blocks, 256, lds, s>>>(ra, *rope);
+  else if (kind == BT_ROW_RMS) gemv_row_kernel<FMT, G, BT_ROW_RMS, false><<<blocks, 256, lds, s>>>(ra, RopeTail{});
+  else if (kind == BT_ROW_SWIGLU) gemv_row_kernel<FMT, G, BT_ROW_SWIGLU, false><<<blocks, 256, lds, s>>>(ra, RopeTail{});
+  else gemv_row_kernel<FMT, G, BT_ROW_PLAIN, false><<<blocks, 256, lds, s>>>(ra, RopeTail{});
 }
 
+// rope: RoPE and the cache put fused (a kind of BT_ROW_RMS, at most 2 slices so that a block holds a pair of runs)
 template <int FMT>
-static void launch_row(RowArgs ra, int kind, hipStream_t s) {
+static void launch_row(RowArgs ra, int kind, hipStream_t s, const RopeTail *rope = nullptr) {
   // slices: up to 4 a run while each keeps 6 chunks or more and the launch stays under 1024 waves
   int sl = 1;
-  while (sl < 4 && ra.chunks / (2 * sl) >= 6 && (int64_t)ra.nruns * sl < 1024) sl *= 2;
+  while (sl < (rope ? 2 : 4) && ra.chunks / (2 * sl) >= 6 && (int64_t)ra.nruns * sl < 1024) sl *= 2;
   ra.slices = sl;
   const int c = (ra.chunks + sl - 1) / sl;  // chunks a slice
   const int g = c <= 6 ? 6 : c % 12 == 0 ? 12 : c % 9 == 0 ? 9 : c % 8 == 0 ? 8 : 12;
   const int k = ra.k, p0 = kind == BT_ROW_RMS ? (k * 4 + 1023) / 1024 : kind == BT_ROW_SWIGLU ? (k * 2 + 1023) / 1024 : 0;
   const int p1 = kind == BT_ROW_PLAIN ? 0 : (k * 2 + 1023) / 1024, prow = (ra.chunks * 128 + 1023) / 1024;
-  const size_t lds = (size_t)(p0 + p1 + prow) * 1024 + 4 * g * 128 + 16 + 4 * 1024;
-  const unsigned blocks = (unsigned)(((int64_t)ra.nruns * sl + 3) / 4);
-  if (g == 9) launch_row_g<FMT, 9>(ra, kind, lds, blocks, s);
-  else if (g == 8) launch_row_g<FMT, 8>(ra, kind, lds, blocks, s);
-  else if (g == 6) launch_row_g<FMT, 6>(ra, kind, lds, blocks, s);
-  else launch_row_g<FMT, 12>(ra, kind, lds, blocks, s);
+  const size_t lds = (size_t)(p0 + p1 + prow) * 1024 + 4 * g * 128 + 16 + 4 * 1024 + (rope ? 256 + 3 * 1024 : 0);
+  const unsigned blocks = (unsigned)(((int64_t)ra.nruns * sl + 3) / 4);  // with RoPE nruns is even: whole pairs
+  if (g == 9) launch_row_g<FMT, 9>(ra, rope, kind, lds, blocks, s);
+  else if (g == 8) launch_row_g<FMT, 8>(ra, rope, kind, lds, blocks, s);
+  else if (g == 6) launch_row_g<FMT, 6>(ra, rope, kind, lds, blocks, s);
+  else launch_row_g<FMT, 12>(ra, rope, kind, lds, blocks, s);
 }
 
-extern "C" int bt_matmul_row(bt_runtime *rt, const bt_row_args *args) {
-  Runtime *r;
-  if (int s = enter(rt, &r)) return s;
+static int row_args(const bt_row_args *args, RowArgs *ra) {
   if (!args) return fail(BT_EINVAL, "matmul_row needs its arguments");
   const bt_row_args &x = *args;
   if (x.kind != BT_ROW_PLAIN && x.kind != BT_ROW_RMS && x.kind != BT_ROW_SWIGLU)
@@ -1572,28 +1637,68 @@ extern "C" int bt_matmul_row(bt_runtime *rt, const bt_row_args *args) {
   if (x.out_dtype != BT_BF16 && x.out_dtype != BT_FP32) return fail(BT_EINVAL, "matmul_row writes bf16 or fp32");
   if (x.k < 1 || x.k > 4096 || x.n < 1 || x.n >= (1 << 30))
     return fail(BT_EINVAL, "matmul_row shape k=%lld (1..4096), n=%lld", (long long)x.k, (long long)x.n);
-  if (!x.a || !x.out || !x.b || (x.kind == BT_ROW_RMS && !x.norm))
-    return fail(BT_EINVAL, "matmul_row needs a, out, B and (for the norm) its weights");
+  if (!x.a || !x.b || (x.kind == BT_ROW_RMS && !x.norm))
+    return fail(BT_EINVAL, "matmul_row needs a, B and (for the norm) its weights");
   if (x.a % 16 || x.norm % 16 || x.b % 16 || (x.kind == BT_ROW_SWIGLU && x.k % 8))
     return fail(BT_EINVAL, "matmul_row reads its inputs 16 bytes at a time: a, norm and B 16-byte aligned%s",
                 x.kind == BT_ROW_SWIGLU ? ", k a multiple of 8" : "");
+  ra->b = (const uint8_t *)(uintptr_t)x.b;
+  ra->a = (const uint8_t *)(uintptr_t)x.a;
+  ra->norm = (const uint8_t *)(uintptr_t)x.norm;
+  ra->res = (const float *)(uintptr_t)x.residual;
+  ra->out = (uint8_t *)(uintptr_t)x.out;
+  ra->chunks = (int32_t)((x.k + 63) / 64);
+  ra->nruns = (int32_t)((x.n + 15) / 16);
+  ra->k = (int32_t)x.k;
+  ra->n = (int32_t)x.n;
+  ra->out_dtype = x.out_dtype;
+  ra->eps = x.eps;
+  ra->slices = 1;
+  ra->half_runs = 0;
+  return BT_OK;
+}
+
+extern "C" int bt_matmul_row(bt_runtime *rt, const bt_row_args *args) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
   RowArgs ra;
-  ra.b = (const uint8_t *)(uintptr_t)x.b;
-  ra.a = (const uint8_t *)(uintptr_t)x.a;
-  ra.norm = (const uint8_t *)(uintptr_t)x.norm;
-  ra.res = (const float *)(uintptr_t)x.residual;
-  ra.out = (uint8_t *)(uintptr_t)x.out;
-  ra.chunks = (int32_t)((x.k + 63) / 64);
-  ra.nruns = (int32_t)((x.n + 15) / 16);
-  ra.k = (int32_t)x.k;
-  ra.n = (int32_t)x.n;
-  ra.out_dtype = x.out_dtype;
-  ra.eps = x.eps;
-  ra.slices = 1;
-  if (x.b_fmt == BT_BF16) launch_row<BT_BF16>(ra, x.kind, r->stream);
-  else if (x.b_fmt == BT_BFP8) launch_row<BT_BFP8>(ra, x.kind, r->stream);
-  else launch_row<BT_BFP4>(ra, x.kind, r->stream);
+  if (int s = row_args(args, &ra)) return s;
+  if (!args->out) return fail(BT_EINVAL, "matmul_row needs out");
+  if (args->b_fmt == BT_BF16) launch_row<BT_BF16>(ra, args->kind, r->stream);
+  else if (args->b_fmt == BT_BFP8) launch_row<BT_BFP8>(ra, args->kind, r->stream);
+  else launch_row<BT_BFP4>(ra, args->kind, r->stream);
   BT_LAUNCHED("matmul_row");
+  return BT_OK;
+}
+
+extern "C" int bt_matmul_row_rope(bt_runtime *rt, const bt_row_args *args, const bt_rope_args *rope) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  RowArgs ra;
+  if (int s = row_args(args, &ra)) return s;
+  if (!rope) return fail(BT_EINVAL, "matmul_row_rope needs RoPE's arguments");
+  const bt_rope_args &p = *rope;
+  if (args->kind != BT_ROW_RMS || args->out_dtype != BT_BF16 || args->residual)
+    return fail(BT_EINVAL, "matmul_row_rope takes the RMSNorm prologue, a bf16 product and no residual");
+  if (p.rows != 1 || p.heads < 1 || p.kv < 1 || p.head_dim < 32 || p.head_dim % 32 || p.cache_rows < 1 ||
+      args->n != (int64_t)(p.heads + 2 * p.kv) * p.head_dim)
+    return fail(BT_EINVAL, "matmul_row_rope: one row of %d + 2 x %d heads of %d (a multiple of 32) for n=%lld",
+                p.heads, p.kv, p.head_dim, (long long)args->n);
+  if (!p.cos || !p.sin || !p.q || !p.cache || !p.places) return fail(BT_EINVAL, "matmul_row_rope needs every buffer");
+  RopeTail tail;
+  tail.cos = (const uint16_t *)(uintptr_t)p.cos;
+  tail.sin = (const uint16_t *)(uintptr_t)p.sin;
+  tail.places = (const int32_t *)(uintptr_t)p.places;
+  tail.q = (uint16_t *)(uintptr_t)p.q;
+  tail.cache = (uint16_t *)(uintptr_t)p.cache;
+  tail.vcache = (uint16_t *)(uintptr_t)p.vcache;
+  tail.cache_sh = p.cache_sh, tail.cache_sr = p.cache_sr, tail.cache_tsh = p.cache_tsh, tail.cache_rows = p.cache_rows;
+  tail.heads = p.heads, tail.kv = p.kv, tail.head_dim = p.head_dim;
+  ra.half_runs = p.head_dim / 32;
+  if (args->b_fmt == BT_BF16) launch_row<BT_BF16>(ra, args->kind, r->stream, &tail);
+  else if (args->b_fmt == BT_BFP8) launch_row<BT_BFP8>(ra, args->kind, r->stream, &tail);
+  else launch_row<BT_BFP4>(ra, args->kind, r->stream, &tail);
+  BT_LAUNCHED("matmul_row_rope");
   return BT_OK;
 }
 

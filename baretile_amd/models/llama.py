@@ -187,13 +187,13 @@ def row_fits(w, c):
 
 
 def row_layer(x, p, c, rot, places, cache, rows):
-  """One block for a single token, as layer() computes it, in six kernels: the norm inside the qkv and gate_up
-  products, RoPE with the cache put, attention, the residual adds inside the o and down products, and silu(gate) * up
-  inside the down product (bt_matmul_row, bt_rope_put). Each fused step rounds once, in fp32, where the lazy graph
-  rounds each operation to bf16."""
+  """One block for a single token, as layer() computes it, in five kernels: the norm inside the qkv and gate_up
+  products, RoPE with the cache put inside the qkv product, attention, the residual adds inside the o and down
+  products, and silu(gate) * up inside the down product (bt_matmul_row, bt_matmul_row_rope). Each fused step rounds
+  once, in fp32, where the lazy graph rounds each operation to bf16."""
   rep = c.heads // c.kv
-  qkv = x.matmul_row(p["qkv_proj"], "bf16", norm=p["input_layernorm"], eps=c.eps)
-  q = qkv.rope_put(rot[0], rot[1], cache, rows, c.heads, c.kv).split(c.heads)
+  q = x.matmul_row(p["qkv_proj"], norm=p["input_layernorm"], eps=c.eps,
+                   rope=(rot[0], rot[1], cache, rows, c.heads, c.kv)).split(c.heads)
   o = q.attend(cache[:c.kv, :, :].repeat_interleave(rep), cache[c.kv:, :, :].repeat_interleave(rep), places)
   x = o.matmul_row(p["o_proj"], "fp32", residual=x)
   gate_up = x.matmul_row(p["gate_up_proj"], "bf16", norm=p["post_attention_layernorm"], eps=c.eps)

@@ -646,12 +646,18 @@ class Tensor:
     a = self.cast("bf16") if self.dtype in BFP else self
     return a._new("matmul", (a, x), (max(a.batch, x.batch), a.rows, x.cols), dtype)
 
-  def matmul_row(self, w, dtype="bf16", norm=None, eps=1e-5, swiglu=False, residual=None):
+  def matmul_row(self, w, dtype="bf16", norm=None, eps=1e-5, swiglu=False, residual=None, rope=None):
     """The product of one row with w (by columns) in one kernel, with the operation before it fused (the decode step
     of llama.py's layer at batch 1, llama.py:106-130; bt_matmul_row): with norm, the RMSNorm of self (an fp32 row,
     rounded to bf16 first) scaled by norm (bf16); with swiglu, silu(gate) * up of self (a bf16 row holding the gate
     then the up half); else self (bf16). residual, an fp32 row, is added to the fp32 sum. The row may be any tensor
-    whose values lie contiguous in memory (an attention output of one row, say). Returns a (1, n) row of dtype."""
+    whose values lie contiguous in memory (an attention output of one row, say). Returns a (1, n) row of dtype.
+
+    rope, (cos, sin, cache, places, heads, kv): the bf16 product then goes through rope_put's RoPE and cache put in
+    the same kernel (bt_matmul_row_rope; with norm, no residual), and the query heads come back as rope_put returns
+    them."""
+    if rope is not None:
+      return self._matmul_row_rope(w, norm, eps, *rope)
     if dtype not in ("bf16", "fp32"): raise ValueError(f"matmul_row writes bf16 or fp32, not {dtype}")
     if not isinstance(w, Tensor) or w.rt is not self.rt or w.layout != "columns" or w.batch != 1:
       raise ValueError("matmul_row needs w laid out by columns, batch 1, on the same runtime")
@@ -679,6 +685,33 @@ class Tensor:
                         w.storage.addr, k, w.cols, kind, _lib.DTYPES[w.dtype], _lib.DTYPES[dtype], eps)
     self.rt.run("matmul_row", "matmul_row", ctypes.byref(args))
     return out
+
+  def _matmul_row_rope(self, w, norm, eps, cos, sin, cache, places, heads, kv):
+    a, nw = self.realize(), norm.realize() if norm is not None else None
+    c, sn, cc, pl = cos.realize(), sin.realize(), cache.realize(), places.realize()
+    nh = heads + 2 * kv
+    if nw is None or not isinstance(w, Tensor) or w.layout != "columns" or w.batch != 1 or w.cols % nh:
+      raise ValueError("matmul_row with rope needs the norm and w by columns, (heads + 2 kv) heads wide")
+    d = w.cols // nh
+    if not (a.dtype == "fp32" and a._contiguous() and a.batch * a.rows * a.cols == w.rows):
+      raise ValueError(f"matmul_row with rope needs a contiguous fp32 row of {w.rows}: {a.shape} {a.dtype}")
+    if not (nw.dtype == "bf16" and nw._contiguous() and nw.batch * nw.rows * nw.cols == w.rows):
+      raise ValueError(f"matmul_row's norm weights must be a contiguous bf16 row of {w.rows}: {nw.shape}")
+    if not (c.dtype == sn.dtype == "bf16" and c._contiguous() and sn._contiguous() and c.cols == sn.cols == w.cols
+            and c.batch * c.rows == sn.batch * sn.rows == 1):
+      raise ValueError(f"matmul_row with rope needs one bf16 row of cos and of sin, {w.cols} wide: {c.shape} {sn.shape}")
+    if not (cc.dtype == "bf16" and cc.batch == 2 * kv and cc.cols == d and cc.sc == 1 and cc.rep == 1 and not cc.cyc
+            and cc.layout == "plain"):
+      raise ValueError(f"matmul_row with rope needs a plain ({2 * kv}, size, {d}) cache: {cc.shape}")
+    if not (pl.dtype == "int32" and pl.batch * pl.rows * pl.cols == 1):
+      raise ValueError("matmul_row with rope needs the token's place as one int32")
+    q = Tensor(self.rt, 1, heads * d)
+    args = _lib.RowArgs(a.addr, nw.addr, 0, 0, w.storage.addr, w.rows, w.cols, _lib.ROW_RMS, _lib.DTYPES[w.dtype],
+                        _lib.DTYPES["bf16"], eps)
+    tail = _lib.RopeArgs(0, c.addr, sn.addr, q.addr, cc.addr, pl.addr, 0, 0, q.sr, cc.sb, cc.sr, cc.rows, 1, heads, kv,
+                         d, 0, 0, 0, 0)
+    self.rt.run("matmul_row_rope", "matmul_row_rope", ctypes.byref(args), ctypes.byref(tail))
+    return q
 
   def rms_rows(self, w, eps=1e-5):
     """RMSNorm of each row of self (fp32, a batch of one) scaled by w (bf16), in one kernel a row apart
@@ -753,14 +786,7 @@ class Tensor:
       raise ValueError(f"attend needs heads 64 or 128 wide and a value for each key: {self.shape} {k.shape} {v.shape}")
     if not (places.rows == self.rows and places.batch in (1, self.batch) and places.cols == 1 and places.dtype == "int32"):
       raise ValueError(f"attend needs places as an int32 column with a row for each query: {places.shape}")
-    q = self.realize()
-    k, v, places = k.realize(), v.realize(), places.realize()
-    if k.rep != v.rep or k.cyc or v.cyc: raise ValueError("attend needs keys and values repeated alike")
-    rep = k.rep
-    if q.sc != 1 or q.rep != 1 or q.cyc: q = q.contiguous()
-    if k.sc != 1: k = k.contiguous()
-    if v.sc != 1: v = v.contiguous()
-    if not places._contiguous(): places = places.contiguous()
+    q, k, v, places, rep = self._attention_operands(k, v, places)
     if merged:  # the heads side by side in each row, as merge() would give them
       out = Tensor(self.rt, q.rows, q.batch * q.cols)
       osh, osr = q.cols, out.sr
@@ -786,6 +812,16 @@ class Tensor:
     self.rt.run("attention", "attention", ctypes.byref(args))
     del scratch
     return out
+
+  def _attention_operands(self, k, v, places):
+    q = self.realize()
+    k, v, places = k.realize(), v.realize(), places.realize()
+    if k.rep != v.rep or k.cyc or v.cyc: raise ValueError("attend needs keys and values repeated alike")
+    if q.sc != 1 or q.rep != 1 or q.cyc: q = q.contiguous()
+    if k.sc != 1: k = k.contiguous()
+    if v.sc != 1: v = v.contiguous()
+    if not places._contiguous(): places = places.contiguous()
+    return q, k, v, places, k.rep
 
   def topk(self, k, parts=1, labels=None):
     """(values, int32 indices) of the k largest entries of each row, descending, in one kernel (tensor.py:685-706):

@@ -231,6 +231,12 @@ typedef struct {
   int32_t one_place, pad_;
 } bt_rope_args;
 int bt_rope_put(bt_runtime *rt, const bt_rope_args *args);
+/* bt_matmul_row (BT_ROW_RMS, a bf16 product, no residual) with bt_rope_put run on its product in the same kernel: the
+ * decode step's RMSNorm, qkv product, RoPE and cache put (llama.py:106-160) for one token. rope->qkv and args->out are
+ * not used; rope->rows is 1, args->n is (heads + 2 kv) head_dim and head_dim a multiple of 32. The query heads land
+ * in rope->q and the key and value heads in the cache, bit for bit what the two calls write. */
+int bt_matmul_row_rope(bt_runtime *rt, const bt_row_args *args, const bt_rope_args *rope);
+
 
 /* ---- attention: replaces attention_kernel and its division/combine launches (kernels.py:794-1005,
  * tensor.py:797-841) -------------------------------------------------------------------------------------------

@@ -335,6 +335,29 @@ def test_rope_put(rt, hd):
   assert not np.any(got_c[:, others])
 
 
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bfp4"])
+@pytest.mark.parametrize("k,hd,heads,kv", [(576, 64, 9, 3), (2048, 128, 8, 2), (320, 64, 2, 1)])
+def test_matmul_row_rope_equals_two_calls(rt, fmt, k, hd, heads, kv):
+  # RMSNorm, qkv product, RoPE and cache put in one kernel (bt_matmul_row_rope) write, bit for bit, what
+  # bt_matmul_row to bf16 then bt_rope_put write: q, the new key and value rows, and nothing else in the cache. 2048
+  # rows of K split each run's sum between two waves.
+  from baretile_amd.models import llama
+  nh, size, place = heads + 2 * kv, 24, 17
+  c = llama.model(dim=heads * hd, heads=heads, kv=kv, layers=1, eps=1e-5, theta=10000.0, head_dim=hd)
+  cos, sin, _ = llama.rotary(c, size)
+  rng = np.random.default_rng(k + hd)
+  wt, _ = _weights(rt, k, nh * hd, fmt, k + nh)
+  x = Tensor.of(rt, rng.normal(0, 2, (1, k)).astype(np.float32), "fp32")
+  norm = Tensor.of(rt, B.bf16(rng.normal(1, 0.1, (1, k)).astype(np.float32)))
+  cs, sn, pl = Tensor.of(rt, cos[[place]]), Tensor.of(rt, sin[[place]]), Tensor.of(rt, [[place]], "int32")
+  c1, c2 = Tensor.zeros(rt, size, hd, batch=2 * kv), Tensor.zeros(rt, size, hd, batch=2 * kv)
+  q1 = x.matmul_row(wt, norm=norm, eps=1e-5, rope=(cs, sn, c1, pl, heads, kv))
+  q2 = x.matmul_row(wt, "bf16", norm=norm, eps=1e-5).rope_put(cs, sn, c2, pl, heads, kv)
+  assert q1.tobytes() == q2.tobytes()
+  assert c1.tobytes() == c2.tobytes()
+  assert np.any(value(c1).reshape(2 * kv, size, hd)[:, place])
+
+
 def test_rope_put_slots(rt):
   # the slots' layout: separate key and value caches of rows * kv heads, row i's heads at i * kv, one place for all
   # rows (llama.slots_layer); against the same float64 RoPE, and nothing else written
