@@ -13,7 +13,11 @@ The numbers follow the reference's device path (llama.py:88-183):
 Llama-family only: Qwen's DeltaNet and experts, gpt-oss sinks and sliding windows other than the plain causal one
 are outside this backend's scope.
 """
+import json
 import math
+import os
+import re
+import struct
 from types import SimpleNamespace
 import numpy as np
 from baretile_amd.tensor import Tensor, jit
@@ -88,29 +92,110 @@ def rotary(c, n):
   return table(np.cos, 1.0), table(np.sin, 0.0), turn
 
 
+class Weight:
+  """A checkpoint matrix read on demand, so the host never holds the whole model (llama.py:229-233): bits() returns
+  its bf16 bits laid out for x @ w, values() those values as float32."""
+  def __init__(self, bits): self.bits = bits
+  def values(self): return (self.bits().astype(np.uint32) << 16).view(np.float32)
+
+
 def fuse(w, c):
-  """q, k, v side by side as qkv_proj, and gate, up as gate_up_proj, in each block (llama.py:238-291)."""
+  """q, k, v side by side as qkv_proj, and gate, up as gate_up_proj, in each block (llama.py:238-291). Takes NumPy
+  arrays or Weights (joined when read)."""
+  def join(xs):
+    if isinstance(xs[0], Weight): return Weight(lambda: np.ascontiguousarray(np.concatenate([x.bits() for x in xs], 1)))
+    return np.concatenate(xs, 1)
   w = dict(w)
   for l in range(c.layers):
     p = f"layers.{l}."
     if p + "q_proj" in w:
-      w[p + "qkv_proj"] = np.concatenate([w.pop(p + n) for n in ("q_proj", "k_proj", "v_proj")], 1)
+      w[p + "qkv_proj"] = join([w.pop(p + n) for n in ("q_proj", "k_proj", "v_proj")])
     if p + "gate_proj" in w:
-      w[p + "gate_up_proj"] = np.concatenate([w.pop(p + n) for n in ("gate_proj", "up_proj")], 1)
+      w[p + "gate_up_proj"] = join([w.pop(p + n) for n in ("gate_proj", "up_proj")])
   return w
 
 
+TYPES = ("llama",)
+
+
+def read_safetensors(path):
+  """A safetensors file's header (each tensor's dtype, shape and byte range) and its data, memory-mapped."""
+  with open(path, "rb") as f:
+    size = struct.unpack("<Q", f.read(8))[0]
+    header = json.loads(f.read(size))
+  return header, np.memmap(path, np.uint8, "r", offset=8 + size)
+
+
+def tensor_bits(data, t, transpose=False):
+  """A checkpoint tensor as bf16 bits (gpt2.py:42-48): BF16 as stored, F32 rounded to nearest even; a vector
+  becomes a one-row matrix."""
+  raw = np.asarray(data[t["data_offsets"][0]:t["data_offsets"][1]])
+  if t["dtype"] == "BF16": bits = raw.view(np.uint16)
+  elif t["dtype"] == "F32": bits = (_bf16(raw.view(np.float32)).view(np.uint32) >> 16).astype(np.uint16)
+  else: raise ValueError(f"a checkpoint tensor must be F32 or BF16, not {t['dtype']}")
+  bits = bits.reshape(t["shape"] if len(t["shape"]) >= 2 else (1, -1))
+  return np.ascontiguousarray(bits.T) if transpose else bits
+
+
+def config(folder, places=4096):
+  """A config from a Hugging Face config.json (llama.py:400-427), Llama family with default RoPE. places, capped
+  at the model's maximum, sizes the RoPE tables. ValueError for another model type or RoPE scaling."""
+  with open(os.path.join(folder, "config.json")) as f: j = json.load(f)
+  j = j.get("text_config", j)
+  if j.get("model_type") not in TYPES:
+    raise ValueError(f"{folder}: model type {j.get('model_type')!r} isn't supported; this backend runs {', '.join(TYPES)}")
+  rope = j.get("rope_parameters") or (j.get("rope_scaling") or {}) | {"rope_theta": j.get("rope_theta", 10000.0)}
+  if (rope.get("rope_type") or rope.get("type") or "default") != "default":
+    raise ValueError(f"RoPE scaling {rope} isn't supported")
+  return model(dim=j["hidden_size"], heads=j["num_attention_heads"], kv=j.get("num_key_value_heads", j["num_attention_heads"]),
+               layers=j["num_hidden_layers"], eps=j["rms_norm_eps"], theta=float(rope["rope_theta"]),
+               vocab=j["vocab_size"], ffn=j.get("intermediate_size"), head_dim=j.get("head_dim"),
+               places=min(j.get("max_position_embeddings", places), places), tied=j.get("tie_word_embeddings", False))
+
+
+def load(folder, places=4096):
+  """(config, {name: Weight}) from model.safetensors or the shards model.safetensors.index.json lists
+  (llama.py:429-462). Names drop "model.", "self_attn." and "mlp."; linear layers are transposed for x @ w and vectors
+  become one-row matrices; the output layer is lm_head, or the embedding's transpose when tied; fuse joins q/k/v and
+  gate/up. Nothing is read until a Weight's bits() are."""
+  c = config(folder, places)
+  index = os.path.join(folder, "model.safetensors.index.json")
+  if os.path.exists(index):
+    with open(index) as f: files = sorted(set(json.load(f)["weight_map"].values()))
+  else:
+    files = ["model.safetensors"]
+  out = {}
+  for file in files:
+    header, data = read_safetensors(os.path.join(folder, file))
+    for full, t in header.items():
+      if full == "__metadata__": continue
+      name = full.removeprefix("model.").removesuffix(".weight")
+      for part in ("self_attn.", "mlp."): name = name.replace(part, "")
+      if name.startswith("layers.") and int(name.split(".")[1]) >= c.layers: continue
+      turn = (name.endswith("_proj") or name == "lm_head") and len(t["shape"]) == 2
+      out[name] = Weight(lambda data=data, t=t, turn=turn: tensor_bits(data, t, turn))
+  out["embed"] = out.pop("embed_tokens")
+  head_w = out.pop("lm_head", None)
+  out["embed.T"] = head_w or Weight(lambda e=out["embed"]: np.ascontiguousarray(e.bits().T))
+  return c, fuse(out, c)
+
+
 def upload(rt, w, c, places=None):
-  """NumPy weights (laid out for x @ w, q/k/v and gate/up fused) to the device (llama.py:479-495). Matrices go to
-  their precision's format and into the matmul's tiles once; norms and the embedding stay bf16; the tied output layer
-  is embed.T in the head's format. Adds the RoPE tables for `places` positions."""
+  """Weights (NumPy float arrays, or Weights from load: their bf16 bits go up as they are) laid out for x @ w with
+  q/k/v and gate/up fused, to the device (llama.py:479-495), one at a time. Matrices go to their precision's format
+  and into the matmul's tiles once; norms and the embedding stay bf16; the tied output layer is embed.T in the head's
+  format. Adds the RoPE tables for `places` positions."""
   prec = c.precision
   out = {}
   for name, a in w.items():
     if name in ("cos", "sin", "turn"): continue
-    a = np.asarray(a, np.float32)
-    if a.ndim == 1: a = a[None]
-    t = Tensor.of(rt, a)
+    if isinstance(a, Weight):
+      bits = a.bits()
+      t = Tensor.frombytes(rt, *bits.shape[-2:], np.ascontiguousarray(bits).tobytes())
+    else:
+      a = np.asarray(a, np.float32)
+      if a.ndim == 1: a = a[None]
+      t = Tensor.of(rt, a)
     if name.endswith("_proj") or name == "embed.T":
       fmt = weight_format(name, prec)
       t = (t.cast(fmt) if fmt != "bf16" else t).columns()

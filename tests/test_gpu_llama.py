@@ -106,3 +106,23 @@ def test_slots_layer_matches_each_slot_in_numpy(rt):
     new_v = np.array(values.tolist()).reshape(S * kv, size, hd)[s * kv:(s + 1) * kv, place]
     for got_r, want_r in ((new_k, cache[:kv, place]), (new_v, cache[kv:, place])):
       assert np.abs(got_r - want_r).max() <= 0.03 * np.abs(want_r).max(), (s, np.abs(got_r - want_r).max())
+
+
+def test_loaded_checkpoint_matches_numpy(rt, tmp_path):
+  # llama.load (safetensors, llama.py:429-462) -> upload in bfp8 -> a prompt's logits, against the oracle on the
+  # same weights (their bf16 values, block floats rounded by oracle.bfp), within test_models.py:849's 3%
+  from test_llama_load import checkpoint
+  checkpoint(str(tmp_path), dim=256, heads=4, kv=2, ffn=256, vocab=96, layers=2, tied=False)
+  c, w = llama.load(str(tmp_path), places=64)
+  c.precision = llama.precision(c, "bfp8")
+  dw = llama.upload(rt, w, c, places=c.places)
+  rc = L.model(dim=c.dim, heads=c.heads, kv=c.kv, layers=c.layers, eps=c.eps, theta=c.theta, vocab=c.vocab, ffn=c.ffn)
+  host = {k: v.values() for k, v in w.items()}
+  host["cos"], host["sin"], host["turn"] = L.rotary(rc, 64)
+  ref = L.arrays(host, L.precision(rc, "bfp8"))
+  ids = [5, 90, 17, 3, 44, 61]
+  got = np.array(llama.forward(Tensor.of(rt, [ids], "int32"), Tensor.of(rt, [list(range(6))], "int32"), dw, c,
+                               llama.kv_cache(rt, c, 64), every=True).tolist())
+  want = L.forward(ids, range(6), ref, rc, L.kv_cache(rc, 64), every=True)
+  assert np.abs(got - want).max() <= 0.03 * np.abs(want).max(), np.abs(got - want).max()
+
