@@ -46,7 +46,8 @@ class AttentionArgs(ctypes.Structure):
               ("v_sr", c_int64), ("o_sh", c_int64), ("o_sr", c_int64), ("places_sh", c_int64),
               ("heads", c_int32), ("rep", c_int32), ("rows", c_int32), ("keys", c_int32), ("head_dim", c_int32),
               ("window", c_int32), ("parts", c_int32), ("pad_", c_int32), ("scratch", c_uint64),
-              ("scratch_bytes", c_uint64), ("firsts", c_uint64), ("firsts_sh", c_int64)]
+              ("scratch_bytes", c_uint64), ("firsts", c_uint64), ("firsts_sh", c_int64), ("kv_fmt", c_int32),
+              ("pad2_", c_int32), ("k_exps", c_uint64), ("v_exps", c_uint64)]
 
 
 ROW_PLAIN, ROW_RMS, ROW_SWIGLU = range(3)
@@ -88,6 +89,7 @@ SIGNATURES = {
   "bt_attention": [RT, POINTER(AttentionArgs)],
   "bt_attention_scratch": [POINTER(AttentionArgs), POINTER(c_uint64)],
   "bt_matmul_row": [RT, POINTER(RowArgs)], "bt_rope_put": [RT, POINTER(RopeArgs)],
+  "bt_put_bfp": [RT, c_int, U64, U64, I64, I64, I64, I64, I64, U64, I64, U64, I64, I64],
   "bt_matmul_row_rope": [RT, POINTER(RowArgs), POINTER(RopeArgs)],
   "bt_matmul_swiglu": [RT, POINTER(Operand), c_int, U64, I64, I64, I64, POINTER(Operand)],
   "bt_rms_rows": [RT, U64, I64, I64, I64, U64, c_float, U64, I64],

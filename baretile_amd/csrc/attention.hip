@@ -45,6 +45,52 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, 
   return *(const bf16x8 *)&v;
 }
 
+__device__ __forceinline__ bf16x8 as_bf16x8(const uint4 &v) { return as_bf16x8(v.x, v.y, v.z, v.w); }
+
+// Where a key head's K (or V) rows come from: bf16 (one buffer), or a block-float cache's value and exponent planes.
+// Offsets are in values; rows past `span` values read as zeros.
+struct KvSrc {
+  __amdgpu_buffer_rsrc_t val, exp;
+};
+template <int KF>
+__device__ __forceinline__ KvSrc kv_src(uint64_t vals, uint64_t exps, int64_t head, int64_t span) {
+  KvSrc s;
+  if (KF == BT_BF16) {
+    s.val = attn_rsrc((const uint16_t *)(uintptr_t)vals + head, (uint32_t)(span * 2));
+    s.exp = s.val;
+  } else {
+    const int shift = KF == BT_BFP8 ? 0 : 1;  // value index -> byte of its q
+    s.val = attn_rsrc((const uint8_t *)(uintptr_t)vals + (head >> shift), (uint32_t)(span >> shift));
+    s.exp = attn_rsrc((const uint8_t *)(uintptr_t)exps + head / 16, (uint32_t)(span / 16));
+  }
+  return s;
+}
+// 8 values from value e on (e a multiple of 8), as bf16 pairs: a block float decoded exactly as the unpacker
+// decodes it (its exponent byte at e / 16).
+template <int KF>
+__device__ __forceinline__ uint4 kv_load8(const KvSrc &s, uint32_t e) {
+  if (KF == BT_BF16) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(s.val, e * 2, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+  }
+  const uint32_t x = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(s.exp, e / 16, 0, 0);
+  uint32_t w[4] = {0, 0, 0, 0};
+  if (KF == BT_BFP8) {
+    const auto q = __builtin_amdgcn_raw_buffer_load_b64(s.val, e, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      w[i / 2] |= unpacked_bits((int)(int8_t)((q[i / 4] >> (8 * (i % 4))) & 255u), x) << (16 * (i % 2));
+  } else {
+    const uint32_t q = __builtin_amdgcn_raw_buffer_load_b32(s.val, e / 2, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int nib = (int)((q >> (4 * i)) & 15u);
+      w[i / 2] |= unpacked_bits((nib >= 8 ? nib - 16 : nib) * 16, x) << (16 * (i % 2));
+    }
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // A lane's pair: which query row it is, which keys it sees, where its q and output rows are.
 struct Pair {
   int lo, hi;  // visible keys lo..hi (empty when lo > hi)
@@ -220,7 +266,7 @@ __device__ __forceinline__ void store_state(float *ws, const State<HD> &st, int 
 
 // Decode: block (kvh, t, part). The tile's visible keys, from its smallest first to its largest last, are cut into
 // `parts` runs of whole 64-key blocks; the 4 waves take the part's blocks in turn.
-template <int HD>
+template <int HD, int KF>
 __global__ void __launch_bounds__(256) attention_decode_kernel(const bt_attention_args a, int tiles, int parts,
                                                                float *scratch) {
   constexpr int VS = HD + 8, VR = KB * VS;  // halfwords of one wave's value block
@@ -244,10 +290,8 @@ __global__ void __launch_bounds__(256) attention_decode_kernel(const bt_attentio
   st.m = -__builtin_inff(), st.l = 0.0f;
 #pragma unroll
   for (int c = 0; c < HD / 16; c++) st.o[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  const uint32_t kbytes = (uint32_t)(((int64_t)(a.keys - 1) * a.k_sr + HD) * 2);
-  const uint32_t vbytes = (uint32_t)(((int64_t)(a.keys - 1) * a.v_sr + HD) * 2);
-  const __amdgpu_buffer_rsrc_t kr = attn_rsrc((const uint16_t *)a.k + (int64_t)kvh * a.k_sh, kbytes);
-  const __amdgpu_buffer_rsrc_t vr = attn_rsrc((const uint16_t *)a.v + (int64_t)kvh * a.v_sh, vbytes);
+  const KvSrc kr = kv_src<KF>(a.k, a.k_exps, (int64_t)kvh * a.k_sh, (int64_t)(a.keys - 1) * a.k_sr + HD);
+  const KvSrc vr = kv_src<KF>(a.v, a.v_exps, (int64_t)kvh * a.v_sh, (int64_t)(a.keys - 1) * a.v_sr + HD);
   uint16_t *vl = lds + wib * VR;
   constexpr int RPI = 64 * 8 / HD;  // value rows one load instruction covers
   const int vrow = lane / (HD / 8), vcol = lane % (HD / 8) * 8;
@@ -256,18 +300,12 @@ __global__ void __launch_bounds__(256) attention_decode_kernel(const bt_attentio
 #pragma unroll
     for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-      for (int kk = 0; kk < HD / 32; kk++) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(
-            kr, (uint32_t)(((int64_t)(kb + 16 * kt + n) * a.k_sr + 32 * kk + 8 * g) * 2), 0, 0);
-        kf[kt][kk] = as_bf16x8(v[0], v[1], v[2], v[3]);
-      }
+      for (int kk = 0; kk < HD / 32; kk++)
+        kf[kt][kk] = as_bf16x8(kv_load8<KF>(kr, (uint32_t)((int64_t)(kb + 16 * kt + n) * a.k_sr + 32 * kk + 8 * g)));
     uint4 vv[KB / RPI];
 #pragma unroll
-    for (int i = 0; i < KB / RPI; i++) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(
-          vr, (uint32_t)(((int64_t)(kb + vrow + RPI * i) * a.v_sr + vcol) * 2), 0, 0);
-      vv[i] = make_uint4(v[0], v[1], v[2], v[3]);
-    }
+    for (int i = 0; i < KB / RPI; i++)
+      vv[i] = kv_load8<KF>(vr, (uint32_t)((int64_t)(kb + vrow + RPI * i) * a.v_sr + vcol));
     wave_lds_sync();  // the previous block's reads of vl are done
 #pragma unroll
     for (int i = 0; i < KB / RPI; i++) *(uint4 *)(vl + (vrow + RPI * i) * VS + vcol) = vv[i];
@@ -477,7 +515,7 @@ __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf
 //
 // Blocks go heaviest first (the last rows of the causal triangle see the most keys): block u takes key head u % kvhs
 // and row block rblocks - 1 - u / kvhs.
-template <int HD>
+template <int HD, int KF>
 __global__ void __launch_bounds__(512, 1) attention_prefill_kernel(const bt_attention_args a, int rblocks, int kvhs) {
   constexpr int KS = HD + 8, VT = KB + 8, KBUF = KB * KS, STG = KBUF + HD * VT;  // halfwords of one stage
   constexpr int KW = KB * HD / 8 / 256;  // 16-byte words of K each thread of a half moves per block
@@ -531,30 +569,22 @@ __global__ void __launch_bounds__(512, 1) attention_prefill_kernel(const bt_atte
   }
   // rows past the block's last visible key read as zeros (they are masked, and may never have been written): the
   // buffers end there
-  const uint32_t kbytes = bhi < 0 ? 0 : (uint32_t)(((int64_t)bhi * a.k_sr + HD) * 2);
-  const uint32_t vbytes = bhi < 0 ? 0 : (uint32_t)(((int64_t)bhi * a.v_sr + HD) * 2);
-  const __amdgpu_buffer_rsrc_t kr = attn_rsrc((const uint16_t *)a.k + (int64_t)kvh * a.k_sh, kbytes);
-  const __amdgpu_buffer_rsrc_t vr = attn_rsrc((const uint16_t *)a.v + (int64_t)kvh * a.v_sh, vbytes);
+  const KvSrc kr = kv_src<KF>(a.k, a.k_exps, (int64_t)kvh * a.k_sh, bhi < 0 ? 0 : (int64_t)bhi * a.k_sr + HD);
+  const KvSrc vr = kv_src<KF>(a.v, a.v_exps, (int64_t)kvh * a.v_sh, bhi < 0 ? 0 : (int64_t)bhi * a.v_sr + HD);
   // K: thread's words at row kr0 + (256 / (HD / 8)) i, column kc; V: keys KPT kg .. + KPT - 1, columns 8 dg .. + 7.
   const int kr0 = th / (HD / 8), kc = th % (HD / 8) * 8;
   constexpr int KSTEP = 256 / (HD / 8);
   const int kg = th % NKG, dg = th / NKG;
-  // byte offsets from a block's first row: the thread's first word, then uniform steps
-  const uint32_t koff = (uint32_t)(((int64_t)kr0 * a.k_sr + kc) * 2), voff = (uint32_t)(((int64_t)KPT * kg * a.v_sr + 8 * dg) * 2);
-  const uint32_t kstep = (uint32_t)(KSTEP * a.k_sr * 2), vstep = (uint32_t)(a.v_sr * 2);
+  // value offsets from a block's first row: the thread's first word, then uniform steps
+  const uint32_t koff = (uint32_t)((int64_t)kr0 * a.k_sr + kc), voff = (uint32_t)((int64_t)KPT * kg * a.v_sr + 8 * dg);
+  const uint32_t kstep = (uint32_t)(KSTEP * a.k_sr), vstep = (uint32_t)a.v_sr;
   uint4 kreg[KW], vreg[KPT];
   auto fetch = [&](int kb) {
-    const uint32_t kbo = (uint32_t)((int64_t)kb * a.k_sr * 2), vbo = (uint32_t)((int64_t)kb * a.v_sr * 2);
+    const uint32_t kbo = (uint32_t)((int64_t)kb * a.k_sr), vbo = (uint32_t)((int64_t)kb * a.v_sr);
 #pragma unroll
-    for (int i = 0; i < KW; i++) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(kr, koff + (kbo + i * kstep), 0, 0);
-      kreg[i] = make_uint4(v[0], v[1], v[2], v[3]);
-    }
+    for (int i = 0; i < KW; i++) kreg[i] = kv_load8<KF>(kr, koff + (kbo + i * kstep));
 #pragma unroll
-    for (int i = 0; i < KPT; i++) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(vr, voff + (vbo + i * vstep), 0, 0);
-      vreg[i] = make_uint4(v[0], v[1], v[2], v[3]);
-    }
+    for (int i = 0; i < KPT; i++) vreg[i] = kv_load8<KF>(vr, voff + (vbo + i * vstep));
   };
   auto stash = [&](uint16_t *stage) {
     uint16_t *kl = stage, *vt = stage + KBUF;
@@ -635,6 +665,29 @@ __global__ void __launch_bounds__(512, 1) attention_prefill_kernel(const bt_atte
   }
 }
 
+template <int HD>
+static void launch_decode_hd(const bt_attention_args &a, unsigned blocks, int tiles, int parts, float *scratch,
+                             hipStream_t s) {
+  if (a.kv_fmt == BT_BFP8) attention_decode_kernel<HD, BT_BFP8><<<blocks, 256, 0, s>>>(a, tiles, parts, scratch);
+  else if (a.kv_fmt == BT_BFP4) attention_decode_kernel<HD, BT_BFP4><<<blocks, 256, 0, s>>>(a, tiles, parts, scratch);
+  else attention_decode_kernel<HD, BT_BF16><<<blocks, 256, 0, s>>>(a, tiles, parts, scratch);
+}
+static void launch_decode(const bt_attention_args &a, unsigned blocks, int tiles, int parts, float *scratch,
+                          hipStream_t s) {
+  if (a.head_dim == 64) launch_decode_hd<64>(a, blocks, tiles, parts, scratch, s);
+  else launch_decode_hd<128>(a, blocks, tiles, parts, scratch, s);
+}
+template <int HD>
+static void launch_prefill_hd(const bt_attention_args &a, unsigned blocks, int rblocks, int kvh, hipStream_t s) {
+  if (a.kv_fmt == BT_BFP8) attention_prefill_kernel<HD, BT_BFP8><<<blocks, 512, 0, s>>>(a, rblocks, kvh);
+  else if (a.kv_fmt == BT_BFP4) attention_prefill_kernel<HD, BT_BFP4><<<blocks, 512, 0, s>>>(a, rblocks, kvh);
+  else attention_prefill_kernel<HD, BT_BF16><<<blocks, 512, 0, s>>>(a, rblocks, kvh);
+}
+static void launch_prefill(const bt_attention_args &a, unsigned blocks, int rblocks, int kvh, hipStream_t s) {
+  if (a.head_dim == 64) launch_prefill_hd<64>(a, blocks, rblocks, kvh, s);
+  else launch_prefill_hd<128>(a, blocks, rblocks, kvh, s);
+}
+
 struct AttnPlan {
   bool decode;
   int tiles, parts, kpp;
@@ -648,12 +701,18 @@ static int plan_attention(const bt_attention_args *a, AttnPlan *p) {
                 a->rows, a->keys, a->window, a->parts);
   if (a->head_dim != 64 && a->head_dim != 128)
     return fail(BT_EINVAL, "attention takes heads 64 or 128 wide, not %d", a->head_dim);
-  if ((a->q | a->k | a->v) % 16 || a->q_sr % 8 || a->k_sr % 8 || a->v_sr % 8 || a->q_sh % 8 || a->k_sh % 8 ||
-      a->v_sh % 8)
+  if (a->q % 16 || (a->kv_fmt == BT_BF16 && (a->k | a->v) % 16) || a->q_sr % 8 || a->k_sr % 8 || a->v_sr % 8 ||
+      a->q_sh % 8 || a->k_sh % 8 || a->v_sh % 8)
     return fail(BT_EINVAL, "attention needs q, k and v rows on 16-byte boundaries");
   if (a->places_sh != 0 && a->places_sh != a->rows) return fail(BT_EINVAL, "places' head stride is 0 or rows");
   if (((int64_t)(a->keys + KB) * std::max(a->k_sr, a->v_sr) + a->head_dim) * 2 >= (1ll << 32))
     return fail(BT_EINVAL, "a key head's rows (and 64 more) must span less than 4 GiB");
+  if (a->kv_fmt != BT_BF16 && a->kv_fmt != BT_BFP8 && a->kv_fmt != BT_BFP4)
+    return fail(BT_EINVAL, "attention's cache is bf16, bfp8 or bfp4, not %d", a->kv_fmt);
+  if (a->kv_fmt != BT_BF16 && (!a->k_exps || !a->v_exps || a->k % 8 || a->v % 8 || a->k_sr % 16 || a->v_sr % 16 ||
+                               a->k_sh % 16 || a->v_sh % 16))
+    return fail(BT_EINVAL, "a block-float cache needs its exponent planes, 8-byte aligned value planes and strides "
+                           "that are multiples of 16");
   if (a->firsts && a->firsts % 4) return fail(BT_EINVAL, "attention's firsts must be int32-aligned");
   if (a->firsts && a->firsts_sh != 0 && a->firsts_sh != a->rows) return fail(BT_EINVAL, "firsts' head stride is 0 or rows");
   const int kvh = a->heads / a->rep, np = a->rep * a->rows;
@@ -697,8 +756,7 @@ int bt_attention(bt_runtime *rt, const bt_attention_args *a) {
   float *scratch = (float *)(uintptr_t)a->scratch;
   if (p.decode) {
     const unsigned blocks = (unsigned)(kvh * p.tiles * p.parts);
-    if (a->head_dim == 64) attention_decode_kernel<64><<<blocks, 256, 0, r->stream>>>(*a, p.tiles, p.parts, scratch);
-    else attention_decode_kernel<128><<<blocks, 256, 0, r->stream>>>(*a, p.tiles, p.parts, scratch);
+    launch_decode(*a, blocks, p.tiles, p.parts, scratch, r->stream);
     BT_LAUNCHED("attention");
     if (p.parts > 1) {
       const unsigned cb = (unsigned)(kvh * p.tiles);
@@ -709,8 +767,7 @@ int bt_attention(bt_runtime *rt, const bt_attention_args *a) {
   } else {
     const int rblocks = (a->rep * a->rows + 127) / 128;
     const unsigned blocks = (unsigned)(kvh * rblocks);
-    if (a->head_dim == 64) attention_prefill_kernel<64><<<blocks, 512, 0, r->stream>>>(*a, rblocks, kvh);
-    else attention_prefill_kernel<128><<<blocks, 512, 0, r->stream>>>(*a, rblocks, kvh);
+    launch_prefill(*a, blocks, rblocks, kvh, r->stream);
     BT_LAUNCHED("attention");
   }
   return BT_OK;

@@ -11,6 +11,24 @@
 
 namespace bt {
 
+// A run of 16 bf16 values with its largest exponent field `top` into the plain planes: the exponent byte, then the
+// 16 signed magnitudes (bfp8: a byte each; bfp4: two to a byte, the first in the low nibble).
+template <int FMT>
+__device__ __forceinline__ void store_run(const uint32_t (&bits)[16], uint32_t top, uint8_t *exp, uint8_t *val) {
+  *exp = (uint8_t)top;
+  if (FMT == BT_BFP8) {
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 16; i++) w[i / 4] |= ((uint32_t)bfp_signed<8>(bits[i], top) & 255u) << (8 * (i % 4));
+    *(uint4 *)val = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    uint32_t w[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 16; i++) w[i / 8] |= ((uint32_t)bfp_signed<4>(bits[i], top) & 15u) << (4 * (i % 8));
+    *(uint2 *)val = make_uint2(w[0], w[1]);
+  }
+}
+
 // One thread a run: 16 values of one row sharing an exponent. Runs are numbered along rows, so neighbouring threads
 // read neighbouring 32-byte pieces of a bf16 row.
 template <int FMT>
@@ -34,17 +52,38 @@ __global__ void __launch_bounds__(256) pack_kernel(const void *src, int src_dtyp
     bits[i] = v;
     top = max(top, (v >> 7) & 255u);
   }
-  exps[t] = (uint8_t)top;
-  if (FMT == BT_BFP8) {
-    uint32_t w[4] = {0, 0, 0, 0};
+  store_run<FMT>(bits, top, exps + t, vals + t * (FMT == BT_BFP8 ? 16 : 8));
+}
+
+// One row of x (bf16) put into a plain block-float tensor at each place (Tensor.put into a block-float cache,
+// kernels.py:1083-1168): a block a row of x, a thread a run of 16 of it in every batch entry, rounded as the cast
+// rounds. A later duplicate place wins: the block first looks for a j > i with the same place. Strides are in
+// values (multiples of 16); the planes hold a value's exponent byte at its index / 16 and its q at its index (bfp8)
+// or index / 2 (bfp4).
+template <int FMT>
+__global__ void __launch_bounds__(256) put_bfp_kernel(uint8_t *exps, uint8_t *vals, int64_t dst_rows, int64_t cols,
+                                                      int64_t dst_sb, int64_t dst_sr, const int32_t *ids, int64_t n,
+                                                      const uint16_t *x, int64_t x_sb, int64_t x_sr, int64_t batch) {
+  __shared__ int later;
+  const int64_t i = blockIdx.x;
+  const int32_t p = ids[i];
+  if (p < 0 || p >= dst_rows) return;
+  if (threadIdx.x == 0) later = 0;
+  __syncthreads();
+  bool found = false;
+  for (int64_t j = i + 1 + threadIdx.x; j < n; j += blockDim.x) found |= ids[j] == p;
+  if (found) later = 1;
+  __syncthreads();
+  if (later) return;
+  const int64_t runs = cols / 16;
+  for (int64_t e = threadIdx.x; e < batch * runs; e += blockDim.x) {
+    const int64_t b = e / runs, j = e % runs;
+    const uint16_t *src = x + b * x_sb + i * x_sr + j * 16;
+    uint32_t bits[16], top = 0;
 #pragma unroll
-    for (int i = 0; i < 16; i++) w[i / 4] |= ((uint32_t)bfp_signed<8>(bits[i], top) & 255u) << (8 * (i % 4));
-    *(uint4 *)(vals + t * 16) = make_uint4(w[0], w[1], w[2], w[3]);
-  } else {
-    uint32_t w[2] = {0, 0};
-#pragma unroll
-    for (int i = 0; i < 16; i++) w[i / 8] |= ((uint32_t)bfp_signed<4>(bits[i], top) & 15u) << (4 * (i % 8));
-    *(uint2 *)(vals + t * 8) = make_uint2(w[0], w[1]);
+    for (int k = 0; k < 16; k++) bits[k] = src[k], top = max(top, (bits[k] >> 7) & 255u);
+    const int64_t at = b * dst_sb + (int64_t)p * dst_sr + j * 16;  // the run's first value
+    store_run<FMT>(bits, top, exps + at / 16, vals + (FMT == BT_BFP8 ? at : at / 2));
   }
 }
 
@@ -270,6 +309,30 @@ int bt_columns_unpack(bt_runtime *rt, int fmt, uint64_t src, int64_t batch, int6
     columns_unpack_kernel<BT_BFP4><<<blocks_for(n, 256), 256, 0, r->stream>>>((const uint8_t *)src, batch, rows, cols,
                                                                                chunks, nruns, (uint16_t *)dst);
   BT_LAUNCHED("columns_unpack");
+  return BT_OK;
+}
+
+int bt_put_bfp(bt_runtime *rt, int fmt, uint64_t exps, uint64_t vals, int64_t batch, int64_t dst_rows, int64_t cols,
+               int64_t dst_sb, int64_t dst_sr, uint64_t ids, int64_t n, uint64_t x, int64_t x_sb, int64_t x_sr) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (fmt != BT_BFP8 && fmt != BT_BFP4) return fail(BT_EINVAL, "put_bfp writes bfp8 or bfp4, not %d", fmt);
+  if (!exps || !vals || !ids || !x) return fail(BT_EINVAL, "put_bfp needs its planes, ids and x");
+  if (batch < 1 || dst_rows < 1 || cols < 16 || cols % 16 || n < 0 || dst_sb % 16 || dst_sr % 16)
+    return fail(BT_EINVAL, "put_bfp shape: batch %lld, %lld rows of %lld (a multiple of 16), strides %lld %lld",
+                (long long)batch, (long long)dst_rows, (long long)cols, (long long)dst_sb, (long long)dst_sr);
+  if (ids % 4 || x % 2) return fail(BT_EINVAL, "put_bfp needs aligned ids and x");
+  if (n == 0) return BT_OK;
+  if (n >= (1ll << 31)) return fail(BT_EINVAL, "put_bfp: too many rows");
+  if (fmt == BT_BFP8)
+    put_bfp_kernel<BT_BFP8><<<(unsigned)n, 256, 0, r->stream>>>((uint8_t *)exps, (uint8_t *)vals, dst_rows, cols, dst_sb,
+                                                               dst_sr, (const int32_t *)ids, n, (const uint16_t *)x, x_sb,
+                                                               x_sr, batch);
+  else
+    put_bfp_kernel<BT_BFP4><<<(unsigned)n, 256, 0, r->stream>>>((uint8_t *)exps, (uint8_t *)vals, dst_rows, cols, dst_sb,
+                                                               dst_sr, (const int32_t *)ids, n, (const uint16_t *)x, x_sb,
+                                                               x_sr, batch);
+  BT_LAUNCHED("put_bfp");
   return BT_OK;
 }
 

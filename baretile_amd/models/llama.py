@@ -209,8 +209,31 @@ def upload(rt, w, c, places=None):
 
 
 def kv_cache(rt, c, size):
-  """A (2 * kv, size, head) bf16 cache of zeros per block: key heads, then value heads (llama.py:365-373)."""
-  return [Tensor.zeros(rt, size, head(c), batch=2 * c.kv) for _ in range(c.layers)]
+  """A (2 * kv, size, head) cache of zeros per block: key heads, then value heads (llama.py:365-373), in the format
+  c.precision gives the KV cache (bf16, or a block float: bfp8, bfp4)."""
+  fmt = (c.precision or {}).get(("kv", None), ("bf16", None))[0] or "bf16"
+  return [Tensor.zeros(rt, size, head(c), batch=2 * c.kv).cast(fmt).realize() for _ in range(c.layers)]
+
+
+_aranges = {}
+
+
+def _arange(rt, n):  # an int32 row 0 .. n-1, made once per runtime (a recording finds it made)
+  key = (id(rt), n)
+  if key not in _aranges or _aranges[key].rt is not rt: _aranges[key] = Tensor.of(rt, [list(range(n))], "int32")
+  return _aranges[key]
+
+
+def rope_into(qkv, cos, sin, cache, rows, c):
+  """RoPE of each token's heads with the key and value heads put into the cache at rows (llama.py:132-160): one
+  kernel for a bf16 cache (rope_put); a block-float cache takes the rows from a bf16 stage through put, which rounds
+  each run of 16 as a cast does (kernels.py:1083-1168). Returns the query heads, (tokens, heads * head)."""
+  if cache.dtype == "bf16": return qkv.rope_put(cos, sin, cache, rows, c.heads, c.kv)
+  n = qkv.rows
+  stage = Tensor(qkv.rt, n, head(c), batch=2 * c.kv)
+  q = qkv.rope_put(cos, sin, stage, _arange(qkv.rt, n), c.heads, c.kv)
+  cache.put(rows, stage)
+  return q
 
 
 def rms(x, w, c):
@@ -234,8 +257,8 @@ def attention(h, p, c, rot, places, cache, rows, firsts=None):
   rep = c.heads // c.kv
   qkv = h.matmul(p["qkv_proj"])
   n = qkv.rows
-  q = qkv.reshape(n, qkv.cols).rope_put(rot[0].reshape(n, rot[0].cols), rot[1].reshape(n, rot[1].cols),
-                                         cache, rows, c.heads, c.kv).split(c.heads)
+  q = rope_into(qkv.reshape(n, qkv.cols), rot[0].reshape(n, rot[0].cols), rot[1].reshape(n, rot[1].cols), cache,
+                rows, c).split(c.heads)
   k, v = cache[:c.kv, :, :], cache[c.kv:, :, :]
   o = q.attend(k.repeat_interleave(rep), v.repeat_interleave(rep), places, firsts=firsts, merged=True)
   return o.matmul(p["o_proj"], "fp32")
@@ -277,8 +300,12 @@ def row_layer(x, p, c, rot, places, cache, rows):
   products, and silu(gate) * up inside the down product (bt_matmul_row, bt_matmul_row_rope). Each fused step rounds
   once, in fp32, where the lazy graph rounds each operation to bf16."""
   rep = c.heads // c.kv
-  q = x.matmul_row(p["qkv_proj"], norm=p["input_layernorm"], eps=c.eps,
-                   rope=(rot[0], rot[1], cache, rows, c.heads, c.kv)).split(c.heads)
+  if cache.dtype == "bf16":
+    q = x.matmul_row(p["qkv_proj"], norm=p["input_layernorm"], eps=c.eps,
+                     rope=(rot[0], rot[1], cache, rows, c.heads, c.kv)).split(c.heads)
+  else:  # a block-float cache: the rows go in through put
+    qkv = x.matmul_row(p["qkv_proj"], "bf16", norm=p["input_layernorm"], eps=c.eps)
+    q = rope_into(qkv, rot[0].reshape(1, rot[0].cols), rot[1].reshape(1, rot[1].cols), cache, rows, c).split(c.heads)
   o = q.attend(cache[:c.kv, :, :].repeat_interleave(rep), cache[c.kv:, :, :].repeat_interleave(rep), places)
   x = o.matmul_row(p["o_proj"], "fp32", residual=x)
   gate_up = x.matmul_row(p["gate_up_proj"], "bf16", norm=p["post_attention_layernorm"], eps=c.eps)
@@ -292,6 +319,7 @@ def slots_layer(x, p, c, rot, keys, values, place):
   each slot's row; place is a (1, 1) int32 row. The slots' query heads become S * heads attention heads of one row.
   RoPE and the cache puts run as one kernel (bt_rope_put), in fp32 with one rounding."""
   S, hd, rep = x.rows, head(c), c.heads // c.kv
+  if keys.dtype != "bf16": raise ValueError("slots_layer takes bf16 caches")
   h = rms(x, p["input_layernorm"], c)
   q = h.matmul(p["qkv_proj"]).rope_put(rot[0], rot[1], keys, place, c.heads, c.kv, values=values)
   o = q.reshape(S * c.heads, 1, hd).attend(keys.repeat_interleave(rep), values.repeat_interleave(rep),

@@ -60,10 +60,10 @@ def _bf16_bits(values):
 class Storage:
   """Device memory that tensors share, freed when the last tensor using it goes. Memory allocated while a jit
   recording captures belongs to the recording too, which keeps it for as long as its graph can replay."""
-  __slots__ = ("rt", "addr", "nbytes", "columns", "captured", "__weakref__")
+  __slots__ = ("rt", "addr", "nbytes", "columns", "captured", "vals", "__weakref__")
 
   def __init__(self, rt, nbytes):
-    self.rt, self.nbytes, self.columns, self.addr = rt, nbytes, None, None
+    self.rt, self.nbytes, self.columns, self.addr, self.vals = rt, nbytes, None, None, 0
     self.captured = rt.recording is not None
     self.addr = rt.dram_alloc(max(256, nbytes))
     if self.captured: rt.recording.storages.append(self)
@@ -111,10 +111,12 @@ class Tensor:
       if layout == "columns": n = self.batch * _tiles_bytes(self.rows, self.cols, self.dtype)
       else:
         e, v = _planes(self.rows, self.cols, self.dtype)
-        n = self.batch * (-(-e // 256) * 256 + v)
+        n = -(-self.batch * e // 256) * 256 + self.batch * v
     elif layout == "columns": n = self.batch * _tiles_bytes(self.rows, self.cols, "bf16")
     else: n = self.batch * self.rows * self.cols * ITEMSIZE[self.dtype]
     self.storage = Storage(self.rt, n)
+    if self.dtype in BFP and layout == "plain":  # the value plane follows the exponent plane, 256-byte aligned
+      self.storage.vals = -(-self.batch * _planes(self.rows, self.cols, self.dtype)[0] // 256) * 256
     self.offset, self.sb, self.sr, self.sc = 0, self.rows * self.cols, self.cols, 1
     self.rep, self.cyc = 1, 0
     return self
@@ -125,10 +127,16 @@ class Tensor:
   @property
   def itemsize(self): return ITEMSIZE.get(self.dtype, 1)
 
-  def _bfp_planes(self):  # (exponent plane, value plane) addresses of a plain block-float tensor
-    e, _ = _planes(self.rows, self.cols, self.dtype)
-    exps = self.storage.addr
-    return exps, exps + -(-self.batch * e // 256) * 256
+  def _bfp_planes(self):
+    """(exponent plane, value plane) addresses of element (0, 0, 0) of a plain block-float tensor or view: a value's
+    exponent byte sits at its index / 16, its q at its index (bfp8) or index / 2 (bfp4); offsets count values."""
+    base = self.storage.addr
+    return base + self.offset // 16, base + self.storage.vals + (self.offset if self.dtype == "bfp8" else self.offset // 2)
+
+  def _bfp_whole(self):  # a plain block float read as whole, contiguous matrices (for unpacking and re-laying)
+    if not self._contiguous():
+      raise ValueError("a block-float view reads back, casts or lays out by columns only as whole, contiguous matrices")
+    return self
 
   @property
   def shape(self): return (*self.lead, self.rows, self.cols)
@@ -233,7 +241,7 @@ class Tensor:
         fmt = _lib.DTYPES[t.dtype]
         self.rt.run("readback", "columns_unpack", fmt, t.storage.addr, t.batch, t.rows, t.cols, out.storage.addr)
       else:
-        e, v = t._bfp_planes()
+        e, v = t._bfp_whole()._bfp_planes()
         self.rt.run("readback", "bfp_unpack", _lib.DTYPES[t.dtype], e, v, t.batch, t.rows, t.cols, out.storage.addr)
       t = out
     if not t._contiguous(): t = t._copy()
@@ -257,8 +265,10 @@ class Tensor:
   # ---- views
   def _view(self, rows, cols, batch, offset, sb, sr, sc, rep=1, cyc=0):
     t = self.realize()
-    if t.dtype in BFP or t.layout != "plain":
-      raise ValueError("a block float or a tensor by columns can only be a matmul's B, read back, or cast")
+    whole_runs = t.dtype in BFP and cols % 16 == 0 and sc == 1 and offset % 16 == 0 and sr % 16 == 0 and sb % 16 == 0
+    if t.layout != "plain" or (t.dtype in BFP and not whole_runs):
+      raise ValueError("a tensor by columns can only be a matmul's B, read back, or cast; a block-float view keeps "
+                       "whole runs of 16 along its rows")
     v = Tensor.__new__(Tensor)
     v.__dict__.update(t.__dict__)
     v.rows, v.cols, v.batch, v.lead = rows, cols, batch, (batch,)
@@ -490,7 +500,7 @@ class Tensor:
         self.rt.run("storage", "columns_unpack", _lib.DTYPES[x.dtype], x.storage.addr, x.batch, x.rows, x.cols,
                     out.storage.addr)
       else:
-        e, v = x._bfp_planes()
+        e, v = x._bfp_whole()._bfp_planes()
         self.rt.run("storage", "bfp_unpack", _lib.DTYPES[x.dtype], e, v, x.batch, x.rows, x.cols, out.storage.addr)
       return out.cast(dtype)
     if dtype in BFP:
@@ -518,7 +528,7 @@ class Tensor:
     out._alloc("columns")
     out.lead = x.lead
     if x.dtype in BFP:
-      e, v = x._bfp_planes()
+      e, v = x._bfp_whole()._bfp_planes()
       self.rt.run("columns", "bfp_columns", _lib.DTYPES[x.dtype], e, v, x.batch, x.rows, x.cols, out.storage.addr)
     else:
       if x.rep != 1 or x.cyc: x = x.contiguous()
@@ -780,8 +790,9 @@ class Tensor:
     own (llama.py:293-318's slots). merged writes the result as merge() of it, (rows, heads * width)."""
     if len(self.shape) > 3: raise ValueError(f"attend takes three dimensions, not {self.shape}")
     if window < 0 or parts is not None and parts <= 0: raise ValueError("attention needs a nonnegative window and positive parts")
-    if not (self.dtype == "bf16" and k.dtype == v.dtype == "bf16" and self.batch == k.batch == v.batch):
-      raise ValueError(f"attend needs bf16 queries, keys and values, equal batches: {self.dtype} {k.dtype} {v.dtype}")
+    if not (self.dtype == "bf16" and k.dtype == v.dtype and k.dtype in ("bf16", *BFP) and self.batch == k.batch == v.batch):
+      raise ValueError(f"attend needs bf16 queries, keys and values in bf16 or one block-float format, equal batches: "
+                       f"{self.dtype} {k.dtype} {v.dtype}")
     if not (self.cols == k.cols == v.cols and self.cols in (64, 128) and k.rows == v.rows):
       raise ValueError(f"attend needs heads 64 or 128 wide and a value for each key: {self.shape} {k.shape} {v.shape}")
     if not (places.rows == self.rows and places.batch in (1, self.batch) and places.cols == 1 and places.dtype == "int32"):
@@ -797,6 +808,9 @@ class Tensor:
     args = _lib.AttentionArgs(q.addr, k.addr, v.addr, out.addr, places.addr, q.sb, q.sr, k.sb, k.sr, v.sb, v.sr,
                               osh, osr, q.rows if places.batch > 1 else 0, q.batch, rep, q.rows, k.rows, q.cols,
                               window, parts or 0, 0, 0, 0)
+    if k.dtype in BFP:  # a block-float cache, read in place (test_kernels.py:2106-2132)
+      (args.k_exps, args.k), (args.v_exps, args.v) = k._bfp_planes(), v._bfp_planes()
+      args.kv_fmt = _lib.DTYPES[k.dtype]
     if firsts is not None:
       if not (firsts.rows == self.rows and firsts.batch in (1, self.batch) and firsts.cols == 1 and firsts.dtype == "int32"):
         raise ValueError(f"attend needs firsts as an int32 column with a row for each query: {firsts.shape}")
@@ -818,7 +832,7 @@ class Tensor:
     k, v, places = k.realize(), v.realize(), places.realize()
     if k.rep != v.rep or k.cyc or v.cyc: raise ValueError("attend needs keys and values repeated alike")
     if q.sc != 1 or q.rep != 1 or q.cyc: q = q.contiguous()
-    if k.sc != 1: k = k.contiguous()
+    if k.sc != 1: k = k.contiguous()  # a block-float view keeps whole runs, so its columns are contiguous already
     if v.sc != 1: v = v.contiguous()
     if not places._contiguous(): places = places.contiguous()
     return q, k, v, places, k.rep
@@ -873,14 +887,19 @@ class Tensor:
     """Write the rows of x at the places in ids, in place; a later duplicate wins (tensor.py:223-241)."""
     if not (ids.dtype == "int32" and ids.shape[-3:-1] == (1, 1) and ids.cols == x.rows):
       raise ValueError("put needs ids as an int32 row, with one position for each row of x")
-    if not ((x.batch, x.cols) == (self.batch, self.cols) and x.dtype == self.dtype):
+    want = "bf16" if self.dtype in BFP else self.dtype  # into a block float (a bfp8/bfp4 cache), bf16 rows
+    if not ((x.batch, x.cols) == (self.batch, self.cols) and x.dtype == want):
       raise ValueError(f"put needs rows of the cache's batch, width and dtype: {x.shape} {x.dtype} into {self.shape} {self.dtype}")
-    if self.dtype in BFP: raise ValueError("a block-float cache is outside this backend's KV path; use bf16")
     dst = self.realize()
     if dst.rep != 1 or dst.cyc or dst.sc != 1: raise ValueError("put requires a plain tensor with rep=1")
     x, ids = x.realize(), ids.realize()
     if x.sc != 1 or x.rep != 1 or x.cyc: x = x.contiguous()
     if not ids._contiguous(): ids = ids.contiguous()
+    if dst.dtype in BFP:  # each run of 16 rounded as cast rounds it (kernels.py:1083-1168)
+      e, v = dst._bfp_planes()
+      self.rt.run("put", "put_bfp", _lib.DTYPES[dst.dtype], e, v, dst.batch, dst.rows, dst.cols,
+                  dst.sb if dst.batch > 1 else 0, dst.sr, ids.addr, ids.cols, x.addr, x.sb if x.batch > 1 else 0, x.sr)
+      return self
     self.rt.run("put", "put", _lib.DTYPES[dst.dtype], dst.addr, dst.batch, dst.rows, dst.cols,
                 dst.sb if dst.batch > 1 else 0, dst.sr, ids.addr, ids.cols, x.addr, x.sb if x.batch > 1 else 0, x.sr)
     return self

@@ -253,7 +253,12 @@ int bt_matmul_row_rope(bt_runtime *rt, const bt_row_args *args, const bt_rope_ar
  * parts splits a decode step's keys (at most 64 query rows per key head: rep * rows <= 64) between that many blocks,
  * as attention_kernel's parts does; 0 picks a count from the shape. With more than one part the blocks write fp32
  * partial sums into scratch (bt_attention_scratch gives the bytes; 16-byte aligned) and a second launch combines
- * them. Calls that share one scratch buffer must not overlap. */
+ * them. Calls that share one scratch buffer must not overlap.
+ *
+ * A block-float cache (kv_fmt BT_BFP8 or BT_BFP4, test_kernels.py:2106-2132) is read in place and gives, bit for bit,
+ * the result of the bf16 values it holds: k and v are then the value planes' and k_exps, v_exps the exponent planes'
+ * addresses of element (0, 0) of key head 0, with the plain layout's rules (a value's q at its index, or index / 2
+ * for bfp4, its exponent byte at index / 16); strides, in values, are multiples of 16. */
 typedef struct {
   uint64_t q, k, v, out, places;
   int64_t q_sh, q_sr, k_sh, k_sr, v_sh, v_sr, o_sh, o_sr, places_sh;
@@ -261,6 +266,9 @@ typedef struct {
   uint64_t scratch, scratch_bytes;
   uint64_t firsts;    /* 0, or int32 with the first key each row sees (head stride firsts_sh: 0 or rows) */
   int64_t firsts_sh;
+  int32_t kv_fmt;     /* BT_BF16 (0), or a block-float cache: BT_BFP8, BT_BFP4 */
+  int32_t pad2_;
+  uint64_t k_exps, v_exps; /* with a block-float cache: k and v are value planes, these the exponent planes */
 } bt_attention_args;
 int bt_attention(bt_runtime *rt, const bt_attention_args *args);
 /* The scratch bytes bt_attention needs for args (0 when it runs in one part). */
@@ -275,6 +283,11 @@ int bt_gather(bt_runtime *rt, int dtype, uint64_t table, int64_t rows, int64_t c
  * skipped. dst and x share dtype (bf16, fp32, int32). */
 int bt_put(bt_runtime *rt, int dtype, uint64_t dst, int64_t batch, int64_t dst_rows, int64_t cols, int64_t dst_sb,
            int64_t dst_sr, uint64_t ids, int64_t n, uint64_t x, int64_t x_sb, int64_t x_sr);
+/* bt_put into a plain block-float tensor (a bfp8 or bfp4 KV cache, kernels.py:1083-1168): x is bf16 and each run of 16
+ * of a row is rounded as bt_bfp_pack rounds it, bit for bit. exps and vals are the exponent and value planes'
+ * addresses of element (0, 0, 0); cols and the destination's strides (in values) are multiples of 16. */
+int bt_put_bfp(bt_runtime *rt, int fmt, uint64_t exps, uint64_t vals, int64_t batch, int64_t dst_rows, int64_t cols,
+               int64_t dst_sb, int64_t dst_sr, uint64_t ids, int64_t n, uint64_t x, int64_t x_sb, int64_t x_sr);
 
 /* ---- top-k: replaces topk_kernel (Tensor.topk, tensor.py:685-706) ----------------------------------------------
  * values[b, r, p * k + j] and ids[b, r, p * k + j]: the k largest of part p of row r (parts equal parts of cols), in

@@ -108,6 +108,25 @@ def test_slots_layer_matches_each_slot_in_numpy(rt):
       assert np.abs(got_r - want_r).max() <= 0.03 * np.abs(want_r).max(), (s, np.abs(got_r - want_r).max())
 
 
+def test_block_float_kv_cache_matches_numpy(rt):
+  # the KV cache in bfp8 (precision's kv entry, tt_transformers' cache format, llama.py:74-83): a prompt's logits and
+  # a one-token step (the row kernels, with the rows put through the block-float put) within 3% of the oracle's,
+  # whose cache keeps the unrounded values
+  c, ref, dc, dw = setup(rt, 2, 256, "bfp8")
+  dc.precision = llama.precision(llama.model(layers=2, dim=576), "bfp8", kv="bfp8")
+  caches = llama.kv_cache(rt, dc, 96)
+  assert caches[0].dtype == "bfp8"
+  ids = [7, 200, 31, 64, 5, 9, 100, 3]
+  got = np.array(llama.forward(Tensor.of(rt, [ids], "int32"), Tensor.of(rt, [list(range(8))], "int32"), dw, dc, caches,
+                               every=True).tolist())
+  rcaches = L.kv_cache(c, 96)
+  want = L.forward(ids, range(8), ref, c, rcaches, every=True)
+  assert np.abs(got - want).max() <= 0.03 * np.abs(want).max(), np.abs(got - want).max()
+  step = np.array(llama.forward(Tensor.of(rt, [[42]], "int32"), Tensor.of(rt, [[8]], "int32"), dw, dc, caches).tolist())[0]
+  want = L.forward([42], [8], ref, c, rcaches)[0]
+  assert np.abs(step - want).max() <= 0.03 * np.abs(want).max(), np.abs(step - want).max()
+
+
 def test_loaded_checkpoint_matches_numpy(rt, tmp_path):
   # llama.load (safetensors, llama.py:429-462) -> upload in bfp8 -> a prompt's logits, against the oracle on the
   # same weights (their bf16 values, block floats rounded by oracle.bfp), within test_models.py:849's 3%

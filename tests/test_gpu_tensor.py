@@ -358,6 +358,44 @@ def test_matmul_row_rope_equals_two_calls(rt, fmt, k, hd, heads, kv):
   assert np.any(value(c1).reshape(2 * kv, size, hd)[:, place])
 
 
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4"])
+def test_block_float_cache(rt, fmt):
+  # test_kernels.py:2106-2132: put writes bf16 rows into a block-float cache, each run of 16 rounded as cast rounds it,
+  # bit for bit (one row, rows in two places, a run of 32, the edges, a later duplicate winning); attention reads
+  # the cache in place, each key and value head serving two query heads, and gives bit for bit what it gives on the
+  # same values in bf16, through the decode kernel (5 query rows) and the prefill kernel (40).
+  rng = np.random.default_rng(16)
+  cache = Tensor.of(rt, np.zeros((4, 96, 64), np.float32)).cast(fmt).realize()
+  want = np.zeros((4, 96, 64))
+  for places in ([5], [33, 34, 70], list(range(32, 64)), [0, 95], [7, 9, 7]):
+    x = B.bf16(rng.normal(0, 2, (4, len(places), 64)) * 10.0 ** rng.integers(-3, 3, (4, len(places), 1)))
+    cache.put(Tensor.of(rt, [places], "int32"), Tensor.of(rt, x.astype(np.float32)))
+    cast = value(Tensor.of(rt, x.astype(np.float32)).cast(fmt)).reshape(4, len(places), 64)
+    for i, p in enumerate(places): want[:, p] = cast[:, i]
+    assert np.array_equal(value(cache).reshape(4, 96, 64), want), (fmt, places)
+  same = Tensor.of(rt, want.astype(np.float32))  # the same values in bf16
+  kb, vb = cache[0:2, :, :].repeat_interleave(2), cache[2:4, :, :].repeat_interleave(2)
+  ks, vs = same[0:2, :, :].repeat_interleave(2), same[2:4, :, :].repeat_interleave(2)
+  for rows in (5, 40):
+    q = Tensor.of(rt, B.bf16(rng.normal(0, 1, (4, rows, 64)) / 8).astype(np.float32))
+    pl = Tensor.of(rt, rng.integers(60, 96, (1, rows, 1)).astype(np.int32), "int32")
+    assert q.attend(kb, vb, pl).tobytes() == q.attend(ks, vs, pl).tobytes(), (fmt, rows)
+
+
+def test_block_float_cache_long_decode(rt):
+  # a 2000-row bfp8 cache of 128-wide heads, decode split into parts and combined, against the bf16 values
+  rng = np.random.default_rng(21)
+  x = B.bf16(rng.normal(0, 1, (4, 2000, 128)))
+  cache = Tensor.of(rt, np.zeros((4, 2000, 128), np.float32)).cast("bfp8").realize()
+  cache.put(Tensor.of(rt, [list(range(2000))], "int32"), Tensor.of(rt, x.astype(np.float32)))
+  same = Tensor.of(rt, value(cache).reshape(4, 2000, 128).astype(np.float32))
+  q = Tensor.of(rt, B.bf16(rng.normal(0, 1, (8, 1, 128)) / 11).astype(np.float32))
+  pl = Tensor.of(rt, [[[1990]]], "int32")
+  got = q.attend(cache[0:2, :, :].repeat_interleave(4), cache[2:4, :, :].repeat_interleave(4), pl, parts=8)
+  want = q.attend(same[0:2, :, :].repeat_interleave(4), same[2:4, :, :].repeat_interleave(4), pl, parts=8)
+  assert got.tobytes() == want.tobytes()
+
+
 def test_rope_put_slots(rt):
   # the slots' layout: separate key and value caches of rows * kv heads, row i's heads at i * kv, one place for all
   # rows (llama.slots_layer); against the same float64 RoPE, and nothing else written
