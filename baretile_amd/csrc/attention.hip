@@ -65,8 +65,42 @@ __device__ __forceinline__ KvSrc kv_src(uint64_t vals, uint64_t exps, int64_t he
   }
   return s;
 }
-// 8 values from value e on (e a multiple of 8), as bf16 pairs: a block float decoded exactly as the unpacker
-// decodes it (its exponent byte at e / 16).
+// 8 block-float values sharing exponent byte x, as bf16 pairs, exactly as the unpacker decodes them: q (bfp8: 8
+// signed bytes in lo, hi; bfp4: 8 signed nibbles in lo) times 2^(x - 133) (bfp8) or 2^(x - 129) (bfp4). For x in
+// 7..254 that product is a normal float whose top half is the exact bf16 (a 7-bit magnitude times a power of two);
+// other x go through the unpacker's modular exponent rule value by value.
+template <int KF>
+__device__ __forceinline__ uint4 kv_decode8(uint32_t lo, uint32_t hi, uint32_t x) {
+  int q[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    if (KF == BT_BFP8) q[i] = (int)(int8_t)(((i < 4 ? lo : hi) >> (8 * (i % 4))) & 255u);
+    else q[i] = ((int)(lo << (28 - 4 * i))) >> 28;
+  }
+  uint32_t w[4];
+  if (x >= 7 && x <= 254) {
+    const float sc = __uint_as_float((x - (KF == BT_BFP8 ? 133u : 129u) + 127u) << 23);
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+      w[p] = (__float_as_uint((float)q[2 * p] * sc) >> 16) | (__float_as_uint((float)q[2 * p + 1] * sc) & 0xFFFF0000u);
+  } else {
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+      w[p] = unpacked_bits(KF == BT_BFP8 ? q[2 * p] : q[2 * p] * 16, x) |
+             unpacked_bits(KF == BT_BFP8 ? q[2 * p + 1] : q[2 * p + 1] * 16, x) << 16;
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+// The value bytes of 8 values from value e on (e a multiple of 8): bfp8 two words, bfp4 one.
+template <int KF>
+__device__ __forceinline__ uint2 kv_raw8(const KvSrc &s, uint32_t e) {
+  if (KF == BT_BFP8) {
+    const auto q = __builtin_amdgcn_raw_buffer_load_b64(s.val, e, 0, 0);
+    return make_uint2(q[0], q[1]);
+  }
+  return make_uint2(__builtin_amdgcn_raw_buffer_load_b32(s.val, e / 2, 0, 0), 0u);
+}
+// 8 values from value e on (e a multiple of 8), as bf16 pairs; a block float's exponent byte read at e / 16.
 template <int KF>
 __device__ __forceinline__ uint4 kv_load8(const KvSrc &s, uint32_t e) {
   if (KF == BT_BF16) {
@@ -74,21 +108,16 @@ __device__ __forceinline__ uint4 kv_load8(const KvSrc &s, uint32_t e) {
     return make_uint4(v[0], v[1], v[2], v[3]);
   }
   const uint32_t x = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(s.exp, e / 16, 0, 0);
-  uint32_t w[4] = {0, 0, 0, 0};
-  if (KF == BT_BFP8) {
-    const auto q = __builtin_amdgcn_raw_buffer_load_b64(s.val, e, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-      w[i / 2] |= unpacked_bits((int)(int8_t)((q[i / 4] >> (8 * (i % 4))) & 255u), x) << (16 * (i % 2));
-  } else {
-    const uint32_t q = __builtin_amdgcn_raw_buffer_load_b32(s.val, e / 2, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const int nib = (int)((q >> (4 * i)) & 15u);
-      w[i / 2] |= unpacked_bits((nib >= 8 ? nib - 16 : nib) * 16, x) << (16 * (i % 2));
-    }
-  }
-  return make_uint4(w[0], w[1], w[2], w[3]);
+  const uint2 q = kv_raw8<KF>(s, e);
+  return kv_decode8<KF>(q.x, q.y, x);
+}
+// A row's HD / 16 exponent bytes (row start e, a multiple of 16), for decoding its pieces one by one.
+template <int KF, int HD>
+__device__ __forceinline__ uint2 kv_row_exps(const KvSrc &s, uint32_t e) {
+  if (KF == BT_BF16) return make_uint2(0, 0);
+  if (HD == 64) return make_uint2(__builtin_amdgcn_raw_buffer_load_b32(s.exp, e / 16, 0, 0), 0u);
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(s.exp, e / 16, 0, 0);
+  return make_uint2(v[0], v[1]);
 }
 
 // A lane's pair: which query row it is, which keys it sees, where its q and output rows are.
@@ -292,16 +321,29 @@ __global__ void __launch_bounds__(256) attention_decode_kernel(const bt_attentio
   for (int c = 0; c < HD / 16; c++) st.o[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const KvSrc kr = kv_src<KF>(a.k, a.k_exps, (int64_t)kvh * a.k_sh, (int64_t)(a.keys - 1) * a.k_sr + HD);
   const KvSrc vr = kv_src<KF>(a.v, a.v_exps, (int64_t)kvh * a.v_sh, (int64_t)(a.keys - 1) * a.v_sr + HD);
+  // a key row's exponents in one load when every row's start in the plane is aligned to their HD / 16 bytes
+  const bool wide = a.k_sr % HD == 0 && a.k_sh % HD == 0 && a.k_exps % (HD / 16) == 0;
   uint16_t *vl = lds + wib * VR;
   constexpr int RPI = 64 * 8 / HD;  // value rows one load instruction covers
   const int vrow = lane / (HD / 8), vcol = lane % (HD / 8) * 8;
   for (int kb = first + KB * wib; kb <= last; kb += 4 * KB) {
     bf16x8 kf[4][HD / 32];
 #pragma unroll
-    for (int kt = 0; kt < 4; kt++)
+    for (int kt = 0; kt < 4; kt++) {
+      const uint32_t row = (uint32_t)((int64_t)(kb + 16 * kt + n) * a.k_sr);
+      if (KF == BT_BF16 || !wide) {
 #pragma unroll
-      for (int kk = 0; kk < HD / 32; kk++)
-        kf[kt][kk] = as_bf16x8(kv_load8<KF>(kr, (uint32_t)((int64_t)(kb + 16 * kt + n) * a.k_sr + 32 * kk + 8 * g)));
+        for (int kk = 0; kk < HD / 32; kk++) kf[kt][kk] = as_bf16x8(kv_load8<KF>(kr, row + 32 * kk + 8 * g));
+      } else {  // the row's exponents once, then each piece's values
+        const uint2 xs = kv_row_exps<KF, HD>(kr, row);
+#pragma unroll
+        for (int kk = 0; kk < HD / 32; kk++) {
+          const int run = 2 * kk + g / 2;
+          const uint2 q = kv_raw8<KF>(kr, row + 32 * kk + 8 * g);
+          kf[kt][kk] = as_bf16x8(kv_decode8<KF>(q.x, q.y, ((run < 4 ? xs.x : xs.y) >> (8 * (run % 4))) & 255u));
+        }
+      }
+    }
     uint4 vv[KB / RPI];
 #pragma unroll
     for (int i = 0; i < KB / RPI; i++)

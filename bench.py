@@ -322,6 +322,34 @@ def c1_leg(cpu_seconds, check=True):
   return res, cpu
 
 
+def bfp8_cache_leg(rt, args, k, v, kvh, keys, hd, out, E, rows, check):
+  """The decode case's K and V as a bfp8 cache (precision's kv entry, llama.py:74-83), read in place by the same
+  attention call: bytes are the block floats' (1088 per 1024 values) plus q and out. Parity: bit for bit the bf16
+  result on the cache's values."""
+  from baretile_amd import _lib
+  from baretile_amd.tensor import Tensor
+  kc = Tensor.frombytes(rt, keys, hd, bf16_bits(k).tobytes(), kvh).cast("bfp8")
+  vc = Tensor.frombytes(rt, keys, hd, bf16_bits(v).tobytes(), kvh).cast("bfp8")
+  saved = (args.k, args.v, args.kv_fmt, args.k_exps, args.v_exps)
+  (args.k_exps, args.k), (args.v_exps, args.v) = kc._bfp_planes(), vc._bfp_planes()
+  args.kv_fmt = _lib.DTYPES["bfp8"]
+  us = graph_us(rt, lambda: _lib.call("attention", rt.handle, byref(args)), 50)
+  nbytes = 2 * kvh * keys * hd * 1088 // 1024 + 2 * E * rows * hd * 2
+  entry = {"us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1), "frac_hbm_peak": round(nbytes / us / 1e3 / PEAK_GBS, 4),
+           "bytes": nbytes}
+  if check:  # the same call on the cache's values in bf16
+    got = bytes(rt.download(out, E * rows * hd * 2))
+    ks, vs = kc.cast("bf16").realize(), vc.cast("bf16").realize()
+    args.k, args.v, args.kv_fmt, args.k_exps, args.v_exps = ks.addr, vs.addr, 0, 0, 0
+    _lib.call("attention", rt.handle, byref(args))
+    rt.wait()
+    entry["parity"] = got == bytes(rt.download(out, E * rows * hd * 2))
+  args.k, args.v, args.kv_fmt, args.k_exps, args.v_exps = saved
+  rt.wait()
+  log("attention", "decode bfp8 cache", entry)
+  return entry
+
+
 def attention_leg(check=True):
   """bf16 q, k, v N(0, 1), 32 query heads over 8 key heads of 128 (batch entries fold into heads),
   fp32 softmax, bf16 out. Decode: 1 query row against 512, 4096 and 16384 keys at batch 1 and 8, HBM-bound (bytes:
@@ -368,6 +396,8 @@ def attention_leg(check=True):
         entry["parity"] = bool(np.allclose(got.reshape(4, rows, hd), want, rtol=0.011, atol=0.011))
       res[name] = entry
       log("attention", name, entry)
+      if kind == "decode" and batch == 8 and keys == 16384:  # beside it: the same cache in bfp8, read in place
+        res[name + "_bfp8_cache"] = bfp8_cache_leg(rt, args, k, v, kvh, keys, hd, out, E, rows, check)
       rt.wait()
       for d in bufs + [dp, out]: rt.dram_free(d)
       if need.value: rt.dram_free(args.scratch)
