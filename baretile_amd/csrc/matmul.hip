@@ -953,12 +953,16 @@ gemm2_kernel(const MatmulArgs args, int mblocks, int nblocks) {
 // same place in both halves, and writes silu(gate) * up for those 128 columns (out: m x f, bf16): the gate and up
 // values rounded to bf16 as stored, silu(g) = g / (1 + exp(-g)) and the product in fp32, rounded once.
 constexpr int GEMM_PLAIN = 0, GEMM_RES = 1, GEMM_SWIGLU = 2;
-template <int DT, int S, int MODE = GEMM_PLAIN>
+// BM: the block's rows, 256 or 128 (a wave BM / 2 of them by 64 columns), for products whose 256-row blocks would
+// leave CUs idle.
+template <int DT, int S, int MODE = GEMM_PLAIN, int BM = 256>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand res) {
   constexpr bool RES = MODE == GEMM_RES;
-  constexpr int BM = 256, BN = 256, STAGE = 32768, A_BYTES = 16384, WM = 8, WN = 4;
-  constexpr int ESZ = DT == BT_FP32 ? 4 : 2, ES = BN * ESZ + 16, HALF = DT == BT_FP32 ? 128 : 256;
+  constexpr int BN = 256, A_BYTES = BM * 64, STAGE = A_BYTES + 16384, WM = BM / 32, WN = 4, WR = BM / 2;
+  constexpr int AL = BM / 128;  // A loads a wave issues a step
+  constexpr int ESZ = DT == BT_FP32 ? 4 : 2, ES = BN * ESZ + 16;
+  constexpr int HALF = (DT == BT_FP32 ? 128 : 256) < BM ? (DT == BT_FP32 ? 128 : 256) : BM;
   constexpr int LDS = RES ? S * STAGE : S * STAGE > HALF * ES ? S * STAGE : HALF * ES;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS];
   const Head h = early_head(args);
@@ -984,9 +988,9 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
   uint32_t asrc[2], bsrc[2];
 #pragma unroll
   for (int j = 0; j < 2; j++) {
-    const int li = wib + 8 * j;  // rows 16 li .. 16 li + 15 of A, tile li of B
+    const int li = wib + 8 * j;  // rows 16 li .. 16 li + 15 of A (li < BM / 16), tile li of B
     const int r = 16 * li + lane / 4, c = (lane & 3) ^ ((r >> 1) & 3);
-    asrc[j] = m0 + r < h.m ? (uint32_t)(((int64_t)(m0 + r) * h.a.sr + 8 * c) * 2) : NOWHERE;
+    asrc[j] = j < AL && m0 + r < h.m ? (uint32_t)(((int64_t)(m0 + r) * h.a.sr + 8 * c) * 2) : NOWHERE;
     int run = n0 / 16 + li;
     bool in = run < h.nruns;
     if (MODE == GEMM_SWIGLU) {  // tiles 0..7: gate columns from 128 bn, 8..15: the same up columns
@@ -1002,7 +1006,7 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int li = wib + 8 * j;
-      lds_load16(ar, asrc[j] == NOWHERE ? NOWHERE : asrc[j] + ao, st + li * 1024);
+      if (j < AL) lds_load16(ar, asrc[j] == NOWHERE ? NOWHERE : asrc[j] + ao, st + li * 1024);
       lds_load16(br, bsrc[j] == NOWHERE ? NOWHERE : bsrc[j] + bo, st + A_BYTES + li * 1024);
     }
   };
@@ -1017,7 +1021,7 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
     if (t < steps) issue(t);
   for (int t = 0; t < steps; t++) {
     // step t landed once at most the later steps' loads are outstanding (fewer near the end)
-    if (t + S - 2 < steps) wait_vm<4 * (S - 2)>();
+    if (t + S - 2 < steps) wait_vm<(AL + 2) * (S - 2)>();
     else wait_vm<0>();
     __syncthreads();
     if (t + S - 1 < steps) issue(t + S - 1);  // into the stage step t - 1 used
@@ -1025,7 +1029,7 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
     bf16x8 fa[WM], fb[WN];
 #pragma unroll
     for (int i = 0; i < WM; i++) {
-      const int r = wm * 128 + 16 * i + col;
+      const int r = wm * WR + 16 * i + col;
       fa[i] = *(const bf16x8 *)(st + r * 64 + 16 * (g ^ ((r >> 1) & 3)));
     }
 #pragma unroll
@@ -1042,7 +1046,7 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
     for (int i = 0; i < WM; i++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const int m = m0 + wm * 128 + 16 * i + 4 * g + r;
+        const int m = m0 + wm * WR + 16 * i + 4 * g + r;
         if (m >= h.m) continue;
 #pragma unroll
         for (int j = 0; j < WN; j++) {
@@ -1066,7 +1070,7 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
         for (int j = 0; j < WN; j++)
 #pragma unroll
           for (int r = 0; r < 4; r++) {
-            uint8_t *at = lds + ((BM == HALF ? wm * 128 : 0) + 16 * i + 4 * g + r) * ES + (wn * 64 + 16 * j + col) * ESZ;
+            uint8_t *at = lds + ((BM == HALF ? wm * WR : 0) + 16 * i + 4 * g + r) * ES + (wn * 64 + 16 * j + col) * ESZ;
             if (DT == BT_FP32) *(float *)at = acc[i][j][r];
             else *(uint16_t *)at = (uint16_t)bf16_packed(acc[i][j][r]);
           }
@@ -1491,19 +1495,24 @@ static void launch_gemm_dt(const MatmulArgs &args, hipStream_t s) {
     if (sc > score + 1e-9) score = sc, best = o;
   }
   if constexpr (FMT == BT_BF16) {
-    if (best == 0 && args.k % 32 == 0) {
-      const int mb = (args.m + 255) / 256, nb = (args.n + 255) / 256;
+    bt_operand res{};
+    if (args.m > 128 && args.k % 32 == 0 && (DT == BT_BF16 || residual_program(args, &res))) {
+      // 256 or 128 rows a block: whichever fills the CUs' rounds better, 128-row blocks counted at 0.85 of the speed
+      auto fill = [&](int bm) {
+        const int64_t blocks = (int64_t)args.batch * ((args.m + bm - 1) / bm) * ((args.n + 255) / 256);
+        return (double)blocks / (double)((blocks + 255) / 256 * 256);
+      };
+      const int bm = fill(256) >= 0.85 * fill(128) ? 256 : 128;
+      const int mb = (args.m + bm - 1) / bm, nb = (args.n + 255) / 256;
       const unsigned blocks = (unsigned)((int64_t)mb * nb * args.batch);
       if constexpr (DT == BT_BF16) {
-        gemm3_kernel<DT, 4><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
-        return;
+        if (bm == 256) gemm3_kernel<DT, 4><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
+        else gemm3_kernel<DT, 4, GEMM_PLAIN, 128><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
       } else {
-        bt_operand res{};
-        if (residual_program(args, &res)) {
-          gemm3_kernel<DT, 4, GEMM_RES><<<blocks, 512, 0, s>>>(args, mb, nb, res);
-          return;
-        }
+        if (bm == 256) gemm3_kernel<DT, 4, GEMM_RES><<<blocks, 512, 0, s>>>(args, mb, nb, res);
+        else gemm3_kernel<DT, 4, GEMM_RES, 128><<<blocks, 512, 0, s>>>(args, mb, nb, res);
       }
+      return;
     }
   }
   if constexpr (DT != BT_FP32) {

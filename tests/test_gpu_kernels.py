@@ -214,10 +214,11 @@ def test_fused_relu_epilogue_config1(rt):
 
 
 # (rows, K, N, output): rows > 64 run the tiled GEMM, except up to 256 rows when its 128 x 128 blocks would be fewer
-# than 128 (then the skinny kernel: 96 x 1536 here). 2048 x 8192 picks its 256 x 256 blocks, 2048 x 4096 in fp32 its
-# 256 x 128 blocks, the rest 128 x 128 blocks; 1000 and 520 leave a partial chunk of K and a partial run of N.
+# than 128 (then the skinny kernel: 96 x 1536 here). With bf16 B (block floats unpacked to it from 512 rows up) and
+# K in 32s, 2048 x 8192 takes 256 x 256 blocks, 2048 x 4096 (fp32 with the residual) and 1000 x 4096 blocks of 128
+# rows; 1000 and 520 leave partial blocks, chunks of K and runs of N.
 GEMM_CASES = [(300, 1000, 520, "bf16"), (96, 576, 1536, "fp32"), (2048, 256, 8192, "bf16"), (2048, 192, 4096, "fp32"),
-              (160, 320, 8192, "bf16")]
+              (160, 320, 8192, "bf16"), (1000, 224, 4096, "bf16")]
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bfp4"])
