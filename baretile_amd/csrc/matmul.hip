@@ -393,6 +393,139 @@ __global__ void __launch_bounds__(SL ? 512 : 256) gemv_kernel(const MatmulArgs a
 // neighbours in the grid, so they read it at the same time. Loads go out as in gemv_kernel: a group of G chunks
 // together and unconditionally, past the last chunk (and for rows past the last) reading zeros through the buffers'
 // ranges; the weights non-temporal when a run has a single reader.
+// Two 16-row tiles of A against two neighbouring runs a wave (17 to 64 rows): each A fragment loaded feeds both
+// runs, halving the loads of A per run, which is what limits the one-run kernel here (its texture units stay busy
+// with A's 16-byte reads while HBM idles). A run's 64 exponent bytes come in one 4-byte load a lane and are handed
+// to the lanes that use them with ds_bpermute. Otherwise as skinny_vec_kernel: groups of G chunks issued together
+// and unconditionally, B scaled by its exponents into bf16, K split into slices summed in order in LDS.
+// RES: fp32 out plus an fp32 residual (the epilogue program `x + r`), added straight from the accumulators.
+template <int FMT, int DT, int G, bool PROG, bool SL, bool RES = false>
+__global__ void __launch_bounds__(SL ? 512 : 256) skinny2_kernel(const MatmulArgs args, int slices_arg,
+                                                                 const bt_operand res) {
+  constexpr int TB = Tile<FMT>::bytes, MT = 2, NR = 2;
+  extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];  // with slices: each wave's partial tiles
+  f32x4 *red = (f32x4 *)dyn;
+  const int slices = SL ? slices_arg : 1;
+  const Head h = early_head(args);
+  const int groups = (h.mtiles + MT - 1) / MT, pairs = (h.nruns + NR - 1) / NR, per = pairs * groups;
+  const SlicePos p = slice_pos(h.batch * per, h.chunks, slices, G);
+  if (slices == 1 && !p.valid) return;
+  const int lane = p.lane, g = p.g, col = p.col;
+  const int b = p.unit / per, rem = p.unit % per;
+  const int run0 = (groups == 1 ? rem : rem / groups) * NR, mg = groups == 1 ? 0 : rem % groups;
+  const int chunks = p.valid ? p.c_end - p.c_begin : 0;  // this wave's slice
+  const int row0 = mg * MT * 16, rows = min(MT * 16, h.m - row0);
+  __amdgpu_buffer_rsrc_t tr[NR];
+#pragma unroll
+  for (int r = 0; r < NR; r++) {
+    const bool in = run0 + r < h.nruns;
+    const uint8_t *tiles = h.b + (h.b_matrix_bytes ? b * h.b_matrix_bytes : 0) +
+                           ((int64_t)(in ? run0 + r : 0) * h.chunks + p.c_begin) * TB;
+    tr[r] = buffer(tiles, in ? (uint32_t)chunks * TB : 0u);
+  }
+  const uint16_t *abase = (const uint16_t *)h.a.ptr + operand_matrix(h.a, b) * h.a.sb + (int64_t)row0 * h.a.sr;
+  const uint32_t abytes = (uint32_t)(((int64_t)(rows - 1) * h.a.sr + h.k) * 2);
+  const __amdgpu_buffer_rsrc_t ar = buffer(abase, abytes);
+  uint32_t arow[MT];
+#pragma unroll
+  for (int t = 0; t < MT; t++)
+    arow[t] = t * 16 + col < rows ? (uint32_t)((t * 16 + col) * h.a.sr * 2 + p.c_begin * 128) : abytes;
+  f32x4 acc[NR * MT];
+#pragma unroll
+  for (int i = 0; i < NR * MT; i++) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c0 = 0; c0 < chunks; c0 += G) {
+    uint4 bq[G][NR], bh[G][NR], a0[G][MT], a1[G][MT];
+    uint32_t ew[G][NR];
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      const uint32_t at = (uint32_t)(c0 + i) * TB, ak = (uint32_t)(c0 + i) * 128 + 16 * g;
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+        if (FMT == BT_BF16) {
+          const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr[r], at + 32 * lane, 0, 0);
+          const auto u = __builtin_amdgcn_raw_buffer_load_b128(tr[r], at + 32 * lane + 16, 0, 0);
+          bq[i][r] = make_uint4(q[0], q[1], q[2], q[3]);
+          bh[i][r] = make_uint4(u[0], u[1], u[2], u[3]);
+        } else {
+          if (FMT == BT_BFP8) {
+            const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr[r], at + 64 + 16 * lane, 0, 0);
+            bq[i][r] = make_uint4(q[0], q[1], q[2], q[3]);
+          } else {
+            const auto q = __builtin_amdgcn_raw_buffer_load_b64(tr[r], at + 64 + 8 * lane, 0, 0);
+            bq[i][r] = make_uint4(q[0], q[1], 0, 0);
+          }
+          ew[i][r] = __builtin_amdgcn_raw_buffer_load_b32(tr[r], at + 4 * col, 0, 0);  // exponent word col of 16
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < MT; t++) {
+        const auto x0 = __builtin_amdgcn_raw_buffer_load_b128(ar, arow[t] + ak, 0, 0);
+        const auto x1 = __builtin_amdgcn_raw_buffer_load_b128(ar, arow[t] + ak + 64, 0, 0);
+        a0[i][t] = make_uint4(x0[0], x0[1], x0[2], x0[3]);
+        a1[i][t] = make_uint4(x1[0], x1[1], x1[2], x1[3]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      if (c0 + i >= chunks) continue;
+#pragma unroll
+      for (int r = 0; r < NR; r++) {
+        bf16x8 bv[2];
+        if (FMT == BT_BF16) {
+          bv[0] = *(const bf16x8 *)&bq[i][r];
+          bv[1] = *(const bf16x8 *)&bh[i][r];
+        } else {
+          // the lane's 16 exponent bytes (rows 8g + j, then 32 + 8g + j): words 4g .. 4g + 3, held by lanes 4g ..
+          uint32_t ex[4];
+#pragma unroll
+          for (int k = 0; k < 4; k++) ex[k] = (uint32_t)__shfl((int)ew[i][r], 4 * g + k, 64);
+          if (FMT == BT_BFP8) {
+            bv[0] = q8_to_bf16<true>(make_uint2(bq[i][r].x, bq[i][r].y), make_uint2(ex[0], ex[1]));
+            bv[1] = q8_to_bf16<true>(make_uint2(bq[i][r].z, bq[i][r].w), make_uint2(ex[2], ex[3]));
+          } else {
+            bv[0] = q4_to_bf16_scaled(bq[i][r].x, make_uint2(ex[0], ex[1]));
+            bv[1] = q4_to_bf16_scaled(bq[i][r].y, make_uint2(ex[2], ex[3]));
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+          acc[r * MT + t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)&a0[i][t], bv[0], acc[r * MT + t], 0, 0, 0);
+          acc[r * MT + t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)&a1[i][t], bv[1], acc[r * MT + t], 0, 0, 0);
+        }
+      }
+    }
+  }
+  if (SL && slices > 1) sum_slices<NR * MT>(acc, p, slices, red);
+  if (p.s != 0 || !p.valid) return;
+  if constexpr (RES) {
+    const bt_operand &out = h.out;
+    const int64_t ob = operand_matrix(out, b) * out.sb, rb = res.ptr ? operand_matrix(res, b) * res.sb : 0;
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      const int n = (run0 + r) * 16 + col;
+      if (n >= h.n) continue;
+#pragma unroll
+      for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int m = (mg * MT + t) * 16 + 4 * g + i;
+          if (m >= h.m) continue;
+          float v = acc[r * MT + t][i];
+          if (res.ptr) v += ((const float *)res.ptr)[rb + (int64_t)m * res.sr + (int64_t)n * res.sc];
+          ((float *)out.ptr)[ob + (int64_t)m * out.sr + (int64_t)n * out.sc] = v;
+        }
+    }
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < NR; r++) {
+    if (run0 + r >= h.nruns) continue;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+      store_tile<DT, false, false, PROG ? 1 : 0>(args, h, acc[r * MT + t], b, mg * MT + t, run0 + r, g, col);
+  }
+}
+
 template <int FMT, int DT, int G, bool ONE, bool PROG, int MT, bool SL>
 __global__ void __launch_bounds__(SL ? 512 : 256) skinny_vec_kernel(const MatmulArgs args, int slices_arg) {
   constexpr int TB = Tile<FMT>::bytes;
@@ -1365,6 +1498,22 @@ static int choose_slices(int64_t units, int chunks) {
   return sl;
 }
 
+static bool residual_program(const MatmulArgs &args, bt_operand *res);
+
+// Slices of the two-runs-a-wave skinny kernel: from K = 2048 up (below it, sums in the GEMM's order), up to 8 while
+// the launch stays under 2048 waves and each slice keeps 32 chunks or more.
+static int pair_slices(const MatmulArgs &args) {
+  const int64_t units2 = (int64_t)args.batch * ((args.nruns + 1) / 2) * ((args.mtiles + 1) / 2);
+  int sl = 1;
+  while (sl < 8 && units2 * sl < 2048 && args.chunks >= 32 * 2 * sl) sl *= 2;
+  return sl;
+}
+// Whether it launches 1024 waves or more; with fewer, one run a wave keeps more of them in flight.
+static bool pairs_fill(const MatmulArgs &args) {
+  const int64_t units2 = (int64_t)args.batch * ((args.nruns + 1) / 2) * ((args.mtiles + 1) / 2);
+  return units2 * pair_slices(args) >= 1024;
+}
+
 template <class Kernel>
 static void launch_sliced(Kernel kernel, const MatmulArgs &args, int64_t units, int slices, int slot_bytes,
                           int tile_bytes, hipStream_t s) {
@@ -1426,6 +1575,17 @@ static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bo
     } else if (two && args.chunks <= 2) {  // short K (a head's width): groups of 2
       if (args.n_inst) launch_sliced(skinny_vec_kernel<FMT, DT, 2, false, true, 2, true>, args, units, sl, 0, 2048, s);
       else launch_sliced(skinny_vec_kernel<FMT, DT, 2, false, false, 2, true>, args, units, sl, 0, 2048, s);
+    } else if (two && pairs_fill(args)) {  // two runs a wave: half the units, each slice's partial 4 tiles
+      const int64_t units2 = (int64_t)args.batch * ((args.nruns + 1) / 2) * ((args.mtiles + 1) / 2);
+      const int sl2 = pair_slices(args);
+      const int wpb = sl2 == 8 ? 8 : 4;
+      const unsigned blocks = (unsigned)((units2 * sl2 + wpb - 1) / wpb);
+      const size_t lds = sl2 > 1 ? (size_t)wpb * 4096 : 0;
+      bt_operand res{};
+      if (DT == BT_FP32 && residual_program(args, &res))
+        skinny2_kernel<FMT, DT, 4, false, true, true><<<blocks, wpb * 64, lds, s>>>(args, sl2, res);
+      else if (args.n_inst) skinny2_kernel<FMT, DT, 4, true, true><<<blocks, wpb * 64, lds, s>>>(args, sl2, res);
+      else skinny2_kernel<FMT, DT, 4, false, true><<<blocks, wpb * 64, lds, s>>>(args, sl2, res);
     } else if (two) {
       if (args.n_inst) launch_sliced(skinny_vec_kernel<FMT, DT, 8, false, true, 2, true>, args, units, sl, 0, 2048, s);
       else launch_sliced(skinny_vec_kernel<FMT, DT, 8, false, false, 2, true>, args, units, sl, 0, 2048, s);
