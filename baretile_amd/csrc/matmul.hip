@@ -398,6 +398,91 @@ __global__ void __launch_bounds__(SL ? 512 : 256) gemv_kernel(const MatmulArgs a
 // with A's 16-byte reads while HBM idles). A run's 64 exponent bytes come in one 4-byte load a lane and are handed
 // to the lanes that use them with ds_bpermute. Otherwise as skinny_vec_kernel: groups of G chunks issued together
 // and unconditionally, B scaled by its exponents into bf16, K split into slices summed in order in LDS.
+// Up to 32 rows of A (one matrix) with a short K (at most G chunks, G <= 12): the block stages all of A (at most
+// 48 KB) in LDS once while its waves' weights are in flight, and each of its 4 waves multiplies NRW runs of B from
+// there. A is read from memory once a block instead of once a run, which is what limits the one-run kernels at 16
+// rows (their A and exponent loads keep the texture units busy while HBM idles). Exponents as in skinny2_kernel.
+template <int FMT, int DT, int MT, int NRW, int G, bool PROG>
+__global__ void __launch_bounds__(256) skinny_lds_kernel(const MatmulArgs args) {
+  constexpr int TB = Tile<FMT>::bytes;
+  extern __shared__ __attribute__((aligned(16))) uint16_t la[];  // A: 16 MT rows, kp halfwords apart
+  const Head h = early_head(args);
+  const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
+  const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int chunks = h.chunks, kp = chunks * 64 + 8;  // padded rows: a fragment read's 16 rows hit distinct banks
+  const int run0 = ((int)blockIdx.x * 4 + wib) * NRW;
+  // 1. A's pieces for this thread (16 bytes each; rows past the last and columns past K are zeros), loaded before
+  // the weights so that staging them waits for these alone
+  const uint16_t *abase = (const uint16_t *)h.a.ptr;
+  const int pieces = chunks * 8, kw = h.k / 8, total = 16 * MT * pieces;
+  constexpr int AP = (16 * MT * 96 + 255) / 256;  // at most 12 chunks: 96 pieces a row
+  uint4 av[AP];
+#pragma unroll
+  for (int j = 0; j < AP; j++) {
+    const int q = (int)threadIdx.x + 256 * j, row = q / pieces, c8 = q % pieces;
+    av[j] = make_uint4(0, 0, 0, 0);
+    if (q < total && row < h.m && c8 < kw) av[j] = *(const uint4 *)(abase + (int64_t)row * h.a.sr + c8 * 8);
+  }
+  // 2. the wave's weights, in flight while A is staged and while earlier runs are multiplied
+  uint4 bq[NRW][G];
+  uint32_t ew[NRW][G];
+#pragma unroll
+  for (int r = 0; r < NRW; r++) {
+    const bool in = run0 + r < h.nruns;
+    const __amdgpu_buffer_rsrc_t tr = buffer(h.b + (int64_t)(in ? run0 + r : 0) * chunks * TB, in ? (uint32_t)chunks * TB : 0u);
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      const uint32_t at = (uint32_t)i * TB;
+      if (FMT == BT_BFP8) {
+        const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 64 + 16 * lane, 0, 0);
+        bq[r][i] = make_uint4(q[0], q[1], q[2], q[3]);
+      } else {
+        const auto q = __builtin_amdgcn_raw_buffer_load_b64(tr, at + 64 + 8 * lane, 0, 0);
+        bq[r][i] = make_uint4(q[0], q[1], 0, 0);
+      }
+      ew[r][i] = __builtin_amdgcn_raw_buffer_load_b32(tr, at + 4 * col, 0, 0);
+    }
+  }
+  // 3. A into LDS
+#pragma unroll
+  for (int j = 0; j < AP; j++) {
+    const int q = (int)threadIdx.x + 256 * j, row = q / pieces, c8 = q % pieces;
+    if (q < total) *(uint4 *)(la + row * kp + c8 * 8) = av[j];
+  }
+  __syncthreads();
+  // 4. each run: the chunks' products from A in LDS and the run's B, scaled by its exponents into bf16
+#pragma unroll
+  for (int r = 0; r < NRW; r++) {
+    f32x4 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      if (i >= chunks) continue;
+      uint32_t ex[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) ex[k] = (uint32_t)__shfl((int)ew[r][i], 4 * g + k, 64);
+      bf16x8 bv[2];
+      if (FMT == BT_BFP8) {
+        bv[0] = q8_to_bf16<true>(make_uint2(bq[r][i].x, bq[r][i].y), make_uint2(ex[0], ex[1]));
+        bv[1] = q8_to_bf16<true>(make_uint2(bq[r][i].z, bq[r][i].w), make_uint2(ex[2], ex[3]));
+      } else {
+        bv[0] = q4_to_bf16_scaled(bq[r][i].x, make_uint2(ex[0], ex[1]));
+        bv[1] = q4_to_bf16_scaled(bq[r][i].y, make_uint2(ex[2], ex[3]));
+      }
+#pragma unroll
+      for (int t = 0; t < MT; t++) {
+        const uint16_t *ar = la + (16 * t + col) * kp + 64 * i + 8 * g;
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)ar, bv[0], acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)(ar + 32), bv[1], acc[t], 0, 0, 0);
+      }
+    }
+    if (run0 + r < h.nruns)
+#pragma unroll
+      for (int t = 0; t < MT; t++) store_tile<DT, false, true, PROG ? 1 : 0>(args, h, acc[t], 0, t, run0 + r, g, col);
+  }
+}
+
 // RES: fp32 out plus an fp32 residual (the epilogue program `x + r`), added straight from the accumulators.
 template <int FMT, int DT, int G, bool PROG, bool SL, bool RES = false>
 __global__ void __launch_bounds__(SL ? 512 : 256) skinny2_kernel(const MatmulArgs args, int slices_arg,
@@ -1523,6 +1608,23 @@ static void launch_sliced(Kernel kernel, const MatmulArgs &args, int64_t units, 
   kernel<<<blocks, wpb * 64, lds, s>>>(args, slices);
 }
 
+template <int FMT, int DT, int MT, int NRW, int G>
+static void launch_lds_g(const MatmulArgs &args, unsigned blocks, size_t lds, hipStream_t s) {
+  if (args.n_inst) skinny_lds_kernel<FMT, DT, MT, NRW, G, true><<<blocks, 256, lds, s>>>(args);
+  else skinny_lds_kernel<FMT, DT, MT, NRW, G, false><<<blocks, 256, lds, s>>>(args);
+}
+template <int FMT, int DT, int MT, int NRW>
+static void launch_lds_n(const MatmulArgs &args, unsigned blocks, size_t lds, hipStream_t s) {
+  if (args.chunks <= 6) launch_lds_g<FMT, DT, MT, NRW, 6>(args, blocks, lds, s);
+  else if (args.chunks <= 9) launch_lds_g<FMT, DT, MT, NRW, 9>(args, blocks, lds, s);
+  else launch_lds_g<FMT, DT, MT, NRW, 12>(args, blocks, lds, s);
+}
+template <int FMT, int DT>
+static void launch_lds(const MatmulArgs &args, unsigned blocks, size_t lds, hipStream_t s) {
+  if (args.m > 16) launch_lds_n<FMT, DT, 2, 1>(args, blocks, lds, s);
+  else launch_lds_n<FMT, DT, 1, 1>(args, blocks, lds, s);
+}
+
 template <int FMT, int DT>
 static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bool vec) {
   const bool rows_contiguous = args.a.sc == 1 && (int64_t)args.k * 2 < (1ll << 31);
@@ -1558,6 +1660,12 @@ static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bo
       else if (group == 8) launch_sliced(gemv_kernel<FMT, DT, 4, 8, true, false, false>, args, units, 1, 8 * SB, 0, s);
       else launch_sliced(gemv_kernel<FMT, DT, 4, 12, true, false, false>, args, units, 1, 12 * SB, 0, s);
     }
+  } else if (FMT != BT_BF16 && vec && fits && args.batch == 1 && args.m <= 32 && args.chunks <= 12 &&
+             ((int64_t)(args.m - 1) * args.a.sr + args.k) * 2 < (1ll << 31)) {
+    // A staged whole in LDS once a block, a run a wave (more runs a wave measured slower: fewer waves in flight)
+    const unsigned blocks = (unsigned)((args.nruns + 3) / 4);
+    const size_t lds = (size_t)(args.m > 16 ? 32 : 16) * (args.chunks * 64 + 8) * 2;
+    launch_lds<FMT, DT>(args, blocks, lds, s);
   } else if (vec && fits && ((int64_t)31 * args.a.sr + 2 * (int64_t)args.k + 1024) * 2 < (1ll << 32)) {
     // two 16-row tiles a wave from 17 rows up; the waves of a run side by side. A short K (3-12 chunks) with many
     // rows: one tile a wave and all of K in one group of loads, so each wave makes one trip to memory.

@@ -213,6 +213,25 @@ def test_fused_relu_epilogue_config1(rt):
   assert np.all(np.abs(fused - np.maximum(ops.matmul(xw, wq), 0)) <= ops.matmul_bound(xw, wq))
 
 
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4"])
+@pytest.mark.parametrize("m,k,n", [(16, 576, 49152), (20, 576, 40000), (7, 320, 1000), (32, 768, 4096)])
+def test_short_k_rows_with_a_in_lds(rt, fmt, m, k, n):
+  # 5 to 32 rows and K of at most 12 chunks: A staged whole in LDS once a block of 4 runs, partial last blocks. Bit for bit the same product 4 rows at a time (the GEMV, same K order), within the
+  # reference's bound of the oracle, and with a relu epilogue program.
+  rng = np.random.default_rng(m * n + k)
+  x, w = rng.normal(0, 1, (m, k)), rng.normal(0, 0.05, (k, n)).astype(np.float32)
+  exps, vals = pack(rt, w, fmt)
+  cols, wq = columns(rt, exps, vals, fmt, 1, k, n), bfp_values(w, fmt)
+  got = matmul(rt, x, cols, fmt, 1, n)[0]
+  rows4 = np.concatenate([matmul(rt, x[i:i + 4], cols, fmt, 1, n)[0] for i in range(0, m, 4)])
+  assert np.array_equal(got, rows4)
+  xw = B.bf16(x)
+  assert np.all(np.abs(got - ops.matmul(xw, wq)) <= ops.matmul_bound(xw, wq))
+  p = Program("bf16", epilogue=True)
+  relu = matmul(rt, x, cols, fmt, 1, n, prog=p.build(p.op("relu", p.value())))[0]
+  assert np.array_equal(relu, np.maximum(got, 0))
+
+
 # (rows, K, N, output): rows > 64 run the tiled GEMM, except up to 256 rows when its 128 x 128 blocks would be fewer
 # than 128 (then the skinny kernel: 96 x 1536 here). With bf16 B (block floats unpacked to it from 512 rows up) and
 # K in 32s, 2048 x 8192 takes 256 x 256 blocks, 2048 x 4096 (fp32 with the residual) and 1000 x 4096 blocks of 128
