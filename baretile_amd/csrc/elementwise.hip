@@ -481,16 +481,36 @@ extern "C" int bt_rope_put(bt_runtime *rt, const bt_rope_args *args) {
 namespace bt {
 
 // RMSNorm of rows: a block a row, two passes over it (the second from cache).
+// RMSNorm of one row a block. Rows of up to 8192 columns (k a multiple of 4, 16-byte aligned rows) are fetched
+// whole into registers by 16-byte loads, all issued before the first is used, so a row costs one trip to memory;
+// longer or unaligned rows loop over the columns and read them twice.
+template <bool REGS>
 __global__ void __launch_bounds__(256) rms_rows_kernel(const float *x, int64_t k, int64_t x_sr, const uint16_t *w,
                                                        float eps, uint16_t *out, int64_t out_sr) {
   __shared__ float part[4];
   const int tid = threadIdx.x, lane = tid & 63, wib = tid >> 6;
   const float *xr = x + (int64_t)blockIdx.x * x_sr;
   uint16_t *o = out + (int64_t)blockIdx.x * out_sr;
+  constexpr int NV = 8;  // 16-byte groups a thread holds: 8 x 4 x 256 = 8192 columns
+  float4 v[REGS ? NV : 1];
   float ss = 0.0f;
-  for (int64_t c = tid; c < k; c += 256) {
-    const float v = round_packed(xr[c]);
-    ss += v * v;
+  if constexpr (REGS) {
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int64_t c = ((int64_t)i * 256 + tid) * 4;
+      v[i] = c < k ? *(const float4 *)(xr + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      v[i].x = round_packed(v[i].x), v[i].y = round_packed(v[i].y);
+      v[i].z = round_packed(v[i].z), v[i].w = round_packed(v[i].w);
+      ss += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
+    }
+  } else {
+    for (int64_t c = tid; c < k; c += 256) {
+      const float e = round_packed(xr[c]);
+      ss += e * e;
+    }
   }
 #pragma unroll
   for (int s = 32; s > 0; s >>= 1) ss += __shfl_xor(ss, s, 64);
@@ -498,7 +518,21 @@ __global__ void __launch_bounds__(256) rms_rows_kernel(const float *x, int64_t k
   __syncthreads();
   const float total = ((part[0] + part[1]) + part[2]) + part[3];
   const float r = 1.0f / sqrtf(total / (float)k + eps);
-  for (int64_t c = tid; c < k; c += 256) o[c] = (uint16_t)bf16_packed(round_packed(xr[c]) * r * bf16_value(w[c]));
+  if constexpr (REGS) {
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int64_t c = ((int64_t)i * 256 + tid) * 4;
+      if (c < k) {
+        const uint2 wv = *(const uint2 *)(w + c);
+        uint2 ov;
+        ov.x = bf16_packed(v[i].x * r * bf16_value(wv.x & 0xFFFFu)) | bf16_packed(v[i].y * r * bf16_value(wv.x >> 16)) << 16;
+        ov.y = bf16_packed(v[i].z * r * bf16_value(wv.y & 0xFFFFu)) | bf16_packed(v[i].w * r * bf16_value(wv.y >> 16)) << 16;
+        *(uint2 *)(o + c) = ov;
+      }
+    }
+  } else {
+    for (int64_t c = tid; c < k; c += 256) o[c] = (uint16_t)bf16_packed(round_packed(xr[c]) * r * bf16_value(w[c]));
+  }
 }
 
 }  // namespace bt
@@ -510,8 +544,9 @@ extern "C" int bt_rms_rows(bt_runtime *rt, uint64_t x, int64_t rows, int64_t k, 
   if (int s = enter(rt, &r)) return s;
   if (!x || !w || !out) return fail(BT_EINVAL, "rms_rows needs x, w and out");
   if (rows < 1 || rows >= (1ll << 31) || k < 1) return fail(BT_EINVAL, "rms_rows shape %lld x %lld", (long long)rows, (long long)k);
-  rms_rows_kernel<<<(unsigned)rows, 256, 0, r->stream>>>((const float *)(uintptr_t)x, k, x_sr, (const uint16_t *)(uintptr_t)w,
-                                                          eps, (uint16_t *)(uintptr_t)out, out_sr);
+  const bool regs = k <= 8192 && k % 4 == 0 && x % 16 == 0 && x_sr % 4 == 0 && w % 8 == 0 && out % 8 == 0 && out_sr % 4 == 0;
+  (regs ? rms_rows_kernel<true> : rms_rows_kernel<false>)<<<(unsigned)rows, 256, 0, r->stream>>>(
+      (const float *)(uintptr_t)x, k, x_sr, (const uint16_t *)(uintptr_t)w, eps, (uint16_t *)(uintptr_t)out, out_sr);
   BT_LAUNCHED("rms_rows");
   return BT_OK;
 }

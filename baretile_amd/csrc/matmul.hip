@@ -484,7 +484,10 @@ __global__ void __launch_bounds__(256) skinny_lds_kernel(const MatmulArgs args) 
 }
 
 // RES: fp32 out plus an fp32 residual (the epilogue program `x + r`), added straight from the accumulators.
-template <int FMT, int DT, int G, bool PROG, bool SL, bool RES = false>
+// SWI: B holds gate columns then up columns (n = 2f); a wave's two runs are gate run u and up run u + n / 32, and it
+// writes silu(g) * u for its 16 columns of the bf16 out (f wide), g and u rounded to bf16 first, as the tiled GEMM's
+// SiLU-mul epilogue does.
+template <int FMT, int DT, int G, bool PROG, bool SL, bool RES = false, bool SWI = false>
 __global__ void __launch_bounds__(SL ? 512 : 256) skinny2_kernel(const MatmulArgs args, int slices_arg,
                                                                  const bt_operand res) {
   constexpr int TB = Tile<FMT>::bytes, MT = 2, NR = 2;
@@ -497,15 +500,17 @@ __global__ void __launch_bounds__(SL ? 512 : 256) skinny2_kernel(const MatmulArg
   if (slices == 1 && !p.valid) return;
   const int lane = p.lane, g = p.g, col = p.col;
   const int b = p.unit / per, rem = p.unit % per;
-  const int run0 = (groups == 1 ? rem : rem / groups) * NR, mg = groups == 1 ? 0 : rem % groups;
+  const int pu = groups == 1 ? rem : rem / groups, mg = groups == 1 ? 0 : rem % groups;
+  const int run0 = pu * NR, half = h.nruns / 2;
   const int chunks = p.valid ? p.c_end - p.c_begin : 0;  // this wave's slice
   const int row0 = mg * MT * 16, rows = min(MT * 16, h.m - row0);
   __amdgpu_buffer_rsrc_t tr[NR];
 #pragma unroll
   for (int r = 0; r < NR; r++) {
-    const bool in = run0 + r < h.nruns;
+    const int run = SWI ? pu + r * half : run0 + r;
+    const bool in = run < h.nruns;
     const uint8_t *tiles = h.b + (h.b_matrix_bytes ? b * h.b_matrix_bytes : 0) +
-                           ((int64_t)(in ? run0 + r : 0) * h.chunks + p.c_begin) * TB;
+                           ((int64_t)(in ? run : 0) * h.chunks + p.c_begin) * TB;
     tr[r] = buffer(tiles, in ? (uint32_t)chunks * TB : 0u);
   }
   const uint16_t *abase = (const uint16_t *)h.a.ptr + operand_matrix(h.a, b) * h.a.sb + (int64_t)row0 * h.a.sr;
@@ -582,6 +587,20 @@ __global__ void __launch_bounds__(SL ? 512 : 256) skinny2_kernel(const MatmulArg
   }
   if (SL && slices > 1) sum_slices<NR * MT>(acc, p, slices, red);
   if (p.s != 0 || !p.valid) return;
+  if constexpr (SWI) {
+    const bt_operand &out = h.out;
+    const int n = pu * 16 + col;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int m = (mg * MT + t) * 16 + 4 * g + i;
+        if (m >= h.m) continue;
+        const float gv = bf16_value(bf16_packed(acc[t][i])), uv = bf16_value(bf16_packed(acc[MT + t][i]));
+        ((uint16_t *)out.ptr)[(int64_t)m * out.sr + n] = (uint16_t)bf16_packed(gv / (1.0f + expf(-gv)) * uv);
+      }
+    return;
+  }
   if constexpr (RES) {
     const bt_operand &out = h.out;
     const int64_t ob = operand_matrix(out, b) * out.sb, rb = res.ptr ? operand_matrix(res, b) * res.sb : 0;
@@ -2006,6 +2025,24 @@ extern "C" int bt_matmul_swiglu(bt_runtime *rt, const bt_operand *a, int b_fmt, 
   args.n_inst = 0;
   args.out = *out;
   if ((int64_t)args.chunks * args.nruns * 2048 >= (1ll << 32)) return fail(BT_EINVAL, "matmul_swiglu's B is too large");
+  const int mb = (int)((m + 255) / 256), nb = (int)((n / 2 + 127) / 128);
+  const int64_t gemm_blocks = ((m + 127) / 128) * ((n + 127) / 128);
+  if ((m <= 64 || (m <= 256 && gemm_blocks < 128)) && a->sr % 8 == 0 && a->ptr % 16 == 0 && ((31 * a->sr + 2 * k + 1024) * 2 < (1ll << 32))) {
+    // few rows: two 16-row tiles by a gate run and its up run a wave, reading B as it is stored (block floats
+    // included), so no scratch is needed
+    const int64_t units2 = (int64_t)(args.nruns / 2) * ((args.mtiles + 1) / 2);
+    const int sl = pair_slices(args);
+    const int wpb = sl == 8 ? 8 : 4;
+    const unsigned blocks = (unsigned)((units2 * sl + wpb - 1) / wpb);
+    const size_t lds = sl > 1 ? (size_t)wpb * 4096 : 0;
+    if (b_fmt == BT_BF16)
+      skinny2_kernel<BT_BF16, BT_BF16, 4, false, true, false, true><<<blocks, wpb * 64, lds, r->stream>>>(args, sl, bt_operand{});
+    else if (b_fmt == BT_BFP8)
+      skinny2_kernel<BT_BFP8, BT_BF16, 4, false, true, false, true><<<blocks, wpb * 64, lds, r->stream>>>(args, sl, bt_operand{});
+    else skinny2_kernel<BT_BFP4, BT_BF16, 4, false, true, false, true><<<blocks, wpb * 64, lds, r->stream>>>(args, sl, bt_operand{});
+    BT_LAUNCHED("matmul_swiglu");
+    return BT_OK;
+  }
   if (b_fmt != BT_BF16) {  // unpacked once into bf16 tiles in the runtime's scratch
     const int64_t tiles = (int64_t)args.chunks * args.nruns;
     void *bt16 = runtime_scratch(r, (size_t)tiles * 2048);
@@ -2016,7 +2053,6 @@ extern "C" int bt_matmul_swiglu(bt_runtime *rt, const bt_operand *a, int b_fmt, 
     BT_LAUNCHED("matmul_swiglu");
     args.b = (const uint8_t *)bt16;
   }
-  const int mb = (int)((m + 255) / 256), nb = (int)((n / 2 + 127) / 128);
   gemm3_kernel<BT_BF16, 4, GEMM_SWIGLU><<<(unsigned)((int64_t)mb * nb), 512, 0, r->stream>>>(args, mb, nb, bt_operand{});
   BT_LAUNCHED("matmul_swiglu");
   return BT_OK;

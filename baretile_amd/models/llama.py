@@ -267,7 +267,7 @@ def attention(h, p, c, rot, places, cache, rows, firsts=None):
 def mlp(h, p):
   """SwiGLU: silu(h @ gate) * (h @ up), then down, with gate and up side by side (llama.py:174-183)."""
   m = p["down_proj"].rows
-  if h.rows >= 256 and h.batch == 1 and m % 16 == 0 and h.cols % 32 == 0:  # a block of tokens: SiLU-mul as the epilogue
+  if h.batch == 1 and m % 16 == 0 and h.cols % 32 == 0:  # SiLU-mul as the product's epilogue
     return h.matmul_swiglu(p["gate_up_proj"]).matmul(p["down_proj"], "fp32")
   gate_up = h.matmul(p["gate_up_proj"])
   return (gate_up[:, :m].silu() * gate_up[:, m:]).matmul(p["down_proj"], "fp32")

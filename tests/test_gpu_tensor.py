@@ -422,23 +422,26 @@ def test_rope_put_slots(rt):
   assert not np.any(got_k[:, others]) and not np.any(got_v[:, others])
 
 
-def test_rms_rows(rt):
-  # RMSNorm of rows in one kernel (bt_rms_rows) against NumPy on the documented formula, to a bf16 rounding
+@pytest.mark.parametrize("rows,k", [(37, 1000), (32, 4096), (5, 8192), (3, 999), (2, 9000), (300, 576)])
+def test_rms_rows(rt, rows, k):
+  # RMSNorm of rows in one kernel (bt_rms_rows) against NumPy on the documented formula, to a bf16 rounding: rows
+  # held in registers (k a multiple of 4 up to 8192) and the two-pass loop (k = 999, 9000)
   rng = np.random.default_rng(7)
-  x = rng.normal(0, 3, (37, 1000)).astype(np.float32)
-  w = B.bf16(rng.normal(1, 0.1, 1000).astype(np.float32)).astype(np.float32)
+  x = rng.normal(0, 3, (rows, k)).astype(np.float32)
+  w = B.bf16(rng.normal(1, 0.1, k).astype(np.float32)).astype(np.float32)
   xb = packed(x).astype(np.float32)
   r = np.float32(1) / np.sqrt(np.mean(xb.astype(np.float64) ** 2, 1, keepdims=True).astype(np.float32) + np.float32(1e-5))
   want = xb * r * w
-  got = value(Tensor.of(rt, x, "fp32").rms_rows(Tensor.of(rt, w[None]), 1e-5)).reshape(37, 1000)
+  got = value(Tensor.of(rt, x, "fp32").rms_rows(Tensor.of(rt, w[None]), 1e-5)).reshape(rows, k)
   assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-30)
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bfp4"])
-def test_matmul_swiglu(rt, fmt):
+@pytest.mark.parametrize("m,k,f", [(300, 256, 272), (32, 576, 1536), (5, 256, 272), (48, 4096, 352)])
+def test_matmul_swiglu(rt, fmt, m, k, f):
   # silu(x @ gate) * (x @ up) with the SiLU-mul as the product's epilogue (bt_matmul_swiglu): against the unfused
-  # product's gate and up values (bit for bit the same sums) put through the documented formula, to a bf16 rounding
-  m, k, f = 300, 256, 272
+  # product's gate and up values put through the documented formula, to a bf16 rounding. 300 rows run the tiled GEMM;
+  # fewer, the kernel that takes a gate run and its up run a wave (48 x 4096: K split over two slices)
   rng = np.random.default_rng(11)
   x = Tensor.of(rt, rng.normal(0, 1, (m, k)).astype(np.float32))
   wt, _ = _weights(rt, k, 2 * f, fmt, 3)
