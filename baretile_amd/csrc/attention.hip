@@ -293,10 +293,11 @@ __device__ __forceinline__ void store_state(float *ws, const State<HD> &st, int 
     for (int i = 0; i < 4; i++) ws[32 + (4 * g + i) * HD + 16 * c + n] = st.o[c][i];
 }
 
-// Decode: block (kvh, t, part). The tile's visible keys, from its smallest first to its largest last, are cut into
+// Decode: block (kvh, t, part). Two waves a SIMD at least: the block-float caches' decoding would otherwise take
+// enough registers to leave one, and half the loads in flight. The tile's visible keys, from its smallest first to its largest last, are cut into
 // `parts` runs of whole 64-key blocks; the 4 waves take the part's blocks in turn.
 template <int HD, int KF>
-__global__ void __launch_bounds__(256) attention_decode_kernel(const bt_attention_args a, int tiles, int parts,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) attention_decode_kernel(const bt_attention_args a, int tiles, int parts,
                                                                float *scratch) {
   constexpr int VS = HD + 8, VR = KB * VS;  // halfwords of one wave's value block
   constexpr int PF = partial_floats<HD>();
