@@ -120,6 +120,37 @@ __device__ __forceinline__ uint2 kv_row_exps(const KvSrc &s, uint32_t e) {
   return make_uint2(v[0], v[1]);
 }
 
+// 8 values' bytes as loaded, decoded later (kv_value8): bf16 four words, bfp8 two, bfp4 one.
+template <int KF> struct Raw8 {
+  uint32_t w[KF == BT_BF16 ? 4 : KF == BT_BFP8 ? 2 : 1];
+};
+template <int KF>
+__device__ __forceinline__ Raw8<KF> kv_fetch8(const KvSrc &s, uint32_t e) {
+  Raw8<KF> r;
+  if constexpr (KF == BT_BF16) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(s.val, e * 2, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.w[i] = v[i];
+  } else {
+    const uint2 q = kv_raw8<KF>(s, e);
+    r.w[0] = q.x;
+    if constexpr (KF == BT_BFP8) r.w[1] = q.y;
+  }
+  return r;
+}
+template <int KF>
+__device__ __forceinline__ uint4 kv_value8(const Raw8<KF> &r, uint32_t x) {
+  if constexpr (KF == BT_BF16) return make_uint4(r.w[0], r.w[1], r.w[2], r.w[3]);
+  else if constexpr (KF == BT_BFP8) return kv_decode8<KF>(r.w[0], r.w[1], x);
+  else return kv_decode8<KF>(r.w[0], 0u, x);
+}
+// A block-float value's exponent byte (value e); 0 for bf16, which has none.
+template <int KF>
+__device__ __forceinline__ uint32_t kv_exp8(const KvSrc &s, uint32_t e) {
+  if constexpr (KF == BT_BF16) return 0u;
+  else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(s.exp, e / 16, 0, 0);
+}
+
 // A lane's pair: which query row it is, which keys it sees, where its q and output rows are.
 struct Pair {
   int lo, hi;  // visible keys lo..hi (empty when lo > hi)
@@ -149,19 +180,22 @@ template <int HD> struct State {
   f32x4 o[HD / 16];
 };
 
-// Folds one block of 64 keys starting at kb into st. kf: the K operand fragments (lane l: key kb + 16kt + l%16,
+// One block of 64 keys starting at kb. kf: the K operand fragments (lane l: key kb + 16kt + l%16,
 // dims 32kk + 8(l/16) .. +8). vl: the block's values in LDS, row-major with a row stride of VS halfwords.
-template <int HD, int VS>
-__device__ __forceinline__ void fold_block(State<HD> &st, const bf16x8 (&kf)[4][HD / 32], const bf16x8 (&qf)[HD / 32],
-                                           const uint16_t *vl, int kb, const Pair &pr, int lane) {
-  const int g = lane >> 4, n = lane & 15;
-  f32x4 s[4];
+// block_scores makes the block's scores S^T = K Q^T; fold_scores folds them and the values into st.
+template <int HD>
+__device__ __forceinline__ void block_scores(f32x4 (&s)[4], const bf16x8 (&kf)[4][HD / 32], const bf16x8 (&qf)[HD / 32]) {
 #pragma unroll
   for (int kt = 0; kt < 4; kt++) {
     s[kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int kk = 0; kk < HD / 32; kk++) s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kt][kk], qf[kk], s[kt], 0, 0, 0);
   }
+}
+template <int HD, int VS>
+__device__ __forceinline__ void fold_scores(State<HD> &st, f32x4 (&s)[4], const uint16_t *vl, int kb, const Pair &pr,
+                                            int lane) {
+  const int g = lane >> 4, n = lane & 15;
   float mx = -__builtin_inff();
 #pragma unroll
   for (int kt = 0; kt < 4; kt++)
@@ -293,17 +327,61 @@ __device__ __forceinline__ void store_state(float *ws, const State<HD> &st, int 
     for (int i = 0; i < 4; i++) ws[32 + (4 * g + i) * HD + 16 * c + n] = st.o[c][i];
 }
 
-// Decode: block (kvh, t, part). Two waves a SIMD at least: the block-float caches' decoding would otherwise take
-// enough registers to leave one, and half the loads in flight. The tile's visible keys, from its smallest first to its largest last, are cut into
-// `parts` runs of whole 64-key blocks; the 4 waves take the part's blocks in turn.
-template <int HD, int KF>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) attention_decode_kernel(const bt_attention_args a, int tiles, int parts,
-                                                               float *scratch) {
+// Decode: block (kvh, t, part). The tile's visible keys, from its smallest first to its largest last, are cut into
+// `parts` runs of whole 64-key blocks; the 4 waves take the part's blocks in turn. A wave's loads run a block ahead:
+// the next block's keys and values are fetched once the current scores are made (the current values are in LDS by
+// then), so they arrive while the current block is folded. Block-float bytes are held as loaded and decoded where they are
+// used. WIDE (block floats): every key row's exponents sit at a multiple of their HD / 16 bytes, one load a row.
+// Two waves a SIMD at least: the block-float caches' decoding would otherwise take enough registers to leave one.
+template <int HD, int KF, bool WIDE> struct KeyBytes {
+  static constexpr int XW = KF == BT_BF16 ? 1 : WIDE ? (HD == 64 ? 1 : 2) : HD / 32;
+  Raw8<KF> q[4][HD / 32];
+  uint32_t x[4][XW];
+};
+template <int HD, int KF, bool WIDE>
+__device__ __forceinline__ void fetch_keys(KeyBytes<HD, KF, WIDE> &kb_, const KvSrc &kr, int kb, int64_t k_sr, int lane) {
+  const int g = lane >> 4, n = lane & 15;
+#pragma unroll
+  for (int kt = 0; kt < 4; kt++) {
+    const uint32_t row = (uint32_t)((int64_t)(kb + 16 * kt + n) * k_sr);
+    if constexpr (KF != BT_BF16 && WIDE) {
+      const uint2 xs = kv_row_exps<KF, HD>(kr, row);
+      kb_.x[kt][0] = xs.x;
+      if constexpr (HD != 64) kb_.x[kt][1] = xs.y;
+    }
+#pragma unroll
+    for (int kk = 0; kk < HD / 32; kk++) {
+      kb_.q[kt][kk] = kv_fetch8<KF>(kr, row + 32 * kk + 8 * g);
+      if constexpr (KF != BT_BF16 && !WIDE) kb_.x[kt][kk] = kv_exp8<KF>(kr, row + 32 * kk + 8 * g);
+    }
+  }
+}
+template <int HD, int KF, bool WIDE>
+__device__ __forceinline__ void decode_keys(bf16x8 (&kf)[4][HD / 32], const KeyBytes<HD, KF, WIDE> &kb_, int lane) {
+  const int g = lane >> 4;
+#pragma unroll
+  for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+    for (int kk = 0; kk < HD / 32; kk++) {
+      uint32_t x = 0;
+      if constexpr (KF != BT_BF16 && WIDE) {
+        const int run = 2 * kk + g / 2;  // the piece's run of 16 in its row
+        x = ((run < 4 ? kb_.x[kt][0] : kb_.x[kt][KeyBytes<HD, KF, WIDE>::XW - 1]) >> (8 * (run % 4))) & 255u;
+      } else if constexpr (KF != BT_BF16) {
+        x = kb_.x[kt][kk];
+      }
+      kf[kt][kk] = as_bf16x8(kv_value8<KF>(kb_.q[kt][kk], x));
+    }
+}
+
+template <int HD, int KF, bool WIDE>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+attention_decode_kernel(const bt_attention_args a, int tiles, int parts, float *scratch) {
   constexpr int VS = HD + 8, VR = KB * VS;  // halfwords of one wave's value block
   constexpr int PF = partial_floats<HD>();
   static_assert(4 * PF * 4 <= 4 * VR * 2, "the wave partials fit in the value blocks' LDS");
   __shared__ __attribute__((aligned(16))) uint16_t lds[4 * VR];
-  const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+  const int lane = threadIdx.x & 63, n = lane & 15;
   const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int bid = blockIdx.x;
   const int part = bid % parts;
@@ -322,38 +400,42 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
   for (int c = 0; c < HD / 16; c++) st.o[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const KvSrc kr = kv_src<KF>(a.k, a.k_exps, (int64_t)kvh * a.k_sh, (int64_t)(a.keys - 1) * a.k_sr + HD);
   const KvSrc vr = kv_src<KF>(a.v, a.v_exps, (int64_t)kvh * a.v_sh, (int64_t)(a.keys - 1) * a.v_sr + HD);
-  // a key row's exponents in one load when every row's start in the plane is aligned to their HD / 16 bytes
-  const bool wide = a.k_sr % HD == 0 && a.k_sh % HD == 0 && a.k_exps % (HD / 16) == 0;
   uint16_t *vl = lds + wib * VR;
-  constexpr int RPI = 64 * 8 / HD;  // value rows one load instruction covers
+  constexpr int RPI = 64 * 8 / HD, VI = KB / RPI;  // value rows one load instruction covers; loads a block
   const int vrow = lane / (HD / 8), vcol = lane % (HD / 8) * 8;
-  for (int kb = first + KB * wib; kb <= last; kb += 4 * KB) {
-    bf16x8 kf[4][HD / 32];
+  KeyBytes<HD, KF, WIDE> kbytes;
+  Raw8<KF> vq[VI];
+  uint32_t vx[VI];
+  auto fetch_values = [&](int kb) {
 #pragma unroll
-    for (int kt = 0; kt < 4; kt++) {
-      const uint32_t row = (uint32_t)((int64_t)(kb + 16 * kt + n) * a.k_sr);
-      if (KF == BT_BF16 || !wide) {
-#pragma unroll
-        for (int kk = 0; kk < HD / 32; kk++) kf[kt][kk] = as_bf16x8(kv_load8<KF>(kr, row + 32 * kk + 8 * g));
-      } else {  // the row's exponents once, then each piece's values
-        const uint2 xs = kv_row_exps<KF, HD>(kr, row);
-#pragma unroll
-        for (int kk = 0; kk < HD / 32; kk++) {
-          const int run = 2 * kk + g / 2;
-          const uint2 q = kv_raw8<KF>(kr, row + 32 * kk + 8 * g);
-          kf[kt][kk] = as_bf16x8(kv_decode8<KF>(q.x, q.y, ((run < 4 ? xs.x : xs.y) >> (8 * (run % 4))) & 255u));
-        }
-      }
+    for (int i = 0; i < VI; i++) {
+      const uint32_t e = (uint32_t)((int64_t)(kb + vrow + RPI * i) * a.v_sr + vcol);
+      vq[i] = kv_fetch8<KF>(vr, e);
+      vx[i] = kv_exp8<KF>(vr, e);
     }
-    uint4 vv[KB / RPI];
-#pragma unroll
-    for (int i = 0; i < KB / RPI; i++)
-      vv[i] = kv_load8<KF>(vr, (uint32_t)((int64_t)(kb + vrow + RPI * i) * a.v_sr + vcol));
+  };
+  int kb = first + KB * wib;
+  if (kb <= last) {
+    fetch_keys<HD, KF, WIDE>(kbytes, kr, kb, a.k_sr, lane);
+    fetch_values(kb);
+  }
+  for (; kb <= last; kb += 4 * KB) {
+    const int next = kb + 4 * KB;
     wave_lds_sync();  // the previous block's reads of vl are done
 #pragma unroll
-    for (int i = 0; i < KB / RPI; i++) *(uint4 *)(vl + (vrow + RPI * i) * VS + vcol) = vv[i];
+    for (int i = 0; i < VI; i++) *(uint4 *)(vl + (vrow + RPI * i) * VS + vcol) = kv_value8<KF>(vq[i], vx[i]);
     wave_lds_sync();
-    fold_block<HD, VS>(st, kf, qf, vl, kb, pr, lane);
+    f32x4 s[4];
+    {
+      bf16x8 kf[4][HD / 32];
+      decode_keys<HD, KF, WIDE>(kf, kbytes, lane);
+      block_scores<HD>(s, kf, qf);
+    }
+    if (next <= last) {
+      fetch_keys<HD, KF, WIDE>(kbytes, kr, next, a.k_sr, lane);
+      fetch_values(next);
+    }
+    fold_scores<HD, VS>(st, s, vl, kb, pr, lane);
   }
   __syncthreads();
   float *ws = (float *)lds;
@@ -711,9 +793,13 @@ __global__ void __launch_bounds__(512, 1) attention_prefill_kernel(const bt_atte
 template <int HD>
 static void launch_decode_hd(const bt_attention_args &a, unsigned blocks, int tiles, int parts, float *scratch,
                              hipStream_t s) {
-  if (a.kv_fmt == BT_BFP8) attention_decode_kernel<HD, BT_BFP8><<<blocks, 256, 0, s>>>(a, tiles, parts, scratch);
-  else if (a.kv_fmt == BT_BFP4) attention_decode_kernel<HD, BT_BFP4><<<blocks, 256, 0, s>>>(a, tiles, parts, scratch);
-  else attention_decode_kernel<HD, BT_BF16><<<blocks, 256, 0, s>>>(a, tiles, parts, scratch);
+  // a key row's exponents in one load when every row's start in the plane is aligned to their HD / 16 bytes
+  const bool wide = a.k_sr % HD == 0 && a.k_sh % HD == 0 && a.k_exps % (HD / 16) == 0;
+  if (a.kv_fmt == BT_BFP8 && wide) attention_decode_kernel<HD, BT_BFP8, true><<<blocks, 256, 0, s>>>(a, tiles, parts, scratch);
+  else if (a.kv_fmt == BT_BFP8) attention_decode_kernel<HD, BT_BFP8, false><<<blocks, 256, 0, s>>>(a, tiles, parts, scratch);
+  else if (a.kv_fmt == BT_BFP4 && wide) attention_decode_kernel<HD, BT_BFP4, true><<<blocks, 256, 0, s>>>(a, tiles, parts, scratch);
+  else if (a.kv_fmt == BT_BFP4) attention_decode_kernel<HD, BT_BFP4, false><<<blocks, 256, 0, s>>>(a, tiles, parts, scratch);
+  else attention_decode_kernel<HD, BT_BF16, false><<<blocks, 256, 0, s>>>(a, tiles, parts, scratch);
 }
 static void launch_decode(const bt_attention_args &a, unsigned blocks, int tiles, int parts, float *scratch,
                           hipStream_t s) {
@@ -765,7 +851,11 @@ static int plan_attention(const bt_attention_args *a, AttnPlan *p) {
   if (p->decode) {
     const int nblk = (a->keys + KB - 1) / KB;
     int parts = a->parts;
-    if (parts == 0) parts = std::min((2048 + kvh * p->tiles - 1) / (kvh * p->tiles), (nblk + 3) / 4);
+    // bf16: one block a CU (MI355X's 256), each wave's loads a block ahead through all of its share of the keys;
+    // block floats: two a CU, so one block's decoding overlaps the other's loads. Measured faster than more,
+    // shorter-lived blocks at 1-32 batch entries and 4096-16384 keys.
+    const int target = a->kv_fmt == BT_BF16 ? 256 : 512;
+    if (parts == 0) parts = std::min((target + kvh * p->tiles / 2) / (kvh * p->tiles), (nblk + 3) / 4);
     p->parts = std::max(1, std::min(std::min(parts, nblk), MAX_PARTS));
     const int pf = 32 + 16 * a->head_dim;
     if (p->parts > 1) p->scratch_bytes = (uint64_t)kvh * p->tiles * p->parts * pf * 4;

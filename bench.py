@@ -330,22 +330,29 @@ def bfp8_cache_leg(rt, args, k, v, kvh, keys, hd, out, E, rows, check):
   from baretile_amd.tensor import Tensor
   kc = Tensor.frombytes(rt, keys, hd, bf16_bits(k).tobytes(), kvh).cast("bfp8")
   vc = Tensor.frombytes(rt, keys, hd, bf16_bits(v).tobytes(), kvh).cast("bfp8")
-  saved = (args.k, args.v, args.kv_fmt, args.k_exps, args.v_exps)
+  saved = (args.k, args.v, args.kv_fmt, args.k_exps, args.v_exps, args.scratch, args.scratch_bytes)
   (args.k_exps, args.k), (args.v_exps, args.v) = kc._bfp_planes(), vc._bfp_planes()
   args.kv_fmt = _lib.DTYPES["bfp8"]
+  need = ctypes.c_uint64()  # the block-float plan splits the keys its own way
+  _lib.call("attention_scratch", byref(args), byref(need))
+  scratch = rt.dram_alloc(need.value) if need.value else 0
+  args.scratch, args.scratch_bytes = scratch, need.value
   us = graph_us(rt, lambda: _lib.call("attention", rt.handle, byref(args)), 50)
   nbytes = 2 * kvh * keys * hd * 1088 // 1024 + 2 * E * rows * hd * 2
   entry = {"us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1), "frac_hbm_peak": round(nbytes / us / 1e3 / PEAK_GBS, 4),
            "bytes": nbytes}
-  if check:  # the same call on the cache's values in bf16
+  if check:  # the same call on the cache's values in bf16, split into the same parts
     got = bytes(rt.download(out, E * rows * hd * 2))
     ks, vs = kc.cast("bf16").realize(), vc.cast("bf16").realize()
     args.k, args.v, args.kv_fmt, args.k_exps, args.v_exps = ks.addr, vs.addr, 0, 0, 0
+    args.parts = need.value // (kvh * 4 * (32 + 16 * hd)) if need.value else 1  # one tile a key head
     _lib.call("attention", rt.handle, byref(args))
     rt.wait()
+    args.parts = 0
     entry["parity"] = got == bytes(rt.download(out, E * rows * hd * 2))
-  args.k, args.v, args.kv_fmt, args.k_exps, args.v_exps = saved
+  args.k, args.v, args.kv_fmt, args.k_exps, args.v_exps, args.scratch, args.scratch_bytes = saved
   rt.wait()
+  if scratch: rt.dram_free(scratch)
   log("attention", "decode bfp8 cache", entry)
   return entry
 
