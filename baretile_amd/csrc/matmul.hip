@@ -1042,6 +1042,137 @@ template <int N> __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 
+// Up to 32 rows of A (one matrix, K a multiple of 64) against a long K, in two launches. skinny_part_kernel cuts K
+// into splits of G chunks: block (group, split) stages its split of A's rows in LDS with direct loads, each of one
+// row's 1 KB (whole cache lines, where the fragment-shaped reads of the other skinny kernels take 16 rows' 64 bytes
+// at once, 8 KB or more apart), while its 4 waves' weights are in flight; each wave then multiplies NRW runs of B
+// from there and writes its fp32 partial tiles. A is read once a block instead of once a wave. parts_reduce_kernel
+// sums each output's splits in split order and runs the epilogue (rounding, program, or SiLU x up).
+template <int FMT, int MT, int NRW, int G>
+__global__ void __launch_bounds__(256) skinny_part_kernel(const MatmulArgs args, int groups, float *part) {
+  constexpr int TB = Tile<FMT>::bytes, KP = G * 64 + 8;  // padded rows: a fragment read's 16 rows hit distinct banks
+  __shared__ __attribute__((aligned(16))) uint16_t la[16 * MT * KP];
+  const Head h = early_head(args);
+  const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
+  const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = (int)blockIdx.x % groups, sp = (int)blockIdx.x / groups;
+  const int c0 = sp * G, cnt = min(G, h.chunks - c0);
+  const int run0 = (grp * 4 + wib) * NRW;
+  // 1. the split of A's rows into LDS: row r's G * 128 bytes in G / 8 loads of 1 KB, the block's waves taking them in
+  // turn (rows past the last read zeros: their offset lies past the buffer's range)
+  const uint32_t abytes = (uint32_t)(((int64_t)(h.m - 1) * h.a.sr + h.k) * 2);
+  const i32x4 ar = buffer_words((const void *)h.a.ptr, abytes);
+  constexpr int LOADS = 16 * MT * G / 8, PER = LOADS / 4;
+  static_assert(LOADS % 4 == 0, "each wave issues the same number of A loads");
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int q = wib + 4 * j, r = q / (G / 8), piece = q % (G / 8);
+    const uint32_t voff =
+        r < h.m ? (uint32_t)(((int64_t)r * h.a.sr + (int64_t)c0 * 64 + piece * 512) * 2) + 16u * lane : abytes;
+    lds_load16(ar, voff, la + r * KP + piece * 512);
+  }
+  // 2. the wave's weights: G chunks of each of its runs from chunk c0 (past the split's last: zeros)
+  uint32_t bq[NRW][G][FMT == BT_BF16 ? 8 : FMT == BT_BFP8 ? 4 : 2], ew[NRW][G];
+#pragma unroll
+  for (int r = 0; r < NRW; r++) {
+    const bool in = run0 + r < h.nruns;
+    const __amdgpu_buffer_rsrc_t tr =
+        buffer(h.b + ((int64_t)(in ? run0 + r : 0) * h.chunks + c0) * TB, in ? (uint32_t)cnt * TB : 0u);
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      const uint32_t at = (uint32_t)i * TB;
+      if (FMT == BT_BF16) {
+        const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 32 * lane, 0, 0);
+        const auto u = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 32 * lane + 16, 0, 0);
+#pragma unroll
+        for (int w = 0; w < 4; w++) bq[r][i][w] = q[w], bq[r][i][4 + w] = u[w];
+        continue;
+      }
+      if (FMT == BT_BFP8) {
+        const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 64 + 16 * lane, 0, 0);
+#pragma unroll
+        for (int w = 0; w < 4; w++) bq[r][i][w] = q[w];
+      } else {
+        const auto q = __builtin_amdgcn_raw_buffer_load_b64(tr, at + 64 + 8 * lane, 0, 0);
+        bq[r][i][0] = q[0], bq[r][i][1] = q[1];
+      }
+      ew[r][i] = __builtin_amdgcn_raw_buffer_load_b32(tr, at + 4 * col, 0, 0);  // exponent word col of 16
+    }
+  }
+  // A's loads, issued first, have landed (loads complete in order; at most 63 can be counted, and with more B loads
+  // than that, 63 outstanding still leaves every A load done)
+  wait_vm<(2 * NRW * G < 63 ? 2 * NRW * G : 63)>();
+  __syncthreads();
+  // 3. each run's products over the split
+#pragma unroll
+  for (int r = 0; r < NRW; r++) {
+    f32x4 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      if (i >= cnt) continue;
+      bf16x8 bv[2];
+      uint32_t ex[4];
+      if (FMT != BT_BF16)
+#pragma unroll
+        for (int k = 0; k < 4; k++) ex[k] = (uint32_t)__shfl((int)ew[r][i], 4 * g + k, 64);
+      if (FMT == BT_BF16) {
+        const uint4 lo = make_uint4(bq[r][i][0], bq[r][i][1], bq[r][i][2], bq[r][i][3]);
+        const uint4 hi = make_uint4(bq[r][i][4], bq[r][i][5], bq[r][i][6], bq[r][i][7]);
+        bv[0] = *(const bf16x8 *)&lo;
+        bv[1] = *(const bf16x8 *)&hi;
+      } else if (FMT == BT_BFP8) {
+        bv[0] = q8_to_bf16<true>(make_uint2(bq[r][i][0], bq[r][i][1]), make_uint2(ex[0], ex[1]));
+        bv[1] = q8_to_bf16<true>(make_uint2(bq[r][i][2], bq[r][i][3]), make_uint2(ex[2], ex[3]));
+      } else {
+        bv[0] = q4_to_bf16_scaled(bq[r][i][0], make_uint2(ex[0], ex[1]));
+        bv[1] = q4_to_bf16_scaled(bq[r][i][1], make_uint2(ex[2], ex[3]));
+      }
+#pragma unroll
+      for (int t = 0; t < MT; t++) {
+        const uint16_t *at = la + (16 * t + col) * KP + 64 * i + 8 * g;
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)at, bv[0], acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)(at + 32), bv[1], acc[t], 0, 0, 0);
+      }
+    }
+    const int n = (run0 + r) * 16 + col;
+    if (n >= h.n) continue;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int m = 16 * t + 4 * g + i;
+        if (m < h.m) part[((int64_t)sp * 16 * MT + m) * h.n + n] = acc[t][i];
+      }
+  }
+}
+
+// The sum of an output's splits, in split order, through the matmul's epilogue: one output a thread. SWI: the
+// product's columns are gate then up (n = 2f); the output is silu(g) * u for f columns, g and u rounded to bf16 first.
+template <int DT, bool SWI>
+__global__ void __launch_bounds__(256) parts_reduce_kernel(const MatmulArgs args, int splits, int rows, const float *part) {
+  const int nout = SWI ? args.n / 2 : args.n;
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= (int64_t)args.m * nout) return;
+  const int m = (int)(e / nout), n = (int)(e % nout);
+  const int64_t stride = (int64_t)rows * args.n;
+  const float *p = part + (int64_t)m * args.n + n;
+  float v = p[0];
+  for (int s = 1; s < splits; s++) v += p[s * stride];
+  const bt_operand &out = args.out;
+  if constexpr (SWI) {
+    float u = p[nout];
+    for (int s = 1; s < splits; s++) u += p[s * stride + nout];
+    const float gv = bf16_value(bf16_packed(v)), uv = bf16_value(bf16_packed(u));
+    ((uint16_t *)out.ptr)[(int64_t)m * out.sr + n] = (uint16_t)bf16_packed(gv / (1.0f + expf(-gv)) * uv);
+  } else {
+    const uint32_t x = __float_as_uint(DT == BT_BF16 ? round_packed(v) : v);
+    const int64_t at = (int64_t)m * out.sr + (int64_t)n * out.sc;
+    store_value<DT>(out, at, args.n_inst ? run_program<DT, false>(args.prog, 0, m, n, x) : x);
+  }
+}
+
 template <int FMT, int DT, int WM, int WN, int S>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gemm2_kernel(const MatmulArgs args, int mblocks, int nblocks) {
@@ -1728,6 +1859,43 @@ static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bo
   else skinny_kernel<FMT, DT, false><<<blocks, 256, 0, s>>>(args);
 }
 
+// The split-K kernels for 5 to 32 rows of one A against a long K (more than 12 chunks, a multiple of 64): false
+// when the product doesn't fit them or the runtime has no scratch for the partials (then the one-launch kernels run
+// it). Splits of 16 chunks, or of 8 when 16 would leave 1024 blocks or more (measured the faster at those sizes).
+template <int FMT, int MT>
+static void launch_part_m(const MatmulArgs &args, int g, int groups, int splits, float *part, hipStream_t s) {
+  const unsigned blocks = (unsigned)(groups * splits);
+  if (g == 16) skinny_part_kernel<FMT, MT, 1, 16><<<blocks, 256, 0, s>>>(args, groups, part);
+  else skinny_part_kernel<FMT, MT, 1, 8><<<blocks, 256, 0, s>>>(args, groups, part);
+}
+static bool launch_parts(Runtime *r, const MatmulArgs &args, int fmt, bool swi) {
+  const bt_operand &a = args.a;
+  if (args.batch != 1 || args.m < 5 || args.m > 32 || args.k % 64 || args.chunks <= 12 ||
+      a.sc != 1 || a.ptr % 16 || a.sr % 8 || ((int64_t)(args.m - 1) * a.sr + args.k) * 2 >= (1ll << 32) ||
+      (int64_t)args.chunks * Tile<BT_BF16>::bytes >= (1ll << 32))
+    return false;
+  const int mt = args.m > 16 ? 2 : 1;
+  // the splits depend on the shape alone, so every format of B sums in the same order: a block-float product stays
+  // bit for bit the bf16 product of its values. One run a wave (two measured slower: fewer waves in flight).
+  const int64_t groups16 = (args.nruns + 3) / 4;
+  const int g = groups16 * ((args.chunks + 15) / 16) < 1024 ? 16 : 8, nrw = 1;
+  const int groups = (args.nruns + 4 * nrw - 1) / (4 * nrw), splits = (args.chunks + g - 1) / g;
+  float *part = (float *)runtime_scratch(r, (size_t)splits * 16 * mt * args.n * 4);
+  if (!part) return false;
+  if (fmt == BT_BF16 && mt == 2) launch_part_m<BT_BF16, 2>(args, g, groups, splits, part, r->stream);
+  else if (fmt == BT_BF16) launch_part_m<BT_BF16, 1>(args, g, groups, splits, part, r->stream);
+  else if (fmt == BT_BFP8 && mt == 2) launch_part_m<BT_BFP8, 2>(args, g, groups, splits, part, r->stream);
+  else if (fmt == BT_BFP8) launch_part_m<BT_BFP8, 1>(args, g, groups, splits, part, r->stream);
+  else if (mt == 2) launch_part_m<BT_BFP4, 2>(args, g, groups, splits, part, r->stream);
+  else launch_part_m<BT_BFP4, 1>(args, g, groups, splits, part, r->stream);
+  const int64_t outs = (int64_t)args.m * (swi ? args.n / 2 : args.n);
+  const unsigned rb = (unsigned)((outs + 255) / 256);
+  if (swi) parts_reduce_kernel<BT_BF16, true><<<rb, 256, 0, r->stream>>>(args, splits, 16 * mt, part);
+  else if (args.prog.dtype == BT_FP32) parts_reduce_kernel<BT_FP32, false><<<rb, 256, 0, r->stream>>>(args, splits, 16 * mt, part);
+  else parts_reduce_kernel<BT_BF16, false><<<rb, 256, 0, r->stream>>>(args, splits, 16 * mt, part);
+  return true;
+}
+
 // The deepest pipeline (3 or 2 chunks) whose LDS fits the 160 KB of a CU.
 template <int FMT, int DT, int WM, int WN> constexpr int gemm2_stages() {
   return Gemm2<FMT, DT, WM, WN, 3>::LDS <= 160 * 1024 ? 3 : 2;
@@ -1890,6 +2058,10 @@ extern "C" int bt_matmul(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_
       b_fmt = BT_BF16;
     }
   }
+  if (launch_parts(r, args, b_fmt, false)) {
+    BT_LAUNCHED("matmul");
+    return BT_OK;
+  }
   if (b_fmt == BT_BF16) launch_skinny<BT_BF16>(args, r->stream);
   else if (b_fmt == BT_BFP8) launch_skinny<BT_BFP8>(args, r->stream);
   else launch_skinny<BT_BFP4>(args, r->stream);
@@ -2028,6 +2200,10 @@ extern "C" int bt_matmul_swiglu(bt_runtime *rt, const bt_operand *a, int b_fmt, 
   const int mb = (int)((m + 255) / 256), nb = (int)((n / 2 + 127) / 128);
   const int64_t gemm_blocks = ((m + 127) / 128) * ((n + 127) / 128);
   if ((m <= 64 || (m <= 256 && gemm_blocks < 128)) && a->sr % 8 == 0 && a->ptr % 16 == 0 && ((31 * a->sr + 2 * k + 1024) * 2 < (1ll << 32))) {
+    if (launch_parts(r, args, b_fmt, true)) {
+      BT_LAUNCHED("matmul_swiglu");
+      return BT_OK;
+    }
     // few rows: two 16-row tiles by a gate run and its up run a wave, reading B as it is stored (block floats
     // included), so no scratch is needed
     const int64_t units2 = (int64_t)(args.nruns / 2) * ((args.mtiles + 1) / 2);

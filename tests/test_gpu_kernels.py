@@ -232,6 +232,37 @@ def test_short_k_rows_with_a_in_lds(rt, fmt, m, k, n):
   assert np.array_equal(relu, np.maximum(got, 0))
 
 
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bfp4"])
+@pytest.mark.parametrize("m,k,n,out", [(32, 4096, 4096, "fp32"), (20, 1024, 1000, "bf16"), (5, 14336, 512, "fp32"),
+                                       (17, 896, 3000, "bf16"), (32, 4096, 28672, "bf16")])
+def test_split_k_rows(rt, fmt, m, k, n, out):
+  # 5 to 32 rows against K of more than 12 chunks (a multiple of 64): K cut into splits of 8 or 16 chunks, each block
+  # staging its split of A in LDS, then the splits summed in order with the epilogue. Within the reference's bound
+  # of the oracle; a block-float product bit for bit the bf16 product of its values (the splits depend on the shape
+  # alone); the epilogue program (relu, or the residual add into fp32) bit for bit the plain result put through it.
+  # Partial runs (1000, 3000), partial splits (896 = 14 chunks), one tile of rows (5, 16) and two (17 to 32).
+  rng = np.random.default_rng(m * n + k)
+  x, w = rng.normal(0, 1, (m, k)), rng.normal(0, 0.05, (k, n)).astype(np.float32)
+  if fmt == "bf16":
+    cols, wq = bf16_columns(rt, w), B.bf16(w)
+  else:
+    exps, vals = pack(rt, w, fmt)
+    cols, wq = columns(rt, exps, vals, fmt, 1, k, n), bfp_values(w, fmt)
+  plain = matmul(rt, x, cols, fmt, 1, n, out=out)[0]
+  xw = B.bf16(x)
+  assert np.all(np.abs(plain - ops.matmul(xw, wq)) <= ops.matmul_bound(xw, wq))
+  if fmt != "bf16":
+    assert np.array_equal(plain, matmul(rt, x, bf16_columns(rt, wq), "bf16", 1, n, out=out)[0])
+  p = Program(out, epilogue=True)
+  if out == "bf16":
+    assert np.array_equal(matmul(rt, x, cols, fmt, 1, n, out=out, prog=p.build(p.op("relu", p.value())))[0],
+                          np.maximum(plain, 0))
+  else:
+    res = B.bf16(rng.normal(0, 1, (m, n)))
+    prog = p.build(p.op("add", p.value(), p.load(p.input(_lib.operand(up(rt, res.astype(np.float32)), "fp32", m * n, n, 1)))))
+    assert np.array_equal(matmul(rt, x, cols, fmt, 1, n, out=out, prog=prog)[0], (plain + res).astype(np.float32))
+
+
 # (rows, K, N, output): rows > 64 run the tiled GEMM, except up to 256 rows when its 128 x 128 blocks would be fewer
 # than 128 (then the skinny kernel: 96 x 1536 here). With bf16 B (block floats unpacked to it from 512 rows up) and
 # K in 32s, 2048 x 8192 takes 256 x 256 blocks, 2048 x 4096 (fp32 with the residual) and 1000 x 4096 blocks of 128
