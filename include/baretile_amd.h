@@ -170,7 +170,9 @@ int bt_reduce(bt_runtime *rt, const bt_program *prog, int kind, int axis, int64_
  * instructions (fidelity 4, tensor.py:12, 756-757). A is bf16 with element strides. B is in columns layout (any of
  * bf16, bfp8, bfp4) with b' = b when b_batch > 1, else 0. The epilogue program, if any, reads the matmul's value
  * from register 0 (rounded to the program's dtype first) and may read other inputs at the same [b, m, n]. Without
- * one, the value is written to out as bf16 (rounded half up) or fp32. */
+ * one, the value is written to out as bf16 (rounded half up) or fp32. 5 to 32 rows of one A against K over 768 (a
+ * multiple of 64) run split-K: fp32 partial sums in the runtime's scratch, summed in a fixed order (inside a capture
+ * that would have to grow that scratch, a one-launch kernel instead, summing in another order). */
 int bt_matmul(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_t b, int64_t b_batch, int64_t batch, int64_t m,
               int64_t k, int64_t n, const bt_program *epilogue, const bt_operand *out);
 
@@ -202,8 +204,10 @@ int bt_matmul_row(bt_runtime *rt, const bt_row_args *args);
  * SiLU-mul epilogue fused_kernel gives the prefill's gate_up): B holds gate then up side by side (n = 2 f columns,
  * n a multiple of 32) and out[i, j] = bf16(silu(g) * u) for j < f, with g, u the products at columns j and f + j
  * rounded to bf16 as stored, silu(g) = g / (1 + exp(-g)), in fp32. A is bf16 with contiguous rows, k a multiple of
- * 32; out is bf16 with contiguous, 16-byte aligned rows. A block-float B is unpacked to bf16 in the runtime's scratch
- * first (BT_ESTATE inside a capture when that scratch would have to grow). */
+ * 32; out is bf16 with contiguous, 16-byte aligned rows. Where the tiled GEMM runs it (more than 64 rows, unless its
+ * grid would be small), a block-float B is unpacked to bf16 in the runtime's scratch first (BT_ESTATE inside a capture
+ * when that scratch would have to grow); fewer rows read B as stored, 5 to 32 of them against a long K through split-K
+ * partial sums in that scratch (inside a capture that would have to grow it, the one-launch kernel instead). */
 int bt_matmul_swiglu(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_t b, int64_t m, int64_t k, int64_t n,
                      const bt_operand *out);
 /* RMSNorm of a block of token rows (llama.py:88-95): out[r, c] = bf16(x * s * w[c]) with x = bf16(x[r, c]) (half
