@@ -3,7 +3,7 @@
 `python -m baretile_amd.build` or build() from Python. The library is one shared object with a C ABI
 (include/baretile_amd.h), loaded by baretile_amd._lib with ctypes.
 """
-import glob, os, subprocess, sys
+import glob, os, subprocess, sys, tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "libbaretile_amd.so")
@@ -22,15 +22,26 @@ def hipcc():
 
 
 def build(verbose=False):
-  """Compile every source into LIB (a temporary name first, so a failed build leaves the old library)."""
+  """Compile every source into LIB (a temporary name first, so a failed build leaves the old library). The sources
+  compile side by side, one hipcc each, then link into one shared object."""
   tmp = LIB + ".tmp"
-  cmd = [hipcc(), *FLAGS, "-o", tmp, *SOURCES]
-  if verbose: print(" ".join(cmd), flush=True)
-  p = subprocess.run(cmd, capture_output=True, text=True)
-  errors = [l for l in (p.stdout + p.stderr).splitlines() if "packed-fp32-ops" not in l and l.strip()]
-  if p.returncode != 0:
-    raise RuntimeError("hipcc failed:\n" + "\n".join(errors[-60:]))
-  if verbose and errors: print("\n".join(errors[-40:]))
+  cc = hipcc()
+  with tempfile.TemporaryDirectory() as work:
+    objs = [os.path.join(work, os.path.basename(s)[:-4] + ".o") for s in SOURCES]
+    cmds = [[cc, *FLAGS, "-c", "-o", o, s] for s, o in zip(SOURCES, objs)]
+    for c in cmds:
+      if verbose: print(" ".join(c), flush=True)
+    procs = [subprocess.Popen(c, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True) for c in cmds]
+    outs = [p.communicate()[0] for p in procs]
+    link = [cc, *FLAGS, "-o", tmp, *objs]
+    for p, out in zip(procs + [None], outs + [None]):
+      if p is None:
+        p = subprocess.run(link, capture_output=True, text=True)
+        out = p.stdout + p.stderr
+      errors = [l for l in out.splitlines() if "packed-fp32-ops" not in l and l.strip()]
+      if p.returncode != 0:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(errors[-60:]))
+      if verbose and errors: print("\n".join(errors[-40:]))
   os.replace(tmp, LIB)
   return LIB
 

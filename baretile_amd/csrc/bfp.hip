@@ -118,8 +118,18 @@ __device__ __forceinline__ int tile_row(int l, int h, int j) { return 32 * h + 8
 // converts to (bfp4: q * 2^-9 * 2^d). The map is a bijection, so readback recovers e exactly.
 template <int FMT> __device__ __forceinline__ uint32_t exp_bias() { return FMT == BT_BFP8 ? 133u : 120u; }
 
-// A bfp4 value in a columns tile: sign << 3 | magnitude (the low nibble of its fp8 e4m3 subnormal form).
-__device__ __forceinline__ uint32_t nibble_sm(int q) { return q < 0 ? 8u | (uint32_t)(-q) : (uint32_t)q; }
+// Where value j (0..7) of a lane's half sits in its 4 bytes of a bfp4 columns tile, as sign and magnitude: for j < 4
+// byte j's bit 7 and bits 0-2; for j >= 4 bits 4-6 of byte j - 4 and bit 3 of byte (j - 3) % 4. The matmul reads
+// these as fp8 bytes with one mask, and with one rotate and a mask.
+__device__ __forceinline__ uint32_t nibble_bits(int q, int j) {
+  const uint32_t mag = (uint32_t)(q < 0 ? -q : q), sgn = q < 0 ? 1u : 0u;
+  return j < 4 ? mag << (8 * j) | sgn << (8 * j + 7) : mag << (8 * (j - 4) + 4) | sgn << (8 * ((j - 3) & 3) + 3);
+}
+__device__ __forceinline__ int nibble_q(uint32_t w, int j) {  // the inverse: value j's signed q from the 4 bytes
+  const uint32_t mag = (w >> (j < 4 ? 8 * j : 8 * (j - 4) + 4)) & 7u;
+  const uint32_t sgn = (w >> (j < 4 ? 8 * j + 7 : 8 * ((j - 3) & 3) + 3)) & 1u;
+  return sgn ? -(int)mag : (int)mag;
+}
 
 // One block a columns tile, one thread a lane. Reads the plain planes, writes the tile.
 template <int FMT>
@@ -145,7 +155,7 @@ __global__ void __launch_bounds__(64) columns_kernel(const uint8_t *exps, const 
       int64_t k = chunk * 64 + tile_row(l, h, j);
       int q = (k < rows && n < cols16) ? plain_q<FMT>(vals, FMT == BT_BFP8 ? cols16 : cols16 / 2, b * rows + k, n) : 0;
       if (FMT == BT_BFP8) w[(h * 8 + j) / 4] |= ((uint32_t)q & 255u) << (8 * (j % 4));
-      else w[h] |= nibble_sm(q) << (8 * (j % 4) + 4 * (j / 4));  // values j and j + 4 share byte j % 4
+      else w[h] |= nibble_bits(q, j);
     }
   if (FMT == BT_BFP8) *(uint4 *)(out + 64 + 16 * l) = make_uint4(w[0], w[1], w[2], w[3]);
   else *(uint2 *)(out + 64 + 8 * l) = make_uint2(w[0], w[1]);
@@ -197,8 +207,7 @@ __global__ void __launch_bounds__(256) columns_unpack_kernel(const uint8_t *src,
   int q;
   if (FMT == BT_BFP8) q = (int)(int8_t)tp[64 + 16 * l + 8 * h + j];
   else {
-    int nib = (tp[64 + 8 * l + 4 * h + (j & 3)] >> (4 * (j >> 2))) & 15;
-    q = (nib & 8 ? -(nib & 7) : nib) * 16;
+    q = nibble_q(*(const uint32_t *)(tp + 64 + 8 * l + 4 * h), j) * 16;
   }
   dst[t] = (uint16_t)unpacked_bits(q, e);
 }

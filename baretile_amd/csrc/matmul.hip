@@ -94,12 +94,15 @@ __device__ __forceinline__ bf16x8 q8_to_bf16(uint2 q, uint2 d) {
   return *(const bf16x8 *)&v;
 }
 
-// bfp4: a lane's 4 bytes for one half hold values i and i + 4 in byte i (low, high nibble), each sign << 3 | magnitude.
-// As fp8 e4m3 a byte sign << 7 | magnitude is the subnormal magnitude * 2^-9, so spreading the nibbles into bytes and
-// converting gives q * 2^-9 exactly.
+// bfp4: a lane's 4 bytes for one half hold its 8 values as sign and magnitude. Byte i has value i's sign in bit 7 and
+// magnitude in bits 0-2, value i + 4's magnitude in bits 4-6, and in bit 3 the sign of value 4 + (i + 3) % 4. So
+// w & 0x87 in every byte is value i as an fp8 e4m3 byte sign << 7 | magnitude, and the same mask over w rotated right
+// by 4 bits is value i + 4 (its magnitude comes down from bits 4-6, its sign from bit 3 of the next byte up). As fp8
+// e4m3 such a byte is the subnormal magnitude * 2^-9, so converting gives q * 2^-9 exactly: 3 instructions spread 8
+// values into bytes.
 __device__ __forceinline__ void q4_to_fp8(uint32_t w, uint32_t &lo, uint32_t &hi) {
-  lo = (w & 0x07070707u) | ((w << 4) & 0x80808080u);  // values 0..3
-  hi = ((w >> 4) & 0x07070707u) | (w & 0x80808080u);  // values 4..7
+  lo = w & 0x87878787u;                                           // values 0..3
+  hi = __builtin_amdgcn_alignbit(w, w, 4u) & 0x87878787u;         // values 4..7
 }
 
 __device__ __forceinline__ bf16x8 q4_to_bf16(uint32_t w) {  // q * 2^-9 as bf16, in k order
@@ -384,7 +387,27 @@ __global__ void __launch_bounds__(SL ? 512 : 256) gemv_kernel(const MatmulArgs a
     __builtin_amdgcn_wave_barrier();
   }
   if (SL && slices > 1) sum_slices<1>(acc, p, slices, red);
-  if (p.s == 0 && p.valid) store_tile<DT, false, ONE, PROG ? 1 : 0>(args, h, acc[0], b, 0, run, g, col);
+  if (p.s != 0 || !p.valid) return;
+  if constexpr (ONE && !PROG) {
+    // the lean kernels' output is one bf16 or fp32 matrix with contiguous rows whose byte offsets fit 32 bits (the
+    // host checks): one buffer store a row, without store_tile's 64-bit address arithmetic and dtype dispatch, whose
+    // dependent instructions sit on the path between a wave's last product and the end of the launch
+    const bool bf = h.out.dtype == BT_BF16;
+    const int n = run * 16 + col;
+    const __amdgpu_buffer_rsrc_t orr =
+        buffer((const void *)(uintptr_t)h.out.ptr, (uint32_t)(((int64_t)(h.m - 1) * h.out.sr + h.n) * (bf ? 2 : 4)));
+#pragma unroll
+    for (int i = 0; i < (ROWS == 1 ? 1 : 4); i++) {
+      const int mm = 4 * g + i;
+      if (mm >= rows || n >= h.n) continue;
+      const uint32_t at = (uint32_t)(mm * (int)h.out.sr + n);
+      if (bf) __builtin_amdgcn_raw_buffer_store_b16((uint16_t)bf16_packed(acc[0][i]), orr, at * 2, 0, 0);
+      else __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(DT == BT_BF16 ? round_packed(acc[0][i]) : acc[0][i]),
+                                                 orr, at * 4, 0, 0);
+    }
+  } else {
+    store_tile<DT, false, ONE, PROG ? 1 : 0>(args, h, acc[0], b, 0, run, g, col);
+  }
 }
 
 // B-side scaling with row-major, 16-byte aligned A: each lane turns its 16 B values into bf16 q * 2^d with
@@ -1786,7 +1809,10 @@ static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bo
     const int sl = choose_slices(units, args.chunks);
     // a plain product of one matrix, K unsliced: the lean kernels, group size fitted to K; anything else (a batch,
     // an epilogue program, slices): one kernel with all of them, groups of 8
-    const bool lean = args.batch == 1 && !args.n_inst && sl == 1;
+    // (and a plain output: bf16 or fp32, contiguous rows, every byte offset within 32 bits)
+    const bool plain_out = (args.out.dtype == BT_BF16 || args.out.dtype == BT_FP32) && args.out.sc == 1 &&
+                           args.out.sr >= 0 && ((int64_t)(args.m - 1) * args.out.sr + args.n) * 4 < (1ll << 31);
+    const bool lean = args.batch == 1 && !args.n_inst && sl == 1 && plain_out;
     if (args.m == 1) {
       constexpr int SB = 64 * 2;  // slot bytes a chunk
       if (!lean && sl > 1) {

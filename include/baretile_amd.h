@@ -84,8 +84,9 @@ int bt_stream(bt_runtime *rt, void **stream);
  * instruction reads B: lane l (0..63) holds rows 32h + 8(l / 16) + j, j = 0..7, of column l % 16, for h = 0, 1.
  * Exponent byte p = 16g + 8h + j belongs to row 32h + 8g + j and holds (e - 133) mod 256 (bfp8) or (e - 120) mod 256
  * (bfp4). bfp8 tiles are 64 + 1024 bytes: lane l's 16 bytes at 64 + 16l, byte 8h + j the signed q of value j.
- * bfp4 tiles are 64 + 512: lane l's 8 bytes at 64 + 8l, byte 4h + i holding values i (low nibble) and i + 4 (high),
- * each as sign << 3 | magnitude. bf16 tiles are 2048 bytes (32 bytes at 32l, no exponents). Rows past K and columns
+ * bfp4 tiles are 64 + 512: lane l's 8 bytes at 64 + 8l, 4 bytes a half h holding its values j = 0..7 as sign and
+ * magnitude: for j < 4 byte j's bit 7 and bits 0-2, for j >= 4 bits 4-6 of byte j - 4 and bit 3 of byte
+ * (j - 3) % 4. bf16 tiles are 2048 bytes (32 bytes at 32l, no exponents). Rows past K and columns
  * past N are zero. A matmul reads exponents as signed bytes, so it takes block floats whose run exponents e lie in
  * 5..255 (bfp8) or 0..247 (bfp4); readback is exact for any. */
 
