@@ -1348,7 +1348,7 @@ constexpr int GEMM_PLAIN = 0, GEMM_RES = 1, GEMM_SWIGLU = 2;
 // leave CUs idle.
 template <int DT, int S, int MODE = GEMM_PLAIN, int BM = 256>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand res) {
+gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand res, int nb_off = 0) {
   constexpr bool RES = MODE == GEMM_RES;
   constexpr int BN = 256, A_BYTES = BM * 64, STAGE = A_BYTES + 16384, WM = BM / 32, WN = 4, WR = BM / 2;
   constexpr int AL = BM / 128;  // A loads a wave issues a step
@@ -1366,7 +1366,7 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
   pid %= per;
   constexpr int GROUP = 8;  // blocks of a column of 8 block rows run together, sharing B's tiles in L2
   const int width = GROUP * nblocks, first = pid / width * GROUP, gsz = min(mblocks - first, GROUP);
-  const int bm = first + pid % width % gsz, bn = pid % width / gsz;
+  const int bm = first + pid % width % gsz, bn = nb_off + pid % width / gsz;  // nb_off: the launch's first block column
   const int m0 = bm * BM, n0 = bn * BN;
 
   const uint16_t *abase = (const uint16_t *)h.a.ptr + operand_matrix(h.a, b) * h.a.sb;
@@ -1614,6 +1614,15 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(const RowArgs args, const
     row_pieces(buffer_words(h.a, (uint32_t)K * 2), p0, raw0, wib, lane);
     row_pieces(buffer_words(h.a + (int64_t)K * 2, (uint32_t)K * 2), p1, raw1, wib, lane);
   }
+  // the residual at the lane's column (row 0: lanes 0..15 of the run's first slice), requested with the inputs so it
+  // has landed by step 3's wait; read at the end, it would add a trip to memory after the last product
+  float resv = 0.0f;
+  if (!ROPE && h.res) {
+    const int n = run * 16 + col;
+    const bool mine_col = valid && sl == 0 && g == 0 && n < h.n;
+    resv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(buffer(h.res, (uint32_t)h.n * 4),
+                                                                mine_col ? (uint32_t)n * 4 : 0xFFFFFFF0u, 0, 0));
+  }
   // 2. the first group's weights (every wave issues 2 G loads; a wave past the last run reads nothing)
   const uint8_t *tiles = h.b + ((int64_t)(valid ? run : 0) * chunks + c_begin) * TB;
   const __amdgpu_buffer_rsrc_t tr = buffer(tiles, valid ? (uint32_t)mine * TB : 0u);
@@ -1739,7 +1748,7 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(const RowArgs args, const
   const int n = run * 16 + col;
   if (g != 0 || n >= h.n) return;
   float v = acc[0];
-  if (h.res) v += h.res[n];
+  if (h.res) v += resv;
   if (h.out_dtype == BT_BF16) ((uint16_t *)h.out)[n] = (uint16_t)bf16_packed(v);
   else ((float *)h.out)[n] = v;
 }
@@ -2255,7 +2264,24 @@ extern "C" int bt_matmul_swiglu(bt_runtime *rt, const bt_operand *a, int b_fmt, 
     BT_LAUNCHED("matmul_swiglu");
     args.b = (const uint8_t *)bt16;
   }
-  gemm3_kernel<BT_BF16, 4, GEMM_SWIGLU><<<(unsigned)((int64_t)mb * nb), 512, 0, r->stream>>>(args, mb, nb, bt_operand{});
+  // One block a CU (the stages fill its LDS), so the blocks run in rounds of 256. When the last round would be at most
+  // half full, the trailing block columns go to a second launch of 128-row blocks: twice the blocks at half the work
+  // each, which fill one round that takes half the time (gate_up of 2048 Llama-3-8B tokens: 896 blocks, 3.5 rounds,
+  // become 768 + 256 blocks of 128 rows, 3 rounds and a half-length one).
+  int tail = 0;
+  if (mb * nb > 256 && (mb * nb) % 256 != 0 && (mb * nb) % 256 <= 128) {
+    const int mb128 = (int)((m + 127) / 128);
+    for (int t = 1; t < nb && mb128 * t <= 256; t++)
+      if ((mb * (nb - t)) % 256 == 0) { tail = t; break; }
+  }
+  gemm3_kernel<BT_BF16, 4, GEMM_SWIGLU><<<(unsigned)((int64_t)mb * (nb - tail)), 512, 0, r->stream>>>(args, mb, nb - tail,
+                                                                                                  bt_operand{}, 0);
   BT_LAUNCHED("matmul_swiglu");
+  if (tail) {
+    const int mb128 = (int)((m + 127) / 128);
+    gemm3_kernel<BT_BF16, 4, GEMM_SWIGLU, 128><<<(unsigned)((int64_t)mb128 * tail), 512, 0, r->stream>>>(
+        args, mb128, tail, bt_operand{}, nb - tail);
+    BT_LAUNCHED("matmul_swiglu");
+  }
   return BT_OK;
 }
