@@ -11,7 +11,7 @@
 // chunks are requested before the first is multiplied.
 //   A-side scaling (up to 4 rows of A): per chunk, each lane scales one k of x by its run's 2^(e - bias) into LDS, so a
 //     bfp8 weight needs only int -> bf16 (1.5 instructions a value) and a bfp4 weight goes through fp8 subnormals
-//     with v_cvt_scalef32_pk_bf16_fp8 (1.25 a value).
+//     with v_cvt_scalef32_pk_bf16_fp8 (7 instructions for 8 values: a mask, a rotate and a mask, 4 conversions).
 //   B-side scaling (more rows): each weight gets its power of two with v_ldexp_f32, reading the biased exponent byte
 //     straight from the tile.
 #include "program.h"
