@@ -500,9 +500,29 @@ __global__ void __launch_bounds__(256) skinny_lds_kernel(const MatmulArgs args) 
         acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)(ar + 32), bv[1], acc[t], 0, 0, 0);
       }
     }
-    if (run0 + r < h.nruns)
+    if (run0 + r >= h.nruns) continue;
+    if constexpr (PROG) {
 #pragma unroll
-      for (int t = 0; t < MT; t++) store_tile<DT, false, true, PROG ? 1 : 0>(args, h, acc[t], 0, t, run0 + r, g, col);
+      for (int t = 0; t < MT; t++) store_tile<DT, false, true, 1>(args, h, acc[t], 0, t, run0 + r, g, col);
+    } else {
+      // without a program the output is plain (bf16 or fp32, contiguous rows, byte offsets within 32 bits: the host
+      // checks): a buffer store a value, as the lean GEMV stores
+      const bool bf = h.out.dtype == BT_BF16;
+      const int n = (run0 + r) * 16 + col;
+      const __amdgpu_buffer_rsrc_t orr =
+          buffer((const void *)(uintptr_t)h.out.ptr, (uint32_t)(((int64_t)(h.m - 1) * h.out.sr + h.n) * (bf ? 2 : 4)));
+#pragma unroll
+      for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int mm = 16 * t + 4 * g + i;
+          if (mm >= h.m || n >= h.n) continue;
+          const uint32_t at = (uint32_t)(mm * (int)h.out.sr + n);
+          if (bf) __builtin_amdgcn_raw_buffer_store_b16((uint16_t)bf16_packed(acc[t][i]), orr, at * 2, 0, 0);
+          else __builtin_amdgcn_raw_buffer_store_b32(
+              __float_as_uint(DT == BT_BF16 ? round_packed(acc[t][i]) : acc[t][i]), orr, at * 4, 0, 0);
+        }
+    }
   }
 }
 
@@ -1790,6 +1810,13 @@ static void launch_sliced(Kernel kernel, const MatmulArgs &args, int64_t units, 
   kernel<<<blocks, wpb * 64, lds, s>>>(args, slices);
 }
 
+// Whether the output is one bf16 or fp32 matrix with contiguous rows whose byte offsets fit 32 bits: what the kernels
+// that store without a program (the lean GEMV, skinny_lds_kernel) assume.
+static bool plain_out(const MatmulArgs &args) {
+  return (args.out.dtype == BT_BF16 || args.out.dtype == BT_FP32) && args.out.sc == 1 && args.out.sr >= 0 &&
+         ((int64_t)(args.m - 1) * args.out.sr + args.n) * 4 < (1ll << 31);
+}
+
 template <int FMT, int DT, int MT, int NRW, int G>
 static void launch_lds_g(const MatmulArgs &args, unsigned blocks, size_t lds, hipStream_t s) {
   if (args.n_inst) skinny_lds_kernel<FMT, DT, MT, NRW, G, true><<<blocks, 256, lds, s>>>(args);
@@ -1818,10 +1845,8 @@ static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bo
     const int sl = choose_slices(units, args.chunks);
     // a plain product of one matrix, K unsliced: the lean kernels, group size fitted to K; anything else (a batch,
     // an epilogue program, slices): one kernel with all of them, groups of 8
-    // (and a plain output: bf16 or fp32, contiguous rows, every byte offset within 32 bits)
-    const bool plain_out = (args.out.dtype == BT_BF16 || args.out.dtype == BT_FP32) && args.out.sc == 1 &&
-                           args.out.sr >= 0 && ((int64_t)(args.m - 1) * args.out.sr + args.n) * 4 < (1ll << 31);
-    const bool lean = args.batch == 1 && !args.n_inst && sl == 1 && plain_out;
+    // (and a plain output)
+    const bool lean = args.batch == 1 && !args.n_inst && sl == 1 && plain_out(args);
     if (args.m == 1) {
       constexpr int SB = 64 * 2;  // slot bytes a chunk
       if (!lean && sl > 1) {
@@ -1846,7 +1871,7 @@ static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bo
       else launch_sliced(gemv_kernel<FMT, DT, 4, 12, true, false, false>, args, units, 1, 12 * SB, 0, s);
     }
   } else if (FMT != BT_BF16 && vec && fits && args.batch == 1 && args.m <= 32 && args.chunks <= 12 &&
-             ((int64_t)(args.m - 1) * args.a.sr + args.k) * 2 < (1ll << 31)) {
+             ((int64_t)(args.m - 1) * args.a.sr + args.k) * 2 < (1ll << 31) && (args.n_inst || plain_out(args))) {
     // A staged whole in LDS once a block, a run a wave (more runs a wave measured slower: fewer waves in flight)
     const unsigned blocks = (unsigned)((args.nruns + 3) / 4);
     const size_t lds = (size_t)(args.m > 16 ? 32 : 16) * (args.chunks * 64 + 8) * 2;
