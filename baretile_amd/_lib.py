@@ -74,7 +74,7 @@ SIGNATURES = {
   "bt_version": [], "bt_device_count": [POINTER(c_int)], "bt_open": [c_int, POINTER(c_void_p)], "bt_close": [RT],
   "bt_alloc": [RT, U64, POINTER(c_uint64)], "bt_free": [RT, U64, c_int], "bt_upload": [RT, U64, c_void_p, U64],
   "bt_download": [RT, c_void_p, U64, U64], "bt_copy": [RT, U64, U64, U64], "bt_fill32": [RT, U64, c_uint32, U64],
-  "bt_wait": [RT, c_double], "bt_event_create": [RT, POINTER(c_void_p)], "bt_event_record": [RT, c_void_p],
+  "bt_wait": [RT, c_double], "bt_sleep": [RT, c_double], "bt_event_create": [RT, POINTER(c_void_p)], "bt_event_record": [RT, c_void_p],
   "bt_event_elapsed": [c_void_p, c_void_p, POINTER(c_float)], "bt_event_destroy": [c_void_p],
   "bt_graph_begin": [RT], "bt_graph_end": [RT, POINTER(c_void_p)], "bt_graph_launch": [RT, c_void_p],
   "bt_graph_destroy": [c_void_p], "bt_stream": [RT, POINTER(c_void_p)], "bt_stream_read": [RT, U64, U64, U64],

@@ -63,6 +63,18 @@ __global__ void __launch_bounds__(256) stream_read_kernel(const uint8_t *p, uint
   if (acc == 0x9E3779B9u && out) out[0] = acc;
 }
 
+// One wave waits until `ticks` of the device's constant-rate wall clock have passed since it started, sleeping between
+// reads, then ends: a launch that stays busy for a set time and always finishes by itself.
+__global__ void sleep_kernel(uint64_t ticks, uint32_t *out) {
+  const uint64_t start = wall_clock64();
+  uint64_t now = start;
+  while (now - start < ticks) {
+    __builtin_amdgcn_s_sleep(127);
+    now = wall_clock64();
+  }
+  if (out && now == start) out[0] = 1;  // never taken once ticks > 0; keeps the loop observable
+}
+
 }  // namespace bt
 
 using namespace bt;
@@ -70,6 +82,20 @@ using namespace bt;
 extern "C" {
 
 const char *bt_last_error(void) { return last_error.c_str(); }
+
+int bt_sleep(bt_runtime *rt, double seconds) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (!(seconds >= 0 && seconds <= 10)) return fail(BT_EINVAL, "sleep takes 0 to 10 seconds, not %g", seconds);
+  int khz = 0;
+  BT_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, r->device));
+  if (khz <= 0) return fail(BT_ESTATE, "the device reports no wall clock rate");
+  const uint64_t ticks = (uint64_t)(seconds * 1000.0 * khz);
+  if (!ticks) return BT_OK;
+  sleep_kernel<<<1, 64, 0, r->stream>>>(ticks, nullptr);
+  BT_LAUNCHED("sleep");
+  return BT_OK;
+}
 
 int bt_stream_read(bt_runtime *rt, uint64_t src, uint64_t bytes, uint64_t scratch_word) {
   Runtime *r;

@@ -16,16 +16,15 @@ are outside this backend's scope.
 import json
 import math
 import os
-import re
-import struct
 from types import SimpleNamespace
 import numpy as np
 from baretile_amd.tensor import Tensor, jit
 
 
 def model(**kw):
-  """A config: dim, heads, kv, layers, eps, theta, vocab, ffn, and optionally head_dim and precision."""
-  base = dict(head_dim=None, vocab=None, ffn=None, precision=None)
+  """A config: dim, heads, kv, layers, eps, theta, vocab, ffn, and optionally head_dim, precision and rope (RoPE
+  scaling parameters, or None)."""
+  base = dict(head_dim=None, vocab=None, ffn=None, precision=None, rope=None)
   return SimpleNamespace(**(base | kw))
 
 
@@ -72,9 +71,21 @@ def _bf16(a):  # float32 rounded to bf16 (nearest even) and back
 
 
 def frequencies(c):
-  """RoPE's inverse frequencies, in fp32 as Hugging Face computes them (llama.py:187-192)."""
+  """RoPE's inverse frequencies in fp32, as Hugging Face computes them (llama.py:187-200). With Llama 3's scaling
+  (c.rope["rope_type"] == "llama3"), frequencies whose wavelength passes original / low_freq_factor are divided by the
+  factor, those under original / high_freq_factor are kept, and the ones between blend the two, linearly in
+  original / wavelength."""
   hd = head(c)
-  return (1 / c.theta ** (np.arange(0, hd, 2, dtype=np.float32) / hd)).astype(np.float32)
+  base = (1 / c.theta ** (np.arange(0, hd, 2, dtype=np.float32) / hd)).astype(np.float32)
+  r = getattr(c, "rope", None) or {}
+  if r.get("rope_type") != "llama3": return base
+  span = r["original_max_position_embeddings"]
+  lo, hi, factor = r["low_freq_factor"], r["high_freq_factor"], r["factor"]
+  wave = np.float32(2 * math.pi) / base
+  slowed = base / np.float32(factor)
+  mix = (np.float32(span) / wave - np.float32(lo)) / np.float32(hi - lo)
+  blended = (1 - mix) * slowed + mix * base
+  return np.select([wave > span / lo, wave < span / hi], [slowed, base], blended).astype(np.float32)
 
 
 def rotary(c, n):
@@ -93,10 +104,14 @@ def rotary(c, n):
 
 
 class Weight:
-  """A checkpoint matrix read on demand, so the host never holds the whole model (llama.py:229-233): bits() returns
-  its bf16 bits laid out for x @ w, values() those values as float32."""
-  def __init__(self, bits): self.bits = bits
-  def values(self): return (self.bits().astype(np.uint32) << 16).view(np.float32)
+  """One matrix of a checkpoint, read only when asked for, so the host never holds a whole model (llama.py:229-233).
+  Made from a function of no arguments that returns the matrix's bf16 bits laid out for x @ w; bits() calls it and
+  values() gives the same as float32."""
+  __slots__ = ("read",)
+
+  def __init__(self, read): self.read = read
+  def bits(self): return self.read()
+  def values(self): return (np.asarray(self.bits(), np.uint32) << 16).view(np.float32)
 
 
 def fuse(w, c):
@@ -118,39 +133,50 @@ def fuse(w, c):
 TYPES = ("llama",)
 
 
-def read_safetensors(path):
-  """A safetensors file's header (each tensor's dtype, shape and byte range) and its data, memory-mapped."""
-  with open(path, "rb") as f:
-    size = struct.unpack("<Q", f.read(8))[0]
-    header = json.loads(f.read(size))
-  return header, np.memmap(path, np.uint8, "r", offset=8 + size)
+class Shards:
+  """The tensors of a safetensors checkpoint in one file or several: each file starts with an 8-byte little-endian
+  header length and a JSON header giving every tensor's dtype, shape and byte range after the header. Nothing but the
+  headers is read until a tensor is asked for, and then only its own bytes."""
+  def __init__(self, paths):
+    self.entries = {}
+    for path in paths:
+      with open(path, "rb") as f:
+        size = int.from_bytes(f.read(8), "little")
+        header = json.loads(f.read(size))
+      for name, entry in header.items():
+        if name != "__metadata__": self.entries[name] = (path, 8 + size, entry)
 
-
-def tensor_bits(data, t, transpose=False):
-  """A checkpoint tensor as bf16 bits (gpt2.py:42-48): BF16 as stored, F32 rounded to nearest even; a vector
-  becomes a one-row matrix."""
-  raw = np.asarray(data[t["data_offsets"][0]:t["data_offsets"][1]])
-  if t["dtype"] == "BF16": bits = raw.view(np.uint16)
-  elif t["dtype"] == "F32": bits = (_bf16(raw.view(np.float32)).view(np.uint32) >> 16).astype(np.uint16)
-  else: raise ValueError(f"a checkpoint tensor must be F32 or BF16, not {t['dtype']}")
-  bits = bits.reshape(t["shape"] if len(t["shape"]) >= 2 else (1, -1))
-  return np.ascontiguousarray(bits.T) if transpose else bits
+  def bf16(self, name, transposed=False):
+    """Tensor `name` as bf16 bits: BF16 as stored, F32 rounded to nearest even. A vector comes back as one row, and a
+    matrix transposed when asked (a linear layer's weight, stored (out, in), used as x @ w)."""
+    path, start, e = self.entries[name]
+    kind = {"BF16": np.uint16, "F32": np.float32}.get(e["dtype"])
+    if kind is None: raise ValueError(f"{name} is {e['dtype']}: checkpoint tensors are read from BF16 or F32")
+    lo, hi = e["data_offsets"]
+    a = np.fromfile(path, kind, (hi - lo) // np.dtype(kind).itemsize, offset=start + lo)
+    if kind is np.float32: a = (_bf16(a).view(np.uint32) >> 16).astype(np.uint16)
+    a = a.reshape(e["shape"] if len(e["shape"]) > 1 else (1, -1))
+    return np.ascontiguousarray(a.T) if transposed else a
 
 
 def config(folder, places=4096):
-  """A config from a Hugging Face config.json (llama.py:400-427), Llama family with default RoPE. places, capped
-  at the model's maximum, sizes the RoPE tables. ValueError for another model type or RoPE scaling."""
+  """A config from a Hugging Face config.json (llama.py:400-427), Llama family. places, capped at the model's maximum,
+  sizes the RoPE tables. RoPE scaling may be Llama 3's (rope_type "llama3", kept in c.rope); ValueError for another
+  model type or another scaling."""
   with open(os.path.join(folder, "config.json")) as f: j = json.load(f)
   j = j.get("text_config", j)
   if j.get("model_type") not in TYPES:
     raise ValueError(f"{folder}: model type {j.get('model_type')!r} isn't supported; this backend runs {', '.join(TYPES)}")
-  rope = j.get("rope_parameters") or (j.get("rope_scaling") or {}) | {"rope_theta": j.get("rope_theta", 10000.0)}
-  if (rope.get("rope_type") or rope.get("type") or "default") != "default":
-    raise ValueError(f"RoPE scaling {rope} isn't supported")
+  rope = dict(j.get("rope_parameters") or j.get("rope_scaling") or {})  # transformers 5 names it rope_parameters
+  theta = float(rope.pop("rope_theta", j.get("rope_theta", 10000.0)))
+  kind = rope.pop("rope_type", None) or rope.get("type") or "default"  # older configs name it type
+  rope.pop("type", None)
+  if kind not in ("default", "llama3"): raise ValueError(f"RoPE scaling {kind!r} ({rope}) isn't supported")
   return model(dim=j["hidden_size"], heads=j["num_attention_heads"], kv=j.get("num_key_value_heads", j["num_attention_heads"]),
-               layers=j["num_hidden_layers"], eps=j["rms_norm_eps"], theta=float(rope["rope_theta"]),
-               vocab=j["vocab_size"], ffn=j.get("intermediate_size"), head_dim=j.get("head_dim"),
-               places=min(j.get("max_position_embeddings", places), places), tied=j.get("tie_word_embeddings", False))
+               layers=j["num_hidden_layers"], eps=j["rms_norm_eps"], theta=theta, vocab=j["vocab_size"],
+               ffn=j.get("intermediate_size"), head_dim=j.get("head_dim"),
+               places=min(j.get("max_position_embeddings", places), places), tied=j.get("tie_word_embeddings", False),
+               rope={"rope_type": kind, **rope} if kind == "llama3" else None)
 
 
 def load(folder, places=4096):
@@ -164,19 +190,16 @@ def load(folder, places=4096):
     with open(index) as f: files = sorted(set(json.load(f)["weight_map"].values()))
   else:
     files = ["model.safetensors"]
+  shards = Shards([os.path.join(folder, f) for f in files])
   out = {}
-  for file in files:
-    header, data = read_safetensors(os.path.join(folder, file))
-    for full, t in header.items():
-      if full == "__metadata__": continue
-      name = full.removeprefix("model.").removesuffix(".weight")
-      for part in ("self_attn.", "mlp."): name = name.replace(part, "")
-      if name.startswith("layers.") and int(name.split(".")[1]) >= c.layers: continue
-      turn = (name.endswith("_proj") or name == "lm_head") and len(t["shape"]) == 2
-      out[name] = Weight(lambda data=data, t=t, turn=turn: tensor_bits(data, t, turn))
+  for full, (_, _, e) in shards.entries.items():
+    name = full.removeprefix("model.").removesuffix(".weight").replace("self_attn.", "").replace("mlp.", "")
+    if name.startswith("layers.") and int(name.split(".")[1]) >= c.layers: continue
+    linear = (name.endswith("_proj") or name == "lm_head") and len(e["shape"]) == 2
+    out[name] = Weight(lambda full=full, linear=linear: shards.bf16(full, linear))
   out["embed"] = out.pop("embed_tokens")
-  head_w = out.pop("lm_head", None)
-  out["embed.T"] = head_w or Weight(lambda e=out["embed"]: np.ascontiguousarray(e.bits().T))
+  tied = Weight(lambda e=out["embed"]: np.ascontiguousarray(e.bits().T))
+  out["embed.T"] = out.pop("lm_head", None) or tied
   return c, fuse(out, c)
 
 

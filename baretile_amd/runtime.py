@@ -38,7 +38,7 @@ class Runtime:
     chip.runtime = weakref.ref(self)
     self.launches, self.numbers, self.log, self.written, self.recording = 0, {}, None, None, None
     self.timing = timing  # with timing, every launch is bracketed by events, for profile()
-    self.times = []  # (launch, name, start event, end event) while timing
+    self.times = []  # (launch, name, start event, end event, bytes read or None) while timing
     self.grid, self.readers = None, None  # kernel-cache key parts of the reference; unused here
     self.cores = [None] * 256  # one "worker" per compute unit, for code that sizes work by len(rt.cores)
     self.deferred = []  # (address, captured) frees asked for during a capture
@@ -96,8 +96,9 @@ class Runtime:
     _lib.call("fill32", self.handle, int(addr), value & 0xFFFFFFFF, int(words))
 
   # ---- launches
-  def launched(self, name):
-    """Counts a launch, and with timing brackets it by events. Returns a callable that ends the bracket."""
+  def launched(self, name, reads=None):
+    """Counts a launch, and with timing brackets it by events. Returns a callable that ends the bracket. reads is the
+    bytes the launch reads from device memory, as its operands' sizes give them, for profile()."""
     self.launches += 1
     if self.log is not None: self.log.append(name)
     if not self.timing or self.recording is not None: return lambda: None
@@ -108,14 +109,21 @@ class Runtime:
     n = self.launches
     def done():
       _lib.call("event_record", self.handle, end)
-      self.times.append((n, name, start, end))
+      self.times.append((n, name, start, end, reads))
     return done
 
-  def run(self, name, fn, *args):
-    """Queue bt_<fn>(handle, *args), counted as launch `name`."""
+  def run(self, name, fn, *args, reads=None):
+    """Queue bt_<fn>(handle, *args), counted as launch `name` that reads `reads` bytes (None: not counted)."""
     self.check()
-    done = self.launched(name)
+    done = self.launched(name, reads)
     _lib.call(fn, self.handle, *args)
+    done()
+
+  def sleep(self, seconds):
+    """Queue a launch that keeps the device busy for `seconds` (at most 10) and then ends by itself."""
+    self.check()
+    done = self.launched("sleep", 0)
+    _lib.call("sleep", self.handle, float(seconds))
     done()
 
   def wait(self, timeout=60, launch=None):
@@ -127,23 +135,27 @@ class Runtime:
     _lib.call("wait", self.handle, float(timeout))
 
   def profile(self, since=0):
-    """Wait, then [(name, launches, microseconds, None)] for the launches after `since` that were timed, grouped by
-    name with the longest first (runtime.py:773-786 reports cycles and NoC bytes; here it is event time)."""
+    """Wait, then [(name, launches, microseconds, bytes)] for the timed launches after `since`, grouped by name with
+    the longest first (runtime.py:773-786, which reports cycles and the NoC bytes read). Here the time is HIP events
+    around each launch, and bytes are what the launches read from device memory by their operands' sizes: algorithmic
+    bytes, not a hardware counter. bytes is None for a name none of whose launches counted them."""
     self.wait()
-    totals = collections.defaultdict(lambda: [0, 0.0])
-    for n, name, start, end in self.times:
+    totals = collections.defaultdict(lambda: [0, 0.0, None])
+    for n, name, start, end, reads in self.times:
       if n <= since: continue
       ms = c_float()
       _lib.call("event_elapsed", start, end, byref(ms))
-      totals[name][0] += 1
-      totals[name][1] += ms.value * 1000
-    return sorted(((name, n, us, None) for name, (n, us) in totals.items()), key=lambda r: -r[2])
+      t = totals[name]
+      t[0] += 1
+      t[1] += ms.value * 1000
+      if reads is not None: t[2] = (t[2] or 0) + int(reads)
+    return sorted(((name, n, us, nbytes) for name, (n, us, nbytes) in totals.items()), key=lambda r: -r[2])
 
   def close(self):
     """Finish queued work and release the stream. The runtime's tensors then raise RuntimeError."""
     if self.closed: return
     self.closed = True
-    for _, _, start, end in self.times:
+    for _, _, start, end, _ in self.times:
       _lib.call("event_destroy", start)
       _lib.call("event_destroy", end)
     self.times = []

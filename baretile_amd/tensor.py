@@ -59,11 +59,14 @@ def _bf16_bits(values):
 
 class Storage:
   """Device memory that tensors share, freed when the last tensor using it goes. Memory allocated while a jit
-  recording captures belongs to the recording too, which keeps it for as long as its graph can replay."""
+  recording captures belongs to the recording too, which keeps it for as long as its graph can replay.
+
+  columns caches, per block-float view read as a matmul's B, the tiles columns() made of it; any write into the
+  storage (realize into, assign, put) drops them."""
   __slots__ = ("rt", "addr", "nbytes", "columns", "captured", "vals", "__weakref__")
 
   def __init__(self, rt, nbytes):
-    self.rt, self.nbytes, self.columns, self.addr, self.vals = rt, nbytes, None, None, 0
+    self.rt, self.nbytes, self.columns, self.addr, self.vals = rt, nbytes, {}, None, 0
     self.captured = rt.recording is not None
     self.addr = rt.dram_alloc(max(256, nbytes))
     if self.captured: rt.recording.storages.append(self)
@@ -73,6 +76,25 @@ class Storage:
       if self.addr is not None: self.rt.dram_free(self.addr, self.captured)
     except Exception:
       pass
+
+
+def _written(storage):
+  """Notes a write into storage that its readers' caches must see: cached columns tiles go, and a jit recording learns
+  which of its inputs the function writes."""
+  storage.columns.clear()
+  if storage.rt.written is not None: storage.rt.written.add(id(storage))
+
+
+def _bytes(*ts):
+  """The bytes a kernel reads for these realized tensors' values, as stored: a block float counts its exponents, a
+  tensor by columns its tiles. What Runtime.profile reports."""
+  n = 0
+  for t in ts:
+    if t is None: continue
+    if t.layout == "columns": n += t.batch * _tiles_bytes(t.rows, t.cols, t.dtype)
+    elif t.dtype in BFP: n += t.batch * sum(_planes(t.rows, t.cols, t.dtype))
+    else: n += t.batch * t.rows * t.cols * ITEMSIZE[t.dtype]
+  return n
 
 
 def _planes(rows, cols, dtype):
@@ -239,10 +261,12 @@ class Tensor:
       out = Tensor(self.rt, t.rows, t.cols, batch=t.batch, dtype="bf16")
       if t.layout == "columns":
         fmt = _lib.DTYPES[t.dtype]
-        self.rt.run("readback", "columns_unpack", fmt, t.storage.addr, t.batch, t.rows, t.cols, out.storage.addr)
+        self.rt.run("readback", "columns_unpack", fmt, t.storage.addr, t.batch, t.rows, t.cols, out.storage.addr,
+                    reads=_bytes(t))
       else:
         e, v = t._bfp_whole()._bfp_planes()
-        self.rt.run("readback", "bfp_unpack", _lib.DTYPES[t.dtype], e, v, t.batch, t.rows, t.cols, out.storage.addr)
+        self.rt.run("readback", "bfp_unpack", _lib.DTYPES[t.dtype], e, v, t.batch, t.rows, t.cols, out.storage.addr,
+                    reads=_bytes(t))
       t = out
     if not t._contiguous(): t = t._copy()
     return bytes(self.rt.download(t.addr, t.batch * t.rows * t.cols * t.itemsize))
@@ -498,10 +522,11 @@ class Tensor:
       out.lead = x.lead
       if x.layout == "columns":
         self.rt.run("storage", "columns_unpack", _lib.DTYPES[x.dtype], x.storage.addr, x.batch, x.rows, x.cols,
-                    out.storage.addr)
+                    out.storage.addr, reads=_bytes(x))
       else:
         e, v = x._bfp_whole()._bfp_planes()
-        self.rt.run("storage", "bfp_unpack", _lib.DTYPES[x.dtype], e, v, x.batch, x.rows, x.cols, out.storage.addr)
+        self.rt.run("storage", "bfp_unpack", _lib.DTYPES[x.dtype], e, v, x.batch, x.rows, x.cols, out.storage.addr,
+                    reads=_bytes(x))
       return out.cast(dtype)
     if dtype in BFP:
       x = self if self.dtype in ("bf16", "fp32") else self.float()
@@ -511,7 +536,7 @@ class Tensor:
       out.lead = x.lead
       e, v = out._bfp_planes()
       self.rt.run("cast", "bfp_pack", _lib.DTYPES[dtype], x.addr, _lib.DTYPES[x.dtype], x.batch, x.rows, x.cols,
-                  x.sb, x.sr, x.sc, e, v)
+                  x.sb, x.sr, x.sc, e, v, reads=_bytes(x))
       return out
     return self._new("cast", (self,), self.shape, dtype)
 
@@ -529,10 +554,12 @@ class Tensor:
     out.lead = x.lead
     if x.dtype in BFP:
       e, v = x._bfp_whole()._bfp_planes()
-      self.rt.run("columns", "bfp_columns", _lib.DTYPES[x.dtype], e, v, x.batch, x.rows, x.cols, out.storage.addr)
+      self.rt.run("columns", "bfp_columns", _lib.DTYPES[x.dtype], e, v, x.batch, x.rows, x.cols, out.storage.addr,
+                  reads=_bytes(x))
     else:
       if x.rep != 1 or x.cyc: x = x.contiguous()
-      self.rt.run("columns", "bf16_columns", x.addr, x.batch, x.rows, x.cols, x.sb, x.sr, x.sc, out.storage.addr)
+      self.rt.run("columns", "bf16_columns", x.addr, x.batch, x.rows, x.cols, x.sb, x.sr, x.sc, out.storage.addr,
+                  reads=_bytes(x))
     return out
 
   def float(self): return self.cast("fp32")
@@ -693,7 +720,7 @@ class Tensor:
     out = Tensor(self.rt, 1, w.cols, dtype=dtype)
     args = _lib.RowArgs(a.addr, nw.addr if nw is not None else 0, res.addr if res is not None else 0, out.addr,
                         w.storage.addr, k, w.cols, kind, _lib.DTYPES[w.dtype], _lib.DTYPES[dtype], eps)
-    self.rt.run("matmul_row", "matmul_row", ctypes.byref(args))
+    self.rt.run("matmul_row", "matmul_row", ctypes.byref(args), reads=_bytes(a, w, nw, res))
     return out
 
   def _matmul_row_rope(self, w, norm, eps, cos, sin, cache, places, heads, kv):
@@ -720,7 +747,7 @@ class Tensor:
                         _lib.DTYPES["bf16"], eps)
     tail = _lib.RopeArgs(0, c.addr, sn.addr, q.addr, cc.addr, pl.addr, 0, 0, q.sr, cc.sb, cc.sr, cc.rows, 1, heads, kv,
                          d, 0, 0, 0, 0)
-    self.rt.run("matmul_row_rope", "matmul_row_rope", ctypes.byref(args), ctypes.byref(tail))
+    self.rt.run("matmul_row_rope", "matmul_row_rope", ctypes.byref(args), ctypes.byref(tail), reads=_bytes(a, w, nw))
     return q
 
   def rms_rows(self, w, eps=1e-5):
@@ -733,7 +760,7 @@ class Tensor:
       raise ValueError(f"rms_rows needs bf16 weights, one for each column: {wt.shape} {wt.dtype}")
     out = Tensor(self.rt, x.rows, x.cols)
     out.lead = self.lead
-    self.rt.run("rms_rows", "rms_rows", x.addr, x.rows, x.cols, x.sr, wt.addr, eps, out.addr, out.sr)
+    self.rt.run("rms_rows", "rms_rows", x.addr, x.rows, x.cols, x.sr, wt.addr, eps, out.addr, out.sr, reads=_bytes(x, wt))
     return out
 
   def matmul_swiglu(self, w):
@@ -749,7 +776,7 @@ class Tensor:
     out.lead = self.lead
     self.rt.run("matmul_swiglu", "matmul_swiglu", ctypes.byref(_lib.operand(a.addr, "bf16", 0, a.sr)),
                 _lib.DTYPES[w.dtype], w.storage.addr, a.rows, a.cols, w.cols,
-                ctypes.byref(_lib.operand(out.addr, "bf16", 0, out.sr)))
+                ctypes.byref(_lib.operand(out.addr, "bf16", 0, out.sr)), reads=_bytes(a, w))
     return out
 
   def rope_put(self, cos, sin, cache, places, heads, kv, values=None):
@@ -779,7 +806,7 @@ class Tensor:
     args = _lib.RopeArgs(x.addr, c.addr, sn.addr, q.addr, cc.addr, pl.addr, x.sr, c.sr, q.sr, cc.sb, cc.sr, cc.rows,
                          x.rows, heads, kv, d, vc.addr if vc is not None else 0, kv * cc.sb if vc is not None else 0,
                          int(pl.cols == 1 and x.rows > 1), 0)
-    self.rt.run("rope_put", "rope_put", ctypes.byref(args))
+    self.rt.run("rope_put", "rope_put", ctypes.byref(args), reads=_bytes(x, c, sn))
     return q
 
   # ---- attention, rows in and out
@@ -823,7 +850,8 @@ class Tensor:
     if need.value:  # the parts' partial sums, freed (stream-ordered) once the launches that use them are queued
       scratch = Storage(self.rt, need.value)
       args.scratch, args.scratch_bytes = scratch.addr, need.value
-    self.rt.run("attention", "attention", ctypes.byref(args))
+    self.rt.run("attention", "attention", ctypes.byref(args), reads=_bytes(q) + q.batch // rep * 2 * k.rows * k.cols *
+                (2 if k.dtype == "bf16" else 17 / 16 if k.dtype == "bfp8" else 9 / 16))
     del scratch
     return out
 
@@ -862,7 +890,7 @@ class Tensor:
     values.lead = ids.lead = self.lead
     self.rt.run("topk", "topk", _lib.DTYPES[x.dtype], x.addr, x.batch, x.rows, x.cols, x.sb if x.batch > 1 else 0, x.sr,
                 parts, k, lab.addr if lab is not None else 0, (lab.sb if lab.batch > 1 else 0) if lab is not None else 0,
-                lab.sr if lab is not None else 0, values.addr, ids.addr)
+                lab.sr if lab is not None else 0, values.addr, ids.addr, reads=_bytes(x, lab))
     return values, ids
 
   def gather(self, ids):
@@ -880,7 +908,7 @@ class Tensor:
     if not ids._contiguous(): ids = ids.contiguous()
     out = Tensor(self.rt, ids.cols, t.cols, dtype=t.dtype)
     self.rt.run("gather", "gather", _lib.DTYPES[t.dtype], t.addr, t.rows, t.cols, t.sr, ids.addr, ids.cols,
-                out.addr, out.sr)
+                out.addr, out.sr, reads=_bytes(ids) + ids.cols * t.cols * t.itemsize)
     return out
 
   def put(self, ids, x):
@@ -895,13 +923,16 @@ class Tensor:
     x, ids = x.realize(), ids.realize()
     if x.sc != 1 or x.rep != 1 or x.cyc: x = x.contiguous()
     if not ids._contiguous(): ids = ids.contiguous()
+    _written(dst.storage)
     if dst.dtype in BFP:  # each run of 16 rounded as cast rounds it (kernels.py:1083-1168)
       e, v = dst._bfp_planes()
       self.rt.run("put", "put_bfp", _lib.DTYPES[dst.dtype], e, v, dst.batch, dst.rows, dst.cols,
-                  dst.sb if dst.batch > 1 else 0, dst.sr, ids.addr, ids.cols, x.addr, x.sb if x.batch > 1 else 0, x.sr)
+                  dst.sb if dst.batch > 1 else 0, dst.sr, ids.addr, ids.cols, x.addr, x.sb if x.batch > 1 else 0, x.sr,
+                  reads=_bytes(x, ids))
       return self
     self.rt.run("put", "put", _lib.DTYPES[dst.dtype], dst.addr, dst.batch, dst.rows, dst.cols,
-                dst.sb if dst.batch > 1 else 0, dst.sr, ids.addr, ids.cols, x.addr, x.sb if x.batch > 1 else 0, x.sr)
+                dst.sb if dst.batch > 1 else 0, dst.sr, ids.addr, ids.cols, x.addr, x.sb if x.batch > 1 else 0, x.sr,
+                reads=_bytes(x, ids))
     return self
 
   # ---- realize
@@ -916,6 +947,12 @@ class Tensor:
                          "tensor by columns")
       if self.op is None: raise ValueError("realize writes into a destination only from an unrealized tensor; assign copies a realized one")
     if self.op is None: return self
+    if into is not None and _reads_into(self, into):
+      # a kernel would overwrite what it still reads: a matmul's operand, or the same memory read at other places.
+      # Compute into storage of its own first, then copy (tensor.py:513-517).
+      into.assign(self.realize())
+      self._adopt(into)
+      return self
     out = into if into is not None else None
     if self.op == "matmul": _realize_matmul(self, None, out)
     elif self.op in REDUCE: _realize_reduce(self, out)
@@ -929,6 +966,16 @@ class Tensor:
     if not (self.op is None and self.rep == 1 and self.cyc == 0 and x.shape[-2:] == self.shape[-2:] and
             x.batch == self.batch and x.dtype == self.dtype):
       raise ValueError("assign requires a realized tensor with rep=1 and an x of the same shape and dtype")
+    if self.dtype in BFP:  # a block float: copied whole, or its values put row by row as a cast rounds them
+      if self.layout != "plain": raise ValueError("assign writes a plain tensor, not one by columns")
+      x = x.realize()
+      try:
+        if x.storage is not self.storage: return _copy_whole(x, self) or self
+      except ValueError:
+        pass
+      rows = x.cast("bf16").realize()  # decoded exactly, so the put gives back the same values
+      if not rows._contiguous(): rows = rows.contiguous()
+      return self.put(_row_ids(self.rt, self.rows), rows)
     if x.op is None and x.storage is self.storage: x = x._copy()  # overlapping storage: read it all first
     src = x if x.op is not None else x._copy_op()
     src.lead = self.lead
@@ -941,6 +988,35 @@ class Tensor:
     self.storage, self.offset, self.sb, self.sr, self.sc = other.storage, other.offset, other.sb, other.sr, other.sc
     self.rep, self.cyc, self.layout = other.rep, other.cyc, other.layout
     self.op, self.srcs, self.args, self.lead = None, (), (), lead
+
+
+def _reads_into(t, into):
+  """Whether computing t into `into` in one kernel could read memory that the kernel has already written: t's graph
+  reads into's storage as a matmul operand, or elementwise at other positions than the ones it writes there."""
+  seen, stack = set(), [(t, False)]
+  while stack:
+    u, by_matmul = stack.pop()
+    if not isinstance(u, Tensor) or (id(u), by_matmul) in seen: continue
+    seen.add((id(u), by_matmul))
+    if u.op is not None:
+      stack.extend((s, by_matmul or u.op == "matmul") for s in u.srcs)
+      continue
+    if u.storage is not into.storage: continue
+    same = (u._dims == into._dims and u.layout == into.layout and
+            (u.offset, u.sb if u.batch > 1 else 0, u.sr, u.sc, u.rep, u.cyc) ==
+            (into.offset, into.sb if into.batch > 1 else 0, into.sr, into.sc, into.rep, into.cyc))
+    if by_matmul or not same: return True
+  return False
+
+
+_ids = weakref.WeakKeyDictionary()
+
+
+def _row_ids(rt, n):
+  """An int32 row 0 .. n-1 on rt, made once (so a recording finds it made)."""
+  made = _ids.setdefault(rt, {})
+  if n not in made: made[n] = Tensor.of(rt, [list(range(n))], "int32")
+  return made[n]
 
 
 def _parts(t):
@@ -961,6 +1037,7 @@ def _run_copy(rt, operand, dtype, out):
 def _dest(t, into):
   """The realized tensor a kernel writes t's value to: into, or new storage."""
   if into is not None:
+    _written(into.storage)
     t._adopt(into)
     return into
   t.storage = None
@@ -1066,7 +1143,8 @@ def _realize_elementwise(t, into):
     return
   low, prog = _build(t, dtype, None)
   out = _dest(t, into)
-  t.rt.run(_name(prog), "elementwise", ctypes.byref(prog), out.batch, out.rows, out.cols, ctypes.byref(out._operand()))
+  t.rt.run(_name(prog), "elementwise", ctypes.byref(prog), out.batch, out.rows, out.cols, ctypes.byref(out._operand()),
+           reads=_bytes(*low.keep))
 
 
 def _name(prog):
@@ -1095,17 +1173,21 @@ def _realize_reduce(t, into):
   kind = _lib.REDUCE_SUM if t.op == "sum" else _lib.REDUCE_MAX  # before _dest, which clears t's op
   out = _dest(t, into)
   t.rt.run("reduce", "reduce", ctypes.byref(prog), kind, k, src.batch, src.rows, src.cols, sweep, step,
-           ctypes.byref(out._operand()))
+           ctypes.byref(out._operand()), reads=_bytes(*low.keep))
 
 
 def _b_tiles(b):
-  """(format, tiles address, batch, keep-alive) for a matmul's B: its columns tiles, made now if it has none."""
+  """(format, tiles address, batch, keep-alive) for a matmul's B: its columns tiles, made now if it has none. A block
+  float's tiles are kept with its storage, per view, until something writes the storage; inside a jit recording they
+  are made in the recording, so every replay reads the storage as it is then."""
   x = b.realize()
   if x.layout == "columns": return _lib.DTYPES[x.dtype], x.storage.addr, x.batch, x
   if x.dtype in BFP:
-    s = x.storage
-    if s.columns is None: s.columns = x.columns()  # a block float is repacked once, and kept with its storage
-    c = s.columns
+    s, key = x.storage, (x.offset, x.sb if x.batch > 1 else 0, x.sr, x.batch, x.rows, x.cols)
+    c = s.columns.get(key) if x.rt.recording is None else None
+    if c is None:
+      c = x.columns()
+      if x.rt.recording is None: s.columns[key] = c
     return _lib.DTYPES[c.dtype], c.storage.addr, c.batch, c
   c = x.columns()
   return _lib.BF16, c.storage.addr, c.batch, c
@@ -1129,7 +1211,8 @@ def _realize_matmul(m, root, into):
     aop = a._operand((batch,), a.rows, a.cols) if a.batch == batch else _lib.Operand(a.addr, 0, a.sr, a.sc, _lib.BF16, 1, 0, 0)
   else: aop = _lib.Operand(a.addr, a.sb, a.sr, a.sc, _lib.BF16, 1, 0, 0)
   m.rt.run("matmul", "matmul", ctypes.byref(aop), fmt, tiles, b_batch, batch, a.rows, a.cols, m.cols,
-           ctypes.byref(prog) if prog is not None else None, ctypes.byref(out._operand()))
+           ctypes.byref(prog) if prog is not None else None, ctypes.byref(out._operand()),
+           reads=_bytes(a, keep_b, *keep))
   if root is not None and m is not root:  # the matmul itself was never stored: a later read recomputes it
     pass
   del keep, keep_b
@@ -1161,6 +1244,7 @@ class Recording:
 
   def send(self):
     """Queue the recorded launches once more."""
+    self.rt.check()
     if self.active or self.graph is None: raise RuntimeError("recording is not ready for replay")
     _lib.call("graph_launch", self.rt.handle, self.graph)
     self.rt.launches += 1
@@ -1184,9 +1268,11 @@ class Recording:
 
 def jit(f):
   """Run f normally on the first call, record the second call into a HIP graph, and replay it from the third
-  (tensor.py:1231-1293). Each call's inputs are copied into the recorded inputs first, and a replay returns the
-  recorded results, which the next call overwrites. Keep input shapes and dtypes fixed."""
-  state = {"signature": None, "rec": None, "ins": None, "out": None}
+  (tensor.py:1231-1293). Each call's inputs are copied into the recording's own input buffers first; an input that f
+  writes (put, assign, realize into) is copied back after each call. A replay returns the recorded results, which the
+  next call overwrites. Keep input shapes, dtypes and layouts fixed; a block-float or by-columns input is taken as a
+  whole tensor, not a view."""
+  state = {"signature": None, "rec": None, "ins": None, "out": None, "wrote": ()}
 
   @functools.wraps(f)
   def run(*xs):
@@ -1194,7 +1280,8 @@ def jit(f):
       raise ValueError("jit inputs must be tensors, with at least one input")
     rt = xs[0].rt
     if any(x.rt is not rt for x in xs): raise ValueError("jit inputs must use the same runtime")
-    sig = [(x.shape, x.dtype) for x in xs]
+    rt.check()
+    sig = [(x.shape, x.dtype, x.layout) for x in xs]
     if state["signature"] is None:
       state["signature"] = sig
       return f(*xs).realize()
@@ -1202,27 +1289,55 @@ def jit(f):
       raise ValueError(f"a jit input is {sig}, where the first call had {state['signature']}")
     xs = [x.realize() for x in xs]
     if state["rec"] is None:
-      ins = [_fresh_copy(x) for x in xs]
+      ins = [_stand_in(x) for x in xs]
+      for x, t in zip(xs, ins): _copy_whole(x, t)
       rt.wait()
       rec = Recording(rt)
-      with rec:
-        out = f(*ins).realize()
-      state.update(rec=rec, ins=ins, out=out)
+      rt.written = set()
+      try:
+        with rec:
+          out = f(*ins).realize()
+      finally:
+        written, rt.written = rt.written, None
+      wrote = [i for i, t in enumerate(ins) if id(t.storage) in written]
+      state.update(rec=rec, ins=ins, out=out, wrote=wrote)
       rec.send()
-      return out
-    for x, t in zip(xs, state["ins"]):
-      if x.storage is not t.storage or x.offset != t.offset:
-        rt.copy(t.addr, x.contiguous().addr, t.batch * t.rows * t.cols * t.itemsize)
-    state["rec"].send()
+    else:
+      ins = state["ins"]
+      for x, t in zip(xs, ins):
+        if x.storage is not t.storage or x.offset != t.offset: _copy_whole(x, t)
+      state["rec"].send()
+    for i in state["wrote"]:  # what f wrote into an input goes back to the caller's tensor
+      if xs[i].storage is not ins[i].storage: _copy_whole(ins[i], xs[i])
     return state["out"]
   return run
 
 
-def _fresh_copy(x):
-  """A new contiguous tensor holding x's values (a jit's own input buffer)."""
-  t = Tensor(x.rt, x.rows, x.cols, batch=x.batch, dtype=x.dtype)
+def _stand_in(x):
+  """A new tensor laid out as x would be if made anew: a jit recording's own buffer for input x."""
+  if x.layout == "columns":
+    t = Tensor(x.rt, x.rows, x.cols, "view", (), x.batch, x.dtype)
+    t.op = None
+    t._alloc("columns")
+  else:
+    t = Tensor(x.rt, x.rows, x.cols, batch=x.batch, dtype=x.dtype)
   t.lead = x.lead
-  if x.dtype in ITEMSIZE and x.layout == "plain":
-    x._copy_op().realize(t) if not x._contiguous() else x.rt.copy(t.addr, x.addr, t.batch * t.rows * t.cols * t.itemsize)
   return t
 
+
+def _copy_whole(src, dst):
+  """Copies src's values into dst, a tensor of the same shape and format that owns its storage. Plain bf16, fp32 and
+  int32 views go through a copy kernel; block floats and tensors by columns are copied byte for byte, which takes
+  them whole: a view of a larger block float would bring another tensor's exponents and values."""
+  if src.dtype in ITEMSIZE and src.layout == "plain" and dst.layout == "plain":
+    if src._contiguous() and dst._contiguous():
+      src.rt.copy(dst.addr, src.addr, src.batch * src.rows * src.cols * src.itemsize)
+    else:
+      src._copy_op().realize(dst)
+    return
+  whole = lambda t: t.offset == 0 and (t.layout == "columns" or t._contiguous())
+  if not (whole(src) and whole(dst) and src.layout == dst.layout and src.storage.nbytes == dst.storage.nbytes and
+          src.storage.vals == dst.storage.vals):
+    raise ValueError("jit takes a block-float or by-columns input only as a whole tensor, not a view of one")
+  src.rt.copy(dst.storage.addr, src.storage.addr, src.storage.nbytes)
+  _written(dst.storage)

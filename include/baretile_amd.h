@@ -57,6 +57,10 @@ int bt_wait(bt_runtime *rt, double timeout_s);
  * (bytes: a multiple of 16, at most 4 GB - 16 KB). The plain streaming read that bench.py sets beside a kernel of the
  * same size, and the known-size read that calibrates the HBM byte counters. */
 int bt_stream_read(bt_runtime *rt, uint64_t src, uint64_t bytes, uint64_t scratch_word);
+/* No counterpart in the reference (a test aid, like test_device.py:962's kernel that never ends, but one that always
+ * does): queues a kernel that stays busy for `seconds` (0 to 10) of the device's wall clock and then ends by itself,
+ * so a wait with a shorter timeout raises TimeoutError and the stream still drains. */
+int bt_sleep(bt_runtime *rt, double seconds);
 /* Timing for Runtime.profile (runtime.py:773-786): events on the runtime's stream. */
 int bt_event_create(bt_runtime *rt, void **ev);
 int bt_event_record(bt_runtime *rt, void *ev);

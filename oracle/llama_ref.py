@@ -9,8 +9,9 @@ Reference sources restated here (Llama family only; Qwen/gpt-oss extras are out 
   models/llama.py:91-95    rms: x * rsqrt(mean(x^2) + eps) * w (bf16 rounding is the identity in NumPy, llama.py:27)
   models/llama.py:103-104  rope: x * cos + (x @ turn) * sin
   models/llama.py:106-183  layer / attention / mlp / glu (NumPy branch: full scores, softmax(s + mask) @ v)
-  models/llama.py:187-227  frequencies (default RoPE) and rotary: fp32 angles, bf16 tables repeated across heads,
-                           q's rows carrying 1/sqrt(head width), v's cos 1 and sin 0
+  models/llama.py:151-154  attention's put: rows going into a block-float (bfp8/bfp4) cache are rounded by gpt2.bfp first
+  models/llama.py:187-227  frequencies (default RoPE and Llama 3's scaling) and rotary: fp32 angles, bf16 tables
+                           repeated across heads, q's rows carrying 1/sqrt(head width), v's cos 1 and sin 0
   models/llama.py:238-291  fuse: q, k, v side by side; gate and up side by side
   models/llama.py:293-316  around (no slots): rows = places, rotary rows, mask over the cache's rows
   models/llama.py:325-363  forward (fp32 residual, last row's logits) and prefill in chunks
@@ -25,6 +26,10 @@ How it is pinned (tests/test_oracle.py):
   kv cache       a decode step after a prompt equals the full-prompt forward at the last position (the reference's
                  own check, test_models.py:851), and prefill in chunks equals one forward (test_models.py:1539)
   precision      the reference's known answers (test_models.py:1549-1556 for the "tt" and "bf16" keys)
+  frequencies    Llama 3's scaled frequencies against transformers' own llama3 RoPE initialisation (rtol 1e-6, as
+                 test_models.py:676-688), with its known answers: short wavelengths kept, long ones slowed by the factor
+  kv rounding    a block-float cache holds, row for row, bfp() of what a bf16 cache holds after the same step, every
+                 row is a fixed point of bfp(), and the logits move by less than the rounding can explain
 """
 import math
 from types import SimpleNamespace
@@ -33,8 +38,9 @@ from oracle import bfp as B
 
 
 def model(**kw):
-  """A config: dim, heads, kv, layers, eps, theta, plus vocab, ffn, head_dim, precision (llama.py:392-394)."""
-  base = dict(head_dim=None, vocab=None, ffn=None, precision=None, places=None)
+  """A config: dim, heads, kv, layers, eps, theta, plus vocab, ffn, head_dim, precision and rope, the RoPE scaling
+  parameters or None (llama.py:392-394, 418-425)."""
+  base = dict(head_dim=None, vocab=None, ffn=None, precision=None, places=None, rope=None)
   return SimpleNamespace(**(base | kw))
 
 
@@ -71,9 +77,20 @@ def weight_format(name, prec):
 
 
 def frequencies(c):
-  """Default RoPE inverse frequencies in float32 (llama.py:187-192)."""
+  """RoPE inverse frequencies in float32 (llama.py:187-200). Llama 3's scaling (rope_type "llama3") divides the
+  frequencies of wavelengths longer than original / low_freq_factor by the factor, keeps those shorter than
+  original / high_freq_factor, and in between blends the two linearly in original / wavelength."""
   hd = head(c)
-  return (1 / c.theta ** (np.arange(0, hd, 2, dtype=np.float32) / hd)).astype(np.float32)
+  inv = (1 / c.theta ** (np.arange(0, hd, 2, dtype=np.float32) / hd)).astype(np.float32)
+  r = getattr(c, "rope", None)
+  if r and r.get("rope_type") == "llama3":
+    factor, lo, hi = r["factor"], r["low_freq_factor"], r["high_freq_factor"]
+    span = r["original_max_position_embeddings"]
+    wave = np.float32(2 * math.pi) / inv
+    slow = inv / np.float32(factor)
+    t = (np.float32(span) / wave - np.float32(lo)) / np.float32(hi - lo)  # 0 at the long end of the blend, 1 at the short
+    inv = np.where(wave > span / lo, slow, np.where(wave < span / hi, inv, (1 - t) * slow + t * inv)).astype(np.float32)
+  return inv
 
 
 def rotary(c, n):
@@ -156,14 +173,24 @@ def merge(a):  # (n, rows, w) -> (rows, n * w)
   return a.transpose(1, 0, 2).reshape(a.shape[1], -1)
 
 
-def attention(h, p, c, rot, mask, cache, rows):
-  """One block's attention on the NumPy branch (llama.py:132-172)."""
+def cache_format(c):
+  """The KV cache's format, precision's kv entry (llama.py:74-83); bf16 without a precision table."""
+  return ((c.precision or {}).get(("kv", None)) or ("bf16", None))[0] or "bf16"
+
+
+def attention(h, p, c, rot, mask, cache, rows, only=None):
+  """One block's attention on the NumPy branch (llama.py:132-172). The new key and value rows go into the cache as a
+  cache of c's format holds them: a block-float cache rounds each run of 16 along a row by bfp (llama.py:151-154).
+  only, a list of row indices, returns those query rows alone (every row's keys and values still go into the cache);
+  a row's attention reads no other query row, so this is the full result's rows."""
   hd, rep, nh = head(c), c.heads // c.kv, c.heads + 2 * c.kv
   qkv = split(h @ p["qkv_proj"], nh)
   qkv = merge(rope(qkv, split(rot[0], nh), split(rot[1], nh), rot[2]))
   heads = split(qkv, nh)
-  cache[:, list(rows)] = heads[c.heads:c.heads + 2 * c.kv]
+  kv, fmt = heads[c.heads:c.heads + 2 * c.kv], cache_format(c)
+  cache[:, list(rows)] = B.bfp(kv, fmt) if fmt != "bf16" else kv
   q, k, v = heads[:c.heads], cache[:c.kv], cache[c.kv:]
+  if only is not None: q, mask = q[:, only], mask[only]
   m = mask.shape[-1]
   if m < k.shape[-2]: k, v = k[:, :m], v[:, :m]
   k, v = np.repeat(k, rep, 0), np.repeat(v, rep, 0)
@@ -180,9 +207,11 @@ def mlp(h, p):
   return (g / (1 + np.exp(-g)) * u) @ p["down_proj"]
 
 
-def layer(x, p, c, rot, mask, cache, rows):
-  """Attention then the SwiGLU MLP, each after an RMSNorm and added to the residual (llama.py:106-130)."""
-  x = x + attention(rms(x, p["input_layernorm"], c.eps), p, c, rot, mask, cache, rows)
+def layer(x, p, c, rot, mask, cache, rows, only=None):
+  """Attention then the SwiGLU MLP, each after an RMSNorm and added to the residual (llama.py:106-130). only: just
+  those rows of the result (see attention)."""
+  a = attention(rms(x, p["input_layernorm"], c.eps), p, c, rot, mask, cache, rows, only)
+  x = (x if only is None else x[only]) + a
   return x + mlp(rms(x, p["post_attention_layernorm"], c.eps), p)
 
 

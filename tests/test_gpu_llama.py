@@ -11,6 +11,8 @@ pytestmark = pytest.mark.gpu
 
 
 def setup(rt, layers, vocab, mode, places=96, seed=12):
+  """An oracle config and weights in SmolLM's shapes, and the same on the device in precision `mode`. The oracle's
+  config carries no precision table (a bf16 KV cache) unless a test gives it one."""
   rng = np.random.default_rng(seed)
   c, w = L.smol(rng, layers, vocab=vocab, places=places)
   prec = L.precision(c, mode)
@@ -108,23 +110,45 @@ def test_slots_layer_matches_each_slot_in_numpy(rt):
       assert np.abs(got_r - want_r).max() <= 0.03 * np.abs(want_r).max(), (s, np.abs(got_r - want_r).max())
 
 
-def test_block_float_kv_cache_matches_numpy(rt):
-  # the KV cache in bfp8 (precision's kv entry, tt_transformers' cache format, llama.py:74-83): a prompt's logits and
-  # a one-token step (the row kernels, with the rows put through the block-float put) within 3% of the oracle's,
-  # whose cache keeps the unrounded values
+@pytest.mark.parametrize("kv", ["bfp8", "bfp4"])
+def test_block_float_kv_cache_matches_numpy(rt, kv):
+  # the KV cache in bfp8 or bfp4 (precision's kv entry, tt_transformers' cache format, llama.py:74-83): a prompt's
+  # logits and a one-token step (the row kernels, with the rows put through the block-float put), against the oracle,
+  # whose cache rounds the rows it puts the same way (llama.py:151-154), within 1% of the logits' span and the same pick
   c, ref, dc, dw = setup(rt, 2, 256, "bfp8")
-  dc.precision = llama.precision(llama.model(layers=2, dim=576), "bfp8", kv="bfp8")
+  dc.precision = llama.precision(llama.model(layers=2, dim=576), "bfp8", kv=kv)
+  c.precision = L.precision(c, "bfp8", kv=kv)
   caches = llama.kv_cache(rt, dc, 96)
-  assert caches[0].dtype == "bfp8"
+  assert caches[0].dtype == kv and L.cache_format(c) == kv
   ids = [7, 200, 31, 64, 5, 9, 100, 3]
   got = np.array(llama.forward(Tensor.of(rt, [ids], "int32"), Tensor.of(rt, [list(range(8))], "int32"), dw, dc, caches,
                                every=True).tolist())
   rcaches = L.kv_cache(c, 96)
   want = L.forward(ids, range(8), ref, c, rcaches, every=True)
-  assert np.abs(got - want).max() <= 0.03 * np.abs(want).max(), np.abs(got - want).max()
+  assert np.abs(got - want).max() <= 0.01 * np.ptp(want), np.abs(got - want).max()
+  assert (got.argmax(-1) == want.argmax(-1)).all()
   step = np.array(llama.forward(Tensor.of(rt, [[42]], "int32"), Tensor.of(rt, [[8]], "int32"), dw, dc, caches).tolist())[0]
   want = L.forward([42], [8], ref, c, rcaches)[0]
-  assert np.abs(step - want).max() <= 0.03 * np.abs(want).max(), np.abs(step - want).max()
+  assert np.abs(step - want).max() <= 0.01 * np.ptp(want) and step.argmax() == want.argmax(), np.abs(step - want).max()
+
+
+@pytest.mark.parametrize("mode", ["bfp4", "tt"])
+def test_llama_precision_modes(rt, mode):
+  # test_models.py:1549-1583: bfp4 mode puts gate_up in bfp4 and the rest in bfp8; tt also makes the KV cache bfp8.
+  # NumPy with the same block-float values and exact products picks the same token, within 1% of the logits' span
+  c, ref, dc, dw = setup(rt, 2, 256, mode, seed=5)
+  c.precision = L.precision(c, mode)
+  formats = {k: t.dtype for k, t in dw.items() if k.endswith("_proj") or k == "embed.T"}
+  assert formats == {k: "bfp4" if "gate_up" in k else "bfp8" for k in formats}
+  caches = llama.kv_cache(rt, dc, 32)
+  assert caches[0].dtype == ("bfp8" if mode == "tt" else "bf16")
+  rcaches = L.kv_cache(c, 32)
+  for ids, places in (([7, 200, 31], [0, 1, 2]), ([5], [3])):
+    got = np.frombuffer(llama.forward(Tensor.of(rt, [ids], "int32"), Tensor.of(rt, [places], "int32"), dw, dc,
+                                      caches).tobytes(), np.float32)
+    want = L.forward(ids, places, ref, c, rcaches)[0]
+    assert got.argmax() == want.argmax() and np.abs(got - want).max() < 0.01 * np.ptp(want), \
+        (places, np.abs(got - want).max(), np.ptp(want))
 
 
 def test_loaded_checkpoint_matches_numpy(rt, tmp_path):

@@ -1,5 +1,6 @@
 """Serving on the GPU: heads (top-k and log-sum-exp) against NumPy, and the slot engine's greedy streams against
 single-sequence decode. Needs a GPU."""
+import math
 import numpy as np
 import pytest
 
@@ -8,6 +9,13 @@ from baretile_amd.tensor import Tensor
 from oracle import llama_ref as L
 
 pytestmark = pytest.mark.gpu
+
+
+def numpy_head(x, t, k=64):
+  """The k largest of a row, largest first with equal values in column order (a stable sort), and
+  log(sum(exp((x - max) * t))) in float64."""
+  ids = np.argsort(-x, kind="stable")[:k]
+  return x[ids], ids, math.log(np.exp((x.astype(np.float64) - x.max()) * t).sum())
 
 
 def test_heads_match_numpy(rt):
@@ -20,9 +28,9 @@ def test_heads_match_numpy(rt):
   values, ids = np.array(values.tolist()).reshape(3, 64), np.array(ids.tolist()).reshape(3, 64)
   lse = np.array(lse.tolist()).reshape(3)
   for i, t in enumerate(ts):
-    want = serve.Head.of(x[i], t)
-    assert np.array_equal(ids[i], want.ids) and np.array_equal(values[i], want.values), i
-    assert abs(lse[i] - want.lse) <= 1e-4 * max(1.0, abs(want.lse)), (i, lse[i], want.lse)
+    want_v, want_i, want_lse = numpy_head(x[i], t)
+    assert np.array_equal(ids[i], want_i) and np.array_equal(values[i], want_v), i
+    assert abs(lse[i] - want_lse) <= 1e-4 * max(1.0, abs(want_lse)), (i, lse[i], want_lse)
 
 
 def model(rt, vocab=512, layers=2, places=64, seed=12):
@@ -35,24 +43,27 @@ def model(rt, vocab=512, layers=2, places=64, seed=12):
 
 
 def test_engine_greedy_matches_single_sequence_decode(rt):
-  # three requests of different lengths decode together in three slots, one replayed step for all; each stream equals
-  # the same prompt decoded alone (llama.generate)
+  # three streams of different lengths decode together in three slots, one replayed step for all; each equals the same
+  # prompt decoded alone (llama.generate)
   dc, dw = model(rt)
   prompts = [[7, 200, 31, 64, 5], [3, 1, 4, 1, 5, 9, 2, 6, 5], [42, 43]]
   engine = serve.Engine(rt, dw, dc, slots=3, places=64, chunk=4)
-  reqs = [serve.Request(p, max_tokens=8, temperature=0) for p in prompts]
-  for r in reqs: assert engine.offer(r)
+  streams = [engine.submit(serve.Stream(p, limit=8)) for p in prompts]
   for _ in range(40):
     engine.step()
-    if all(r.finish for r in reqs): break
-  for p, r in zip(prompts, reqs):
+    if all(s.ended for s in streams): break
+  for p, s in zip(prompts, streams):
     want, _ = llama.generate(dw, dc, p, 8, 64)
-    assert r.finish == "length" and r.made == want, (p, r.made, want)
-  # a fourth request reuses a free slot, and its prompt's shared prefix
-  r = serve.Request(prompts[1][:6] + [100], max_tokens=4, temperature=0)
-  assert engine.offer(r)
+    assert s.ended == "limit" and s.tokens == want, (p, s.tokens, want)
+  # a fourth stream reuses a free slot's cache rows for its prompt's shared prefix
+  s = engine.submit(serve.Stream(prompts[1][:6] + [100], limit=4))
   for _ in range(20):
     engine.step()
-    if r.finish: break
+    if s.ended: break
   want, _ = llama.generate(dw, dc, prompts[1][:6] + [100], 4, 64)
-  assert r.made == want and r.cached == 6
+  assert s.tokens == want and s.reused == 6
+  # a stream that runs out of rows ends with "full" after the last token its slot can feed
+  s = engine.submit(serve.Stream(list(range(1, 59)), limit=50))
+  while not s.ended: engine.step()
+  assert s.ended == "full" and len(s.tokens) == 64 - 1 - 58 + 1
+  with pytest.raises(ValueError): engine.submit(serve.Stream(list(range(63))))

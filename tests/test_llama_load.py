@@ -93,5 +93,33 @@ def test_load_keeps_the_configs_blocks_and_refuses_other_models(tmp_path):
   assert c.layers == 1 and not any(k.startswith("layers.1.") for k in w)
   json.dump(cfg | {"model_type": "qwen3_moe"}, open(tmp_path / "config.json", "w"))
   with pytest.raises(ValueError, match="isn't supported"): llama.load(str(tmp_path))
-  json.dump(cfg | {"rope_scaling": {"rope_type": "llama3", "factor": 8.0}}, open(tmp_path / "config.json", "w"))
+  json.dump(cfg | {"rope_scaling": {"rope_type": "yarn", "factor": 8.0}}, open(tmp_path / "config.json", "w"))
   with pytest.raises(ValueError, match="RoPE scaling"): llama.load(str(tmp_path))
+
+
+LLAMA3 = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+          "original_max_position_embeddings": 8192}
+
+
+@pytest.mark.parametrize("style", ["rope_scaling", "rope_parameters", "type"])
+def test_load_takes_llama3_rope_scaling(tmp_path, style):
+  # llama.py:400-427 with Llama 3.1's config: the scaling is kept as c.rope, whichever way transformers wrote it, and
+  # the frequencies equal the oracle's (which transformers' own llama3 initialisation pins) bit for bit
+  from oracle import llama_ref as L
+  checkpoint(str(tmp_path), dim=128, heads=2, kv=1, layers=1)
+  cfg = json.load(open(tmp_path / "config.json"))
+  cfg.pop("rope_theta")
+  if style == "rope_scaling": cfg |= {"rope_scaling": LLAMA3, "rope_theta": 500000.0}
+  elif style == "rope_parameters": cfg |= {"rope_parameters": LLAMA3 | {"rope_theta": 500000.0}}
+  else:
+    old = {k: v for k, v in LLAMA3.items() if k != "rope_type"} | {"type": "llama3"}
+    cfg |= {"rope_scaling": old, "rope_theta": 500000.0}
+  json.dump(cfg, open(tmp_path / "config.json", "w"))
+  c, _ = llama.load(str(tmp_path), places=64)
+  assert c.rope == LLAMA3 and c.theta == 500000.0 and c.places == 64
+  rc = L.model(dim=c.dim, heads=c.heads, kv=c.kv, layers=c.layers, eps=c.eps, theta=c.theta, rope=c.rope)
+  assert np.array_equal(llama.frequencies(c), L.frequencies(rc))
+  got, want = llama.rotary(c, 64), L.rotary(rc, 64)
+  assert all(np.array_equal(g, w) for g, w in zip(got, want))
+  plain = llama.model(**{**vars(c), "rope": None})
+  assert not np.array_equal(llama.frequencies(plain), llama.frequencies(c))

@@ -248,3 +248,64 @@ def test_precision_known_answers():
   assert L.weight_format("embed.T", p8) == "bfp8" and L.weight_format("layers.3.down_proj", p8) == "bfp8"
   assert L.weight_format("layers.3.input_layernorm", p8) == "bf16" and L.weight_format("embed", p8) == "bf16"
   with pytest.raises(ValueError): L.precision(big, "fp8")
+
+
+def test_llama3_frequencies_match_transformers():
+  # test_models.py:676-688: Llama 3.1's scaled frequencies against transformers' own llama3 initialisation, within a
+  # relative 1e-6, with the known answers: the shortest wavelength kept, the longest slowed by exactly the factor
+  from transformers import LlamaConfig
+  from transformers.modeling_rope_utils import ROPE_INIT_FUNCTIONS
+  rope = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+          "original_max_position_embeddings": 8192}
+  hf = LlamaConfig(hidden_size=4096, num_attention_heads=32, rope_theta=500000.0, rope_scaling=rope,
+                   max_position_embeddings=131072)
+  want = ROPE_INIT_FUNCTIONS["llama3"](hf, "cpu")[0].numpy()
+  c = L.model(dim=4096, heads=32, kv=8, layers=1, eps=1e-5, theta=500000.0, rope=rope)
+  got = L.frequencies(c)
+  assert got.dtype == np.float32 and np.allclose(got, want, rtol=1e-6, atol=0), np.abs(got / want - 1).max()
+  plain = L.frequencies(L.model(dim=4096, heads=32, kv=8, layers=1, eps=1e-5, theta=500000.0))
+  assert plain[0] == got[0] and plain[-1] == 8 * got[-1]
+  # some frequencies fall in the blend, where a wrong interpolation (its ends swapped) would be far off
+  blend = (got != plain) & (got != plain / 8)
+  assert blend.sum() >= 3
+  swapped = L.model(**vars(c))
+  swapped.rope = dict(rope, low_freq_factor=4.0, high_freq_factor=1.0)
+  assert not np.allclose(L.frequencies(swapped)[blend], want[blend], rtol=1e-3)
+
+
+def test_block_float_kv_cache_rounds_its_rows():
+  # llama.py:151-154: with a bfp8 or bfp4 cache, the rows NumPy puts are gpt2.bfp of the rows a bf16 cache would get.
+  # Checked on one step from the same starting cache: every cached row is bfp() of the bf16 run's row (so a fixed point
+  # of bfp), rows not written stay as they were, and the logits move by no more than the rounding explains.
+  rng = np.random.default_rng(21)
+  c, w = L.smol(rng, 1, vocab=64, places=16)
+  ids, places = [3, 17, 40, 9], range(4)
+  plain = L.kv_cache(c, 16)
+  want_logits = L.forward(ids, places, w, c, plain, every=True)
+  for fmt in B.FORMATS:
+    cb = L.model(**vars(c))
+    cb.precision = L.precision(c, "bf16", kv=fmt)
+    assert L.cache_format(cb) == fmt and L.cache_format(c) == "bf16"
+    caches = L.kv_cache(cb, 16)
+    got_logits = L.forward(ids, places, w, cb, caches, every=True)
+    # the first step's rows come from identical inputs in both runs, so they are exactly bfp() of the bf16 run's
+    assert np.array_equal(caches[0][:, :4], B.bfp(plain[0][:, :4], fmt))
+    assert np.array_equal(B.bfp(caches[0][:, :4], fmt), caches[0][:, :4])
+    assert not caches[0][:, 4:].any()
+    assert not np.array_equal(caches[0][:, :4], plain[0][:, :4])  # the rounding did something
+    err = np.abs(got_logits - want_logits).max()
+    assert 0 < err < (0.05 if fmt == "bfp8" else 0.4) * np.abs(want_logits).max(), (fmt, err)
+
+
+def test_layer_rows_equal_the_full_layer():
+  # layer(..., only=rows) is those rows of the full result, and fills the cache the same way
+  rng = np.random.default_rng(4)
+  c, w = L.smol(rng, 1, vocab=64, places=32)
+  x = rng.normal(0, 1, (20, 576)).astype(np.float32)
+  rot = (w["cos"][:20], w["sin"][:20], w["turn"])
+  mask = np.where(np.arange(32) > np.arange(20)[:, None], np.float32(-1e9), np.float32(0))
+  full_cache, part_cache = L.kv_cache(c, 32), L.kv_cache(c, 32)
+  full = L.layer(x, L.block(w, 0), c, rot, mask, full_cache[0], range(20))
+  rows = [0, 7, 19]
+  part = L.layer(x, L.block(w, 0), c, rot, mask, part_cache[0], range(20), only=rows)
+  assert np.allclose(part, full[rows], rtol=1e-6, atol=1e-6) and np.array_equal(part_cache[0], full_cache[0])

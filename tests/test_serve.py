@@ -1,39 +1,25 @@
-"""Serving: heads of logits on the device, the slot engine against single-sequence decode, and the host sampler."""
-import numpy as np
+"""Serving's host logic, on the CPU: how a stream takes tokens and ends, and which prompt tokens a slot can skip."""
 import pytest
 
 from baretile_amd.models import serve
 
 
-def test_sampling_from_a_head_matches_the_row():
-  # serve.py:143-188: where the head decides the pick (greedy, a top_k or top_p cut within it), a pick from the head
-  # equals the pick from the whole row with the same seed
-  rng = np.random.default_rng(0)
-  for trial in range(40):
-    logits = rng.normal(0, 3, 1000)
-    for kw in (dict(temperature=0), dict(temperature=0.7, top_k=20), dict(temperature=0.5, top_p=0.9)):
-      a, b = serve.Request([1], seed=trial, **kw), serve.Request([1], seed=trial, **kw)
-      head = serve.Head.of(logits, serve.scale(a), k=64)
-      assert a.pick(head) == b.draw(logits), (trial, kw)
+def test_stream_ends_at_limit_stop_or_full_slot():
+  s = serve.Stream([1, 2], limit=3, stop=(5,))
+  assert not s.offer(7, True) and s.tokens == [7] and s.ended is None
+  assert s.offer(5, True) and s.ended == "stop" and s.tokens == [7] and s.finished.is_set()
+  s = serve.Stream([1], limit=2)
+  assert not s.offer(4, True) and s.offer(4, True) and s.ended == "limit" and s.wait(0) == [4, 4]
+  s = serve.Stream([1], limit=9)
+  assert s.offer(3, False) and s.ended == "full" and s.tokens == [3]  # the token is kept; no row is left to feed it
+  with pytest.raises(TimeoutError): serve.Stream([1]).wait(0)
+  for bad in (dict(prompt=[], limit=2), dict(prompt=[1], limit=0), dict(prompt=[1], limit=1.5)):
+    with pytest.raises(ValueError): serve.Stream(**bad)
 
 
-def test_sampling_without_a_cut_keeps_every_probability():
-  # with no cut a draw may land past the head's mass and then reads the row back: every token keeps its probability
-  rng = np.random.default_rng(1)
-  logits = rng.normal(0, 1, 50)
-  r = serve.Request([1], seed=5, temperature=1.5)
-  head = serve.Head.of(logits, serve.scale(r), k=10)
-  n = 40000
-  counts = np.bincount([r.pick(head) for _ in range(n)], minlength=50)
-  p = np.exp(logits / 1.5 - (logits / 1.5).max())
-  assert np.abs(counts / n - p / p.sum()).max() < 0.01
-
-
-def test_request_ends():
-  r = serve.Request([1, 2], max_tokens=2, temperature=0, eos=(5,))
-  assert not r.take(np.array([0.0, 3.0, 1.0, 0.0, 0.0, 0.0]), True) and r.made == [1]
-  assert r.take(np.array([0.0, 0.0, 1.0, 0.0, 0.0, 9.0]), True) and r.finish == "stop" and r.made == [1]
-  r = serve.Request([1], max_tokens=1, temperature=0)
-  assert r.take(np.array([0.0, 3.0]), True) and r.finish == "length"
-  with pytest.raises(ValueError): serve.Request([1], temperature=-1)
-  with pytest.raises(ValueError): serve.Request([1], top_p=0)
+def test_shared_prefix_keeps_the_last_prompt_token():
+  assert serve.shared([], [1, 2, 3]) == 0
+  assert serve.shared([1, 2, 9, 9], [1, 2, 3]) == 2
+  assert serve.shared([1, 2, 3, 4], [1, 2, 3]) == 2  # all of it is kept, but the last token runs again for its logits
+  assert serve.shared([1, 2, 3], [1, 2, 3, 4, 5]) == 3
+  assert serve.shared([5], [1]) == 0
