@@ -81,6 +81,7 @@ SIGNATURES = {
   "bt_bfp_pack": [RT, c_int, U64, c_int, I64, I64, I64, I64, I64, I64, U64, U64],
   "bt_bfp_unpack": [RT, c_int, U64, U64, I64, I64, I64, U64],
   "bt_bfp_columns": [RT, c_int, U64, U64, I64, I64, I64, U64],
+  "bt_bfp_range": [RT, c_int, U64, U64, I64, I64, I64, U64],
   "bt_bf16_columns": [RT, U64, I64, I64, I64, I64, I64, I64, U64],
   "bt_columns_unpack": [RT, c_int, U64, I64, I64, I64, U64],
   "bt_elementwise": [RT, POINTER(Program), I64, I64, I64, POINTER(Operand)],

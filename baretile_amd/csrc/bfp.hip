@@ -87,6 +87,32 @@ __global__ void __launch_bounds__(256) put_bfp_kernel(uint8_t *exps, uint8_t *va
   }
 }
 
+// Counts, into *bad, the runs of the plain planes that hold a nonzero value under an exponent the matmul kernels can't
+// read: they take the exponent byte as the signed power (e - 133) (bfp8) or (e - 120) (bfp4), so bfp8 needs e >= 5 and
+// bfp4 e <= 247; and a bfp4 B decoded in registers needs e >= 3, where every value is a normal bf16. A run of zeros
+// multiplies to zero under any exponent, so it never counts. One thread a run.
+template <int FMT>
+__global__ void __launch_bounds__(256) range_kernel(const uint8_t *exps, const uint8_t *vals, int64_t runs,
+                                                   uint32_t *bad) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= runs) return;
+  const uint32_t e = exps[t];
+  if (FMT == BT_BFP8 ? e >= 5u : e >= 3u && e <= 247u) return;
+  uint32_t any = 0;
+  if (FMT == BT_BFP8) {
+    const uint4 v = *(const uint4 *)(vals + t * 16);
+    any = v.x | v.y | v.z | v.w;
+  } else {
+    const uint2 v = *(const uint2 *)(vals + t * 8);
+    any = v.x | v.y;
+  }
+  if (any) atomicAdd(bad, 1u);
+}
+
+__global__ void zero_word_kernel(uint32_t *word) {
+  if (threadIdx.x == 0) word[0] = 0;
+}
+
 // Signed q of value c in row r of matrix b of the plain planes.
 template <int FMT>
 __device__ __forceinline__ int plain_q(const uint8_t *vals, int64_t row_bytes, int64_t b_rows_r, int64_t c) {
@@ -284,6 +310,26 @@ int bt_bfp_columns(bt_runtime *rt, int fmt, uint64_t exps, uint64_t vals, int64_
     columns_kernel<BT_BFP4><<<(unsigned)tiles, 64, 0, r->stream>>>((const uint8_t *)exps, (const uint8_t *)vals, rows,
                                                                     cols, chunks, nruns, (uint8_t *)dst);
   BT_LAUNCHED("bfp_columns");
+  return BT_OK;
+}
+
+int bt_bfp_range(bt_runtime *rt, int fmt, uint64_t exps, uint64_t vals, int64_t batch, int64_t rows, int64_t cols,
+                 uint64_t bad) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (int s = check_fmt(fmt)) return s;
+  if (int s = check_shape(batch, rows, cols)) return s;
+  if (vals % 16 || bad % 4) return fail(BT_EINVAL, "the value plane must be 16-byte aligned and the count 4-byte aligned");
+  const int64_t runs = batch * rows * ((cols + 15) / 16);
+  zero_word_kernel<<<1, 64, 0, r->stream>>>((uint32_t *)(uintptr_t)bad);
+  BT_LAUNCHED("bfp_range");
+  if (fmt == BT_BFP8)
+    range_kernel<BT_BFP8><<<blocks_for(runs, 256), 256, 0, r->stream>>>((const uint8_t *)exps, (const uint8_t *)vals,
+                                                                         runs, (uint32_t *)(uintptr_t)bad);
+  else
+    range_kernel<BT_BFP4><<<blocks_for(runs, 256), 256, 0, r->stream>>>((const uint8_t *)exps, (const uint8_t *)vals,
+                                                                         runs, (uint32_t *)(uintptr_t)bad);
+  BT_LAUNCHED("bfp_range");
   return BT_OK;
 }
 

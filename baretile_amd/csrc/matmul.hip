@@ -121,24 +121,35 @@ __device__ __forceinline__ bf16x8 q4_to_bf16(uint32_t w) {  // q * 2^-9 as bf16,
   return *(const bf16x8 *)&v;
 }
 
-__device__ __forceinline__ bf16x8 q4_to_bf16_scaled(uint32_t w, uint2 d) {  // q * 2^-9 * 2^d, in k order
+// bfp4, B side, without a per-value ldexp: the lane's 8 values of one half (w, laid out as q4_to_fp8 reads it) times
+// their own powers of two. Each pair converts through fp8 with the scale 2^127, which puts a nonzero q at the bf16
+// exponent field lg|q| + 245, normal whatever q is; then a saturating 16-bit subtraction takes each value's gap
+// x = 247 - e off its exponent field (the sign bit is above it, the mantissa below), giving q * 2^(e - 129) exactly,
+// and leaves a zero at zero (0 - anything saturates to 0). x0 and x1 hold the gaps of values 0..3 and 4..7 as bytes;
+// a columns tile stores d = e - 120 as a byte, and 247 - e = 127 - d = d ^ 0x7F bytewise. Exact for run exponents e in
+// 3..247, where every result is a normal bf16.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t gap_sub(uint32_t bits, uint32_t x, uint32_t sel) {
+  const uint32_t gap = __builtin_amdgcn_perm(0u, x, sel) << 7;  // two gaps, one in each 16-bit half's exponent field
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, bits),
+                                                                    __builtin_bit_cast(u16x2, gap)));
+}
+__device__ __forceinline__ bf16x8 q4_to_bf16_gaps(uint32_t w, uint32_t x0, uint32_t x1) {
   uint32_t lo, hi;
   q4_to_fp8(w, lo, hi);
-  float f[8];
-  auto a = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
-  auto b = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
-  auto c = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
-  auto e = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-  f[0] = a[0]; f[1] = a[1]; f[2] = b[0]; f[3] = b[1]; f[4] = c[0]; f[5] = c[1]; f[6] = e[0]; f[7] = e[1];
-  uint32_t r[4];
-#pragma unroll
-  for (int p = 0; p < 4; p++) {
-    float u0 = ldexpf(f[2 * p], (int)(int8_t)((2 * p < 4 ? d.x : d.y) >> (8 * ((2 * p) & 3))));
-    float u1 = ldexpf(f[2 * p + 1], (int)(int8_t)((2 * p + 1 < 4 ? d.x : d.y) >> (8 * ((2 * p + 1) & 3))));
-    r[p] = pack_hi(u0, u1);
-  }
-  uint4 v = make_uint4(r[0], r[1], r[2], r[3]);
+  const uint32_t c0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 0x1p127f, false));
+  const uint32_t c1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 0x1p127f, true));
+  const uint32_t c2 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 0x1p127f, false));
+  const uint32_t c3 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 0x1p127f, true));
+  uint4 v = make_uint4(gap_sub(c0, x0, 0x0C010C00u), gap_sub(c1, x0, 0x0C030C02u), gap_sub(c2, x1, 0x0C010C00u),
+                       gap_sub(c3, x1, 0x0C030C02u));
   return *(const bf16x8 *)&v;
+}
+
+// q * 2^-9 * 2^d for a lane's 8 bfp4 values, d the signed exponent bytes of values 0..3 (d.x) and 4..7 (d.y) as a
+// columns tile stores them: the same exact values as q4_to_bf16_gaps, which computes them.
+__device__ __forceinline__ bf16x8 q4_to_bf16_scaled(uint32_t w, uint2 d) {
+  return q4_to_bf16_gaps(w, d.x ^ 0x7F7F7F7Fu, d.y ^ 0x7F7F7F7Fu);
 }
 
 // Lane l's 8 values of A for its row, columns k0 .. k0+7 (zero outside A). row is the lane's row of A (row 0 for a
@@ -1091,7 +1102,7 @@ template <int N> __device__ __forceinline__ void wait_vm() {
 // at once, 8 KB or more apart), while its 4 waves' weights are in flight; each wave then multiplies NRW runs of B
 // from there and writes its fp32 partial tiles. A is read once a block instead of once a wave. parts_reduce_kernel
 // sums each output's splits in split order and runs the epilogue (rounding, program, or SiLU x up).
-template <int FMT, int MT, int NRW, int G>
+template <int FMT, int MT, int NRW, int G, bool FULL = false>
 __global__ void __launch_bounds__(256) skinny_part_kernel(const MatmulArgs args, int groups, float *part) {
   constexpr int TB = Tile<FMT>::bytes, KP = G * 64 + 8;  // padded rows: a fragment read's 16 rows hit distinct banks
   __shared__ __attribute__((aligned(16))) uint16_t la[16 * MT * KP];
@@ -1114,8 +1125,10 @@ __global__ void __launch_bounds__(256) skinny_part_kernel(const MatmulArgs args,
         r < h.m ? (uint32_t)(((int64_t)r * h.a.sr + (int64_t)c0 * 64 + piece * 512) * 2) + 16u * lane : abytes;
     lds_load16(ar, voff, la + r * KP + piece * 512);
   }
-  // 2. the wave's weights: G chunks of each of its runs from chunk c0 (past the split's last: zeros)
-  uint32_t bq[NRW][G][FMT == BT_BF16 ? 8 : FMT == BT_BFP8 ? 4 : 2], ew[NRW][G];
+  // 2. the wave's weights: G chunks of each of its runs from chunk c0 (past the split's last: zeros). A bfp4 lane takes
+  // its group's 16 exponent bytes (rows 16g .. 16g + 15 of the tile: both halves' 8) with one load; the other formats
+  // take one exponent word a lane and share them by shuffles.
+  uint32_t bq[NRW][G][FMT == BT_BF16 ? 8 : FMT == BT_BFP8 ? 4 : 2], ew[NRW][G][FMT == BT_BFP4 ? 4 : 1];
 #pragma unroll
   for (int r = 0; r < NRW; r++) {
     const bool in = run0 + r < h.nruns;
@@ -1138,8 +1151,12 @@ __global__ void __launch_bounds__(256) skinny_part_kernel(const MatmulArgs args,
       } else {
         const auto q = __builtin_amdgcn_raw_buffer_load_b64(tr, at + 64 + 8 * lane, 0, 0);
         bq[r][i][0] = q[0], bq[r][i][1] = q[1];
+        const auto e = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 16 * g, 0, 0);
+#pragma unroll
+        for (int w = 0; w < 4; w++) ew[r][i][w] = e[w];
+        continue;
       }
-      ew[r][i] = __builtin_amdgcn_raw_buffer_load_b32(tr, at + 4 * col, 0, 0);  // exponent word col of 16
+      ew[r][i][0] = __builtin_amdgcn_raw_buffer_load_b32(tr, at + 4 * col, 0, 0);  // exponent word col of 16
     }
   }
   // A's loads, issued first, have landed (loads complete in order; at most 63 can be counted, and with more B loads
@@ -1154,12 +1171,12 @@ __global__ void __launch_bounds__(256) skinny_part_kernel(const MatmulArgs args,
     for (int t = 0; t < MT; t++) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < G; i++) {
-      if (i >= cnt) continue;
+      if (!FULL && i >= cnt) continue;
       bf16x8 bv[2];
       uint32_t ex[4];
-      if (FMT != BT_BF16)
+      if (FMT == BT_BFP8)
 #pragma unroll
-        for (int k = 0; k < 4; k++) ex[k] = (uint32_t)__shfl((int)ew[r][i], 4 * g + k, 64);
+        for (int k = 0; k < 4; k++) ex[k] = (uint32_t)__shfl((int)ew[r][i][0], 4 * g + k, 64);
       if (FMT == BT_BF16) {
         const uint4 lo = make_uint4(bq[r][i][0], bq[r][i][1], bq[r][i][2], bq[r][i][3]);
         const uint4 hi = make_uint4(bq[r][i][4], bq[r][i][5], bq[r][i][6], bq[r][i][7]);
@@ -1169,8 +1186,8 @@ __global__ void __launch_bounds__(256) skinny_part_kernel(const MatmulArgs args,
         bv[0] = q8_to_bf16<true>(make_uint2(bq[r][i][0], bq[r][i][1]), make_uint2(ex[0], ex[1]));
         bv[1] = q8_to_bf16<true>(make_uint2(bq[r][i][2], bq[r][i][3]), make_uint2(ex[2], ex[3]));
       } else {
-        bv[0] = q4_to_bf16_scaled(bq[r][i][0], make_uint2(ex[0], ex[1]));
-        bv[1] = q4_to_bf16_scaled(bq[r][i][1], make_uint2(ex[2], ex[3]));
+        bv[0] = q4_to_bf16_gaps(bq[r][i][0], ew[r][i][0] ^ 0x7F7F7F7Fu, ew[r][i][1] ^ 0x7F7F7F7Fu);
+        bv[1] = q4_to_bf16_gaps(bq[r][i][1], ew[r][i][2] ^ 0x7F7F7F7Fu, ew[r][i][3] ^ 0x7F7F7F7Fu);
       }
 #pragma unroll
       for (int t = 0; t < MT; t++) {
@@ -1925,7 +1942,10 @@ static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bo
 template <int FMT, int MT>
 static void launch_part_m(const MatmulArgs &args, int g, int groups, int splits, float *part, hipStream_t s) {
   const unsigned blocks = (unsigned)(groups * splits);
-  if (g == 16) skinny_part_kernel<FMT, MT, 1, 16><<<blocks, 256, 0, s>>>(args, groups, part);
+  const bool full = args.chunks % g == 0;  // every split whole: no chunk tests
+  if (g == 16 && full) skinny_part_kernel<FMT, MT, 1, 16, true><<<blocks, 256, 0, s>>>(args, groups, part);
+  else if (g == 16) skinny_part_kernel<FMT, MT, 1, 16><<<blocks, 256, 0, s>>>(args, groups, part);
+  else if (full) skinny_part_kernel<FMT, MT, 1, 8, true><<<blocks, 256, 0, s>>>(args, groups, part);
   else skinny_part_kernel<FMT, MT, 1, 8><<<blocks, 256, 0, s>>>(args, groups, part);
 }
 static bool launch_parts(Runtime *r, const MatmulArgs &args, int fmt, bool swi) {

@@ -554,6 +554,13 @@ class Tensor:
     out.lead = x.lead
     if x.dtype in BFP:
       e, v = x._bfp_whole()._bfp_planes()
+      if self.rt.recording is None:  # a matmul reads exponents in a narrower range than a block float can hold
+        bad = Storage(self.rt, 4)
+        self.rt.run("range", "bfp_range", _lib.DTYPES[x.dtype], e, v, x.batch, x.rows, x.cols, bad.addr)
+        n = int.from_bytes(self.rt.download(bad.addr, 4), "little")
+        if n:
+          raise ValueError(f"{n} runs of this {x.dtype} tensor hold values under an exponent outside "
+                           f"{'5..255' if x.dtype == 'bfp8' else '3..247'}, which a matmul can't multiply exactly")
       self.rt.run("columns", "bfp_columns", _lib.DTYPES[x.dtype], e, v, x.batch, x.rows, x.cols, out.storage.addr,
                   reads=_bytes(x))
     else:

@@ -4,7 +4,9 @@ The headline is the decode GEMV on block-float weights: one 
 x [B, 576] @ W [576, 49152] with W packed as bfp4 (B = 1) or bfp8, fp32 accumulation and a bf16 result. Inputs are
 resident in HBM before timing starts. Each step reads a different copy of W from a pool larger than the 256 MB
 Infinity Cache, so every step streams its weights from HBM. Steps are captured into one HIP graph and replayed, and
-HIP events on the runtime's stream bracket the timed replay. `value` is the achieved HBM bandwidth of the headline
+HIP events on the runtime's stream bracket the timed replay. The pool holds 1 GiB of copies, four times the Infinity
+Cache, and every launch takes the next copy in a cursor that runs on across the warmup and timed graphs, so a timed
+launch reads a copy last touched more than 600 MB of traffic earlier, whatever --steps is. `value` is the achieved HBM bandwidth of the headline
 configuration: the algorithmic bytes of one step (packed W, x and the output) over the measured time per step. The
 other five GEMV configurations (bfp4 and bfp8 at B = 1, 4, 16) are in "configs".
 
@@ -29,7 +31,7 @@ if ROOT not in sys.path: sys.path.insert(0, ROOT)
 
 K_DIM, N_DIM = 576, 49152
 PEAK_GBS = 8000.0  # MI355X HBM3E
-POOL_BYTES = 320 << 20  # > 256 MB Infinity Cache
+POOL_BYTES = 1 << 30  # four times the 256 MB Infinity Cache
 
 
 def step_bytes(fmt, rows):
@@ -46,8 +48,9 @@ def log(*a):
 
 
 def gpu_leg(fmt, rows, steps, warmup):
-  """Times `steps` GEMV launches on one GPU, then a plain streaming read of the same weight bytes. Returns
-  (us per GEMV, its result, x, w, us per streaming read)."""
+  """Times `steps` GEMV launches on one GPU, then a plain streaming read of the same weight bytes, then a launch that
+  does almost nothing, each in a graph of `steps` launches. Returns (us per GEMV, its result, x, w, us per streaming
+  read, us per near-empty launch)."""
   from baretile_amd import _lib
   from baretile_amd.runtime import Runtime
   rt = Runtime()
@@ -72,6 +75,7 @@ def gpu_leg(fmt, rows, steps, warmup):
     copies = max(2, -(-POOL_BYTES // wbytes))
     pool = [rt.dram_alloc(wbytes) for _ in range(copies)]
     for p in pool: rt.run("columns", "bfp_columns", code, exps, vals, 1, K_DIM, N_DIM, p)
+    cursor = [0]  # the next copy: runs on across every graph captured here
     dx = rt.dram_alloc(xb.nbytes)
     rt.upload(dx, xb.tobytes())
     out = rt.dram_alloc(rows * N_DIM * 2)
@@ -80,18 +84,25 @@ def gpu_leg(fmt, rows, steps, warmup):
     rt.wait()
 
     def launch(i):
-      _lib.call("matmul", rt.handle, byref(a), code, pool[i % copies], 1, 1, rows, K_DIM, N_DIM, None, byref(o))
+      _lib.call("matmul", rt.handle, byref(a), code, pool[cursor[0] % copies], 1, 1, rows, K_DIM, N_DIM, None, byref(o))
+      cursor[0] += 1
 
     def timed(fn, warm):
       """us per launch of fn(i) for i < steps, captured into one graph and replayed between two events."""
       for i in range(3): fn(i)  # the first launches load the code object
       rt.wait()
-      graph = c_void_p()
-      _lib.call("graph_begin", rt.handle)
-      for i in range(steps): fn(i)
-      _lib.call("graph_end", rt.handle, byref(graph))
-      for _ in range(max(1, warm // max(1, steps)) if warm else 0): _lib.call("graph_launch", rt.handle, graph)
-      rt.wait()
+      def capture(n):
+        graph = c_void_p()
+        _lib.call("graph_begin", rt.handle)
+        for i in range(n): fn(i)
+        _lib.call("graph_end", rt.handle, byref(graph))
+        return graph
+      if warm:  # the untimed steps, in a graph of their own
+        wg = capture(min(warm, steps))
+        for _ in range(max(1, warm // min(warm, steps))): _lib.call("graph_launch", rt.handle, wg)
+        rt.wait()
+        _lib.call("graph_destroy", wg)
+      graph = capture(steps)
       start, end = c_void_p(), c_void_p()
       _lib.call("event_create", rt.handle, byref(start))
       _lib.call("event_create", rt.handle, byref(end))
@@ -111,8 +122,13 @@ def gpu_leg(fmt, rows, steps, warmup):
     got = np.frombuffer(bytes(rt.download(out, rows * N_DIM * 2)), np.uint16).reshape(rows, N_DIM)
     # the same weight bytes read by a plain streaming kernel, from the same pool: what one launch of this size can get
     word = rt.dram_alloc(256)
-    read_us = timed(lambda i: _lib.call("stream_read", rt.handle, pool[i % copies], wbytes // 16 * 16, word), steps)
-    return us, got, x, w, read_us
+    def read(i):
+      _lib.call("stream_read", rt.handle, pool[cursor[0] % copies], wbytes // 16 * 16, word)
+      cursor[0] += 1
+    read_us = timed(read, steps)
+    # the fixed cost of a launch in such a graph: a kernel that writes one word and reads nothing
+    floor_us = timed(lambda i: _lib.call("fill32", rt.handle, word, 0, 1), steps)
+    return us, got, x, w, read_us, floor_us
   finally:
     rt.close()
 
@@ -136,19 +152,32 @@ def measured_traffic():
     return None
 
 
-def cpu_leg(fmt, rows, seconds=10.0):
+def timed_cpu(fn, seconds, threads=None):
+  """(seconds per call, calls) of fn() repeated for `seconds` after one untimed call; with threads, BLAS is held to
+  that many threads meanwhile."""
+  from contextlib import nullcontext
+  try:
+    from threadpoolctl import threadpool_limits
+    limit = threadpool_limits(threads) if threads else nullcontext()
+  except ImportError:
+    limit = nullcontext()
+  with limit:
+    fn()
+    n, start = 0, time.perf_counter()
+    while time.perf_counter() - start < seconds or n < 1:
+      fn()
+      n += 1
+  return (time.perf_counter() - start) / n, n
+
+
+def cpu_leg(fmt, rows, seconds=10.0, threads=None):
   """NumPy float32 x @ Wdeq on the host (the oracle's matmul of the block-float values), W dequantized outside the
   timer. Runs whole GEMVs until `seconds` have passed."""
   from oracle import bfp as B
   rng = np.random.default_rng(0)
   x = B.bf16(rng.normal(0, 1, (rows, K_DIM))).astype(np.float32)
   w = B.bfp(rng.normal(0, 0.02, (K_DIM, N_DIM)).astype(np.float32), fmt).astype(np.float32)
-  x @ w
-  n, start = 0, time.perf_counter()
-  while time.perf_counter() - start < seconds:
-    x @ w
-    n += 1
-  per = (time.perf_counter() - start) / n
+  per, n = timed_cpu(lambda: x @ w, seconds, threads)
   return per * 1e6, n
 
 
@@ -182,7 +211,17 @@ def decode_leg(tokens=128, prompt_len=32, check=True, replay=True):
     toks, logits = llama.generate(dw, dc, prompt, tokens, size, clock=clock, replay=replay)
     first = clock[0] - start  # prefill of the prompt and the first pick
     steady = (clock[-1] - clock[2]) / (len(clock) - 3)  # replays of the recorded step (the 2nd step records)
+    # bytes a token reads: every bfp8 linear and the tied head, the norms, one embedding row, and the keys and values of
+    # the positions it attends to (the cache holds prompt_len + step rows at step)
+    wb = 30 * (576 * 960 + 576 * 576 + 576 * 3072 + 1536 * 576) * 1088 // 1024 + 576 * 49152 * 1088 // 1024
+    ctx = prompt_len + (tokens - 1) / 2
+    per_token = wb + 61 * 576 * 2 + 576 * 2 + int(30 * 2 * 3 * 64 * 2 * ctx)
     out = {"tok/s": round((len(clock) - 1) / (clock[-1] - clock[0]), 1), "steady_tok/s": round(1 / steady, 1),
+           "roofline": {"bound": "hbm", "bytes_per_token": per_token, "unit": "GB/s",
+                        "achieved": round(per_token / steady / 1e9, 1), "peak": PEAK_GBS,
+                        "frac": round(per_token / steady / 1e9 / PEAK_GBS, 4),
+                        "note": "the weights fit the 256 MB Infinity Cache, so this bound is loose: the step is "
+                                "launch- and latency-bound"},
            "ms_per_token": round(1000 * (clock[-1] - clock[0]) / (len(clock) - 1), 4),
            "prefill_ms": round(1000 * first, 3), "tokens": tokens, "prompt": prompt_len, "graph_replay": replay,
            "kernels_per_token": None}
@@ -421,41 +460,61 @@ def attention_leg(check=True):
       reps += 1
     per = (time.perf_counter() - t0) / reps
     nbytes = 2 * 8 * 4096 * 128 * 2 + 2 * 32 * 128 * 2
+    # and the causal prefill, on one key head's 4 query heads (an eighth of the 2048-row case)
+    qp = rng.standard_normal((4, 2048, 128)).astype(np.float32)
+    kp, vp = rng.standard_normal((1, 2048, 128)).astype(np.float32), rng.standard_normal((1, 2048, 128)).astype(np.float32)
+    plp = np.broadcast_to(np.arange(2048)[None, :, None], (4, 2048, 1))
+    pper, preps = timed_cpu(lambda: ops.attention(qp, kp, vp, plp, 0, 4), 3.0)
+    pflops = 4 * 4 * 128 * 2048 * 2049 // 2
     cpu = {"value": round(nbytes / per / 1e9, 3), "unit": "GB/s", "cores": blas_threads()[0], "kind": "port",
            "sample": f"{reps} calls of the oracle's attention (NumPy float64) at decode, 4096 keys, batch 1: "
-           f"{per * 1e3:.1f} ms each"}
+           f"{per * 1e3:.1f} ms each", "host_cpus": os.cpu_count(),
+           "prefill": {"value": round(pflops / pper / 1e12, 5), "unit": "TFLOP/s",
+                       "sample": f"{preps} calls of the oracle's causal attention over 2048 rows for one key head and its "
+                       f"4 query heads (an eighth of config 4's prefill), {pper:.2f} s each"}}
   return res, cpu
 
 
-def layer_leg(check=True):
+def layer_leg(check=True, cpu_seconds=10.0):
   """one Llama-3-8B-shaped block (4096 wide, 32 query and 8 key heads of 128, SwiGLU 14336) with
   every projection N(0, 0.02) in bfp4 and bf16 norms: a 2048-token prefill from position 0 (matrix-core bound;
   flops 2 * 2048 * 218,103,808 for the projections plus the causal attention), then one batch-32 decode step, each
   slot at position 4095 of its own 4096-row bf16 cache (HBM-bound: the 122,683,392 bytes of bfp4 weights plus
-  32 * 4096 * 8 * 128 * 2 * 2 bytes of K and V)."""
+  32 * 4096 * 8 * 128 * 2 * 2 bytes of K and V).
+
+  Parity: the oracle's layer (oracle/llama_ref.layer) on the same block floats (read back from the device) for key
+  rows of the prefill and key slots of the decode step, within the reference's 3% of the block's change to x
+  (test_models.py:818-833). CPU baseline: the oracle's layer timed on the host, a prefill of 128 tokens and one slot's
+  decode token."""
   from baretile_amd.models import llama
   from baretile_amd.runtime import Runtime
   from baretile_amd.tensor import Tensor
+  from oracle import bfp as B, llama_ref as L
   dim, heads, kv, hd, ffn, size, tokens, slots = 4096, 32, 8, 128, 14336, 4096, 2048, 32
   rng = np.random.default_rng(0)
   rt = Runtime()
-  res = {}
+  res, cpu = {}, None
   try:
     c = llama.model(dim=dim, heads=heads, kv=kv, layers=1, eps=1e-5, theta=500000.0, ffn=ffn, head_dim=hd)
     c.precision = {(op, 0): ("bfp4", 4) for op in ("qkv", "o", "gate_up", "down")}
+    rc = L.model(dim=dim, heads=heads, kv=kv, layers=1, eps=1e-5, theta=500000.0, ffn=ffn, head_dim=hd)
     shapes = {"qkv_proj": (dim, (heads + 2 * kv) * hd), "o_proj": (heads * hd, dim), "gate_up_proj": (dim, 2 * ffn),
               "down_proj": (ffn, dim)}
-    w = {}
+    w, ref = {}, {}
     for name, shape in shapes.items():
-      w[f"layers.0.{name}"] = Tensor.of(rt, rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)).cast("bfp4").columns()
+      t = Tensor.of(rt, rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)).cast("bfp4").columns()
+      w[f"layers.0.{name}"] = t
+      if check: ref[name] = B.bf16_floats(np.frombuffer(t.tobytes(), np.uint16).reshape(shape))
     for name in ("input_layernorm", "post_attention_layernorm"):
-      w[f"layers.0.{name}"] = Tensor.of(rt, rng.normal(1, 0.1, (1, dim)).astype(np.float32))
+      n = B.bf16(rng.normal(1, 0.1, (1, dim)))
+      w[f"layers.0.{name}"], ref[name] = Tensor.of(rt, n), n
     cos, sin, turn = llama.rotary(c, size)
     w["cos"], w["sin"], w["turn"] = Tensor.of(rt, cos), Tensor.of(rt, sin), Tensor.of(rt, turn).columns()
     p = llama.block(w, 0)
     wbytes = sum(shape[0] * shape[1] for shape in shapes.values()) * 576 // 1024
     # prefill
-    x = Tensor.of(rt, rng.standard_normal((1, tokens, dim), dtype=np.float32), "fp32")
+    xh = rng.standard_normal((tokens, dim), dtype=np.float32)
+    x = Tensor.of(rt, xh[None], "fp32")
     cache = Tensor.zeros(rt, size, hd, batch=2 * kv)
     places = Tensor.of(rt, [list(range(tokens))], "int32")
     rot = (w["cos"].gather(places), w["sin"].gather(places), w["turn"])
@@ -469,15 +528,28 @@ def layer_leg(check=True):
     eager = (time.perf_counter() - t0) / reps * 1e6
     us, y = replay_us(rt, run, 5)
     flops = 2 * tokens * sum(a * b for a, b in shapes.values()) + 4 * heads * hd * tokens * (tokens + 1) // 2
-    res["prefill_2048"] = {"us": round(us, 1), "TFLOP/s": round(flops / us / 1e6, 1),
-                           "frac_mfma_peak": round(flops / us / 1e6 / 2500.0, 4), "flops": flops,
-                           "eager_us": round(eager, 1), "finite": bool(np.isfinite(np.frombuffer(y, np.float32)).all())}
-    log("layer prefill", res["prefill_2048"])
+    entry = {"us": round(us, 1), "TFLOP/s": round(flops / us / 1e6, 1),
+             "frac_mfma_peak": round(flops / us / 1e6 / 2500.0, 4), "flops": flops, "eager_us": round(eager, 1)}
+    if check:  # key rows against the oracle's layer, which still computes every row's keys and values
+      rows = [0, 1, 255, 1024, 2047]
+      got = np.frombuffer(y, np.float32).reshape(tokens, dim)[rows]
+      mask = np.where(np.arange(tokens) > np.arange(tokens)[:, None], np.float32(-1e9), np.float32(0))
+      t0 = time.perf_counter()
+      want = L.layer(xh, ref, rc, (cos[:tokens], sin[:tokens], turn), mask, np.zeros((2 * kv, tokens, hd)),
+                     range(tokens), only=rows)
+      log("layer prefill oracle rows in", round(time.perf_counter() - t0, 1), "s")
+      change, err = np.abs(want - xh[rows]).max(), np.abs(got - want).max()
+      entry.update({"parity": bool(err < 0.03 * change), "parity_rows": rows, "max_err_over_change": round(float(err / change), 5)})
+    res["prefill_2048"] = entry
+    log("layer prefill", entry)
     del y, cache
     # batch-32 decode at position 4095 of each slot's cache
-    keys = Tensor.of(rt, rng.standard_normal((slots * kv, size, hd), dtype=np.float32))
-    values = Tensor.of(rt, rng.standard_normal((slots * kv, size, hd), dtype=np.float32))
-    xs = Tensor.of(rt, rng.standard_normal((1, slots, dim), dtype=np.float32), "fp32")
+    K = B.bf16(rng.standard_normal((slots * kv, size, hd), dtype=np.float32))
+    V = B.bf16(rng.standard_normal((slots * kv, size, hd), dtype=np.float32))
+    K[:, size - 1:], V[:, size - 1:] = 0, 0
+    keys, values = Tensor.of(rt, K), Tensor.of(rt, V)
+    xs_h = rng.standard_normal((slots, dim), dtype=np.float32)
+    xs = Tensor.of(rt, xs_h[None], "fp32")
     at = Tensor.of(rt, [[size - 1] * slots], "int32")
     rot = (w["cos"].gather(at), w["sin"].gather(at), w["turn"])
     place = Tensor.of(rt, [[size - 1]], "int32")
@@ -490,14 +562,39 @@ def layer_leg(check=True):
     eager = (time.perf_counter() - t0) / reps * 1e6
     us, y = replay_us(rt, step, 20)
     nbytes = wbytes + slots * size * kv * hd * 2 * 2
-    res["decode_B32_ctx4096"] = {"us": round(us, 1), "GB/s": round(nbytes / us / 1e3, 1),
-                                 "frac_hbm_peak": round(nbytes / us / 1e3 / PEAK_GBS, 4), "bytes": nbytes,
-                                 "tok/s": round(slots / us * 1e6, 1), "eager_us": round(eager, 1),
-                                 "finite": bool(np.isfinite(np.frombuffer(y, np.float32)).all())}
-    log("layer decode", res["decode_B32_ctx4096"])
+    entry = {"us": round(us, 1), "GB/s": round(nbytes / us / 1e3, 1), "frac_hbm_peak": round(nbytes / us / 1e3 / PEAK_GBS, 4),
+             "bytes": nbytes, "tok/s": round(slots / us * 1e6, 1), "eager_us": round(eager, 1)}
+    if check:  # key slots against the oracle's layer run on each slot alone
+      got = np.frombuffer(y, np.float32).reshape(slots, dim)
+      worst, sl = 0.0, [0, 13, 31]
+      for s_ in sl:
+        cache_s = np.concatenate([K[s_ * kv:(s_ + 1) * kv], V[s_ * kv:(s_ + 1) * kv]]).astype(np.float64)
+        want = L.layer(xs_h[s_:s_ + 1], ref, rc, (cos[[size - 1]], sin[[size - 1]], turn), np.zeros((1, size), np.float32),
+                       cache_s, [size - 1])[0]
+        worst = max(worst, float(np.abs(got[s_] - want).max() / np.abs(want - xs_h[s_]).max()))
+      entry.update({"parity": worst < 0.03, "parity_slots": sl, "max_err_over_change": round(worst, 5)})
+    res["decode_B32_ctx4096"] = entry
+    log("layer decode", entry)
+    if check:  # the oracle's layer on the host: a 128-token prefill, and one slot's decode token
+      n = 128
+      mask = np.where(np.arange(n) > np.arange(n)[:, None], np.float32(-1e9), np.float32(0))
+      per, reps = timed_cpu(lambda: L.layer(xh[:n], ref, rc, (cos[:n], sin[:n], turn), mask,
+                                            np.zeros((2 * kv, n, hd)), range(n)), cpu_seconds / 2)
+      pflops = 2 * n * sum(a * b for a, b in shapes.values()) + 4 * heads * hd * n * (n + 1) // 2
+      cache_s = np.concatenate([K[:kv], V[:kv]]).astype(np.float64)
+      dper, dreps = timed_cpu(lambda: L.layer(xs_h[:1], ref, rc, (cos[[size - 1]], sin[[size - 1]], turn),
+                                              np.zeros((1, size), np.float32), cache_s, [size - 1]), cpu_seconds / 2)
+      dbytes = wbytes + size * kv * hd * 2 * 2
+      threads, api = blas_threads()
+      cpu = {"value": round(dbytes / dper / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+             "sample": f"the oracle's layer for one slot's decode token at position 4095 ({dreps} runs, {dper * 1e3:.0f} "
+             f"ms each; bytes counted as the GPU figure counts one slot's: bfp4 weights plus its K and V), NumPy "
+             f"float32/float64 ({api} BLAS)", "host_cpus": os.cpu_count(),
+             "prefill": {"value": round(pflops / per / 1e12, 4), "unit": "TFLOP/s",
+                         "sample": f"the oracle's layer on a 128-token prefill, {reps} runs, {per:.2f} s each"}}
   finally:
     rt.close()
-  return res
+  return res, cpu
 
 
 def blas_threads():
@@ -531,7 +628,7 @@ def main():
     for rows in (1, 4, 16):
       if args.only and args.only != f"{fmt}_B{rows}" and args.only != "gemv": continue
       steps = args.steps if (fmt, rows) == ("bfp4", 1) else max(50, args.steps // 4)
-      us, got, x, w, read_us = gpu_leg(fmt, rows, steps, args.warmup if (fmt, rows) == ("bfp4", 1) else steps)
+      us, got, x, w, read_us, floor_us = gpu_leg(fmt, rows, steps, args.warmup if (fmt, rows) == ("bfp4", 1) else steps)
       ok = check(got, x, w, fmt)
       gbs = step_bytes(fmt, rows) / us / 1e3
       wb = weight_bytes(fmt)
@@ -539,7 +636,8 @@ def main():
                                    "frac_hbm_peak": round(gbs / PEAK_GBS, 4), "bytes": step_bytes(fmt, rows),
                                    "steps": steps, "parity": ok,
                                    "stream_read_us": round(read_us, 3), "stream_read_GB/s": round(wb / read_us / 1e3, 1),
-                                   "frac_of_stream_read": round(read_us / us, 4)}
+                                   "frac_of_stream_read": round(read_us / us, 4),
+                                   "launch_floor_us": round(floor_us, 3)}
       log(fmt, rows, configs[f"{fmt}_B{rows}"])
   extra = {}
   if args.only in (None, "c1"):
@@ -548,7 +646,7 @@ def main():
   if args.only in (None, "attention"):
     extra["attention"], extra["attention_cpu_baseline"] = attention_leg(check=not args.no_cpu)
   if args.only in (None, "layer"):
-    extra["layer"] = layer_leg(check=not args.no_cpu)
+    extra["layer"], extra["layer_cpu_baseline"] = layer_leg(check=not args.no_cpu, cpu_seconds=args.cpu_seconds)
   if not args.no_decode and args.only in (None, "decode"):
     extra["decode"], extra["decode_cpu_baseline"] = decode_leg(check=not args.no_cpu, replay=not args.eager)
     log("decode", extra["decode"])
@@ -559,10 +657,13 @@ def main():
   cpu = None
   if not args.no_cpu:
     us_cpu, n = cpu_leg("bfp4", 1, args.cpu_seconds)
+    us_one, n_one = cpu_leg("bfp4", 1, min(3.0, args.cpu_seconds), threads=1)
     threads, api = blas_threads()
     cpu = {"value": round(step_bytes("bfp4", 1) / us_cpu / 1e3, 3), "unit": "GB/s", "cores": threads,
            "kind": "port", "sample": f"{n} whole GEMVs x[1,576] @ W[576,49152] (bfp4 values dequantized to float32 "
-           f"outside the timer) with NumPy float32 ({api} BLAS), {us_cpu:.0f} us each"}
+           f"outside the timer) with NumPy float32 ({api} BLAS), {us_cpu:.0f} us each",
+           "host_cpus": os.cpu_count(), "one_thread": {"value": round(step_bytes("bfp4", 1) / us_one / 1e3, 3),
+                                                       "cores": 1, "sample": f"{n_one} GEMVs, {us_one:.0f} us each"}}
   line = {
     "metric": "bfp4/bfp8 GEMV HBM GB/s (%peak); decode tok/s, SmolLM-135M shape, 1 GPU",
     "value": head["GB/s"], "unit": "GB/s", "n_gpus": 1, "steps": head["steps"], "warmup": args.warmup,

@@ -91,8 +91,8 @@ int bt_stream(bt_runtime *rt, void **stream);
  * bfp4 tiles are 64 + 512: lane l's 8 bytes at 64 + 8l, 4 bytes a half h holding its values j = 0..7 as sign and
  * magnitude: for j < 4 byte j's bit 7 and bits 0-2, for j >= 4 bits 4-6 of byte j - 4 and bit 3 of byte
  * (j - 3) % 4. bf16 tiles are 2048 bytes (32 bytes at 32l, no exponents). Rows past K and columns
- * past N are zero. A matmul reads exponents as signed bytes, so it takes block floats whose run exponents e lie in
- * 5..255 (bfp8) or 0..247 (bfp4); readback is exact for any. */
+ * past N are zero. A matmul reads exponents as signed bytes, so it takes block floats whose nonzero runs' exponents e
+ * lie in 5..255 (bfp8) or 3..247 (bfp4) (bt_bfp_range counts the others); readback is exact for any. */
 
 /* bf16 (round to nearest even first, as gpt2.bfp does: models/gpt2.py:19-30) or fp32 matrices -> plain planes.
  * src strides are in elements. */
@@ -104,6 +104,12 @@ int bt_bfp_unpack(bt_runtime *rt, int fmt, uint64_t exps, uint64_t vals, int64_t
 /* plain planes -> columns tiles (Tensor.columns, tensor.py:597-611). */
 int bt_bfp_columns(bt_runtime *rt, int fmt, uint64_t exps, uint64_t vals, int64_t batch, int64_t rows, int64_t cols,
                    uint64_t dst);
+/* The number of runs of a plain block float that a matmul can't multiply, written to the uint32 at `bad` (no
+ * counterpart in the reference, whose unpacker reads any exponent): runs with a nonzero value whose exponent lies
+ * outside 5..255 (bfp8) or 3..247 (bfp4), the range the matmul kernels read exponents in. Tensor.columns() checks it
+ * before a block float becomes a matmul's B. */
+int bt_bfp_range(bt_runtime *rt, int fmt, uint64_t exps, uint64_t vals, int64_t batch, int64_t rows, int64_t cols,
+                 uint64_t bad);
 /* bf16 matrices with any strides -> bf16 columns tiles (a matmul's B read as it is, or transposed by strides). */
 int bt_bf16_columns(bt_runtime *rt, uint64_t src, int64_t batch, int64_t rows, int64_t cols, int64_t sb, int64_t sr,
                     int64_t sc, uint64_t dst);

@@ -111,8 +111,11 @@ def test_jit_with_block_float_and_written_inputs(rt):
     want = np.zeros((16, 32), np.float32)
     want[[i, 5 + i]] = rows
     assert np.array_equal(value(cache)[0], want), i
-  with pytest.raises(ValueError):
-    jit(lambda w: x @ w)(Tensor.of(rt, rng.normal(0, 1, (2, 64, 32)).tolist()).cast("bfp8")[0])
+  # a view of a larger block float can't be copied byte for byte into the recording's input (the first call runs
+  # eagerly; the second, which records, refuses it)
+  g, pair = jit(lambda w: x @ w), Tensor.of(rt, rng.normal(0, 1, (2, 64, 32)).tolist()).cast("bfp8")
+  g(pair[1])
+  with pytest.raises(ValueError, match="whole tensor"): g(pair[1])
 
 
 def test_wait_times_out_and_the_stream_drains(rt):
@@ -160,3 +163,20 @@ def test_profile_reports_time_and_bytes(chip):
     assert list(rows) == [r[0] for r in sorted(rt.profile(base), key=lambda r: -r[2])]
   finally:
     rt.close()
+
+
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4"])
+def test_matmul_refuses_exponents_it_cannot_read(rt, fmt):
+  # a run whose exponent the matmul kernels can't read (bfp8: a top exponent field of 1, the smallest normal bf16;
+  # bfp4: 248, values near 2^121) makes columns() raise instead of multiplying wrong; a run of zeros under exponent 0
+  # is fine, and readback stays exact either way
+  a = np.full((64, 32), 0.5, np.float32)
+  a[3, :16] = 2.0 ** -126 if fmt == "bfp8" else 2.0 ** 121
+  a[9, 16:] = 0
+  w = Tensor.of(rt, a.tolist()).cast(fmt)
+  assert np.array_equal(value(w)[0], B.bfp(a, fmt))
+  with pytest.raises(ValueError, match="exponent"): w.columns()
+  with pytest.raises(ValueError, match="exponent"): (Tensor.of(rt, np.ones((2, 64)).tolist()) @ w).realize()
+  a[3, :16] = 1.0
+  w = Tensor.of(rt, a.tolist()).cast(fmt).columns()
+  assert np.array_equal(value(Tensor.of(rt, np.eye(64).tolist()) @ w)[0], B.bfp(a, fmt))
