@@ -15,6 +15,7 @@
 //   B-side scaling (more rows): each weight gets its power of two with v_ldexp_f32, reading the biased exponent byte
 //     straight from the tile.
 #include "program.h"
+#include <cstdlib>
 
 namespace bt {
 
@@ -1233,6 +1234,155 @@ __global__ void __launch_bounds__(256) parts_reduce_kernel(const MatmulArgs args
   }
 }
 
+// 5 to 32 rows of one A (K a multiple of 512) against B streamed once. Block (group, split) takes 4 runs of B, a wave
+// each, over its split's stages of 8 chunks (512 rows of K). A's rows for a stage go into one half of a two-stage LDS
+// ring by direct loads while the other half is multiplied, and each wave's weights for the next stage are in flight
+// while it multiplies this one, so a block covers any length of K with the same LDS. Every run sums its chunks in the
+// same order as the other kernels (a chunk's lower 32 rows, then its upper 32), in one accumulator over the split.
+// EPI 0 writes fp32 partial tiles for parts_reduce_kernel (more than one split); 1 stores through the matmul's
+// epilogue (one split); 2 is SiLU x up (one split): waves 0 and 1 take gate runs 2j and 2j + 1, waves 2 and 3 the up
+// runs at the same columns of the other half, and the up tiles reach the gate waves through LDS.
+template <int FMT, int MT, int EPI, int DT>
+__global__ void __launch_bounds__(256) skinny_stream_kernel(const MatmulArgs args, int groups, int stages, float *part) {
+  constexpr int C = 8, TB = Tile<FMT>::bytes, KP = C * 64 + 8, ROWS = 16 * MT, APW = ROWS / 4;
+  constexpr int NQ = FMT == BT_BF16 ? 8 : FMT == BT_BFP8 ? 4 : 2, NE = FMT == BT_BFP4 ? 4 : 1;
+  constexpr int LOADS = APW + 2 * C;  // loads a wave issues for one stage, A's and its weights'
+  __shared__ __attribute__((aligned(16))) uint16_t la[2][ROWS * KP];
+  const Head h = early_head(args);
+  const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
+  const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = (int)blockIdx.x % groups, sp = (int)blockIdx.x / groups;
+  const int run = EPI == 2 ? (wib < 2 ? 0 : h.nruns / 2) + 2 * grp + (wib & 1) : grp * 4 + wib;
+  const bool in = run < h.nruns;
+  const int first = sp * stages * C;  // the split's first chunk
+  const uint32_t abytes = (uint32_t)(((int64_t)(h.m - 1) * h.a.sr + h.k) * 2);
+  const i32x4 ar = buffer_words((const void *)h.a.ptr, abytes);
+  const __amdgpu_buffer_rsrc_t tr =
+      buffer(h.b + (int64_t)(in ? run : 0) * h.chunks * TB, in ? (uint32_t)h.chunks * TB : 0u);
+  uint32_t bq[2][C][NQ], ew[2][C][NE];
+  // stage st: A's rows (a row's 1 KB a load, the block's waves in turn; rows past the last read zeros), and the wave's
+  // 8 chunks of weights
+  auto issue = [&](int st, uint16_t *buf, uint32_t(&q)[C][NQ], uint32_t(&e)[C][NE]) {
+    const int c0 = first + st * C;
+#pragma unroll
+    for (int j = 0; j < APW; j++) {
+      const int r = wib + 4 * j;
+      const uint32_t voff = r < h.m ? (uint32_t)(((int64_t)r * h.a.sr + (int64_t)c0 * 64) * 2) + 16u * lane : abytes;
+      lds_load16(ar, voff, buf + r * KP);
+    }
+#pragma unroll
+    for (int i = 0; i < C; i++) {
+      const uint32_t at = (uint32_t)(c0 + i) * TB;
+      if (FMT == BT_BF16) {
+        const auto lo = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 32 * lane, 0, 0);
+        const auto hi = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 32 * lane + 16, 0, 0);
+#pragma unroll
+        for (int w = 0; w < 4; w++) q[i][w] = lo[w], q[i][4 + w] = hi[w];
+      } else if (FMT == BT_BFP8) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 64 + 16 * lane, 0, 0);
+#pragma unroll
+        for (int w = 0; w < 4; w++) q[i][w] = v[w];
+        e[i][0] = __builtin_amdgcn_raw_buffer_load_b32(tr, at + 4 * col, 0, 0);
+      } else {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(tr, at + 64 + 8 * lane, 0, 0);
+        q[i][0] = v[0], q[i][1] = v[1];
+        const auto x = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 16 * g, 0, 0);
+#pragma unroll
+        for (int w = 0; w < 4; w++) e[i][w] = x[w];
+      }
+    }
+  };
+  f32x4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; t++) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto multiply = [&](const uint16_t *buf, const uint32_t(&q)[C][NQ], const uint32_t(&e)[C][NE]) {
+#pragma unroll
+    for (int i = 0; i < C; i++) {
+      bf16x8 bv[2];
+      if (FMT == BT_BF16) {
+        const uint4 lo = make_uint4(q[i][0], q[i][1], q[i][2], q[i][3]), hi = make_uint4(q[i][4], q[i][5], q[i][6], q[i][7]);
+        bv[0] = *(const bf16x8 *)&lo;
+        bv[1] = *(const bf16x8 *)&hi;
+      } else if (FMT == BT_BFP8) {
+        uint32_t ex[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) ex[k] = (uint32_t)__shfl((int)e[i][0], 4 * g + k, 64);
+        bv[0] = q8_to_bf16<true>(make_uint2(q[i][0], q[i][1]), make_uint2(ex[0], ex[1]));
+        bv[1] = q8_to_bf16<true>(make_uint2(q[i][2], q[i][3]), make_uint2(ex[2], ex[3]));
+      } else {
+        bv[0] = q4_to_bf16_gaps(q[i][0], e[i][0] ^ 0x7F7F7F7Fu, e[i][1] ^ 0x7F7F7F7Fu);
+        bv[1] = q4_to_bf16_gaps(q[i][1], e[i][2] ^ 0x7F7F7F7Fu, e[i][3] ^ 0x7F7F7F7Fu);
+      }
+#pragma unroll
+      for (int t = 0; t < MT; t++) {
+        const uint16_t *at = buf + (16 * t + col) * KP + 64 * i + 8 * g;
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)at, bv[0], acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)(at + 32), bv[1], acc[t], 0, 0, 0);
+      }
+    }
+  };
+  // stage st is multiplied from ring half st % 2 while stage st + 1 loads into the other; loads complete in order, so
+  // with the next stage's LOADS issued, at most LOADS outstanding means this stage's have all landed
+  issue(0, la[0], bq[0], ew[0]);
+  for (int st = 0; st < stages; st += 2) {
+    if (st + 1 < stages) {
+      issue(st + 1, la[1], bq[1], ew[1]);
+      wait_vm<LOADS>();
+    } else {
+      wait_vm<0>();
+    }
+    __syncthreads();
+    multiply(la[0], bq[0], ew[0]);
+    __syncthreads();
+    if (st + 1 >= stages) break;
+    if (st + 2 < stages) {
+      issue(st + 2, la[0], bq[0], ew[0]);
+      wait_vm<LOADS>();
+    } else {
+      wait_vm<0>();
+    }
+    __syncthreads();
+    multiply(la[1], bq[1], ew[1]);
+    __syncthreads();
+  }
+  if constexpr (EPI == 0) {
+    const int n = run * 16 + col;
+    if (n >= h.n) return;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int m = 16 * t + 4 * g + i;
+        if (m < h.m) part[((int64_t)sp * ROWS + m) * h.n + n] = acc[t][i];
+      }
+  } else if constexpr (EPI == 1) {
+    if (!in) return;
+#pragma unroll
+    for (int t = 0; t < MT; t++) store_tile<DT>(args, h, acc[t], 0, t, run, g, col);
+  } else {
+    float *up = (float *)&la[0][0];  // free after the last barrier: the up waves' tiles, for the gate waves
+    if (wib >= 2)
+#pragma unroll
+      for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) up[(((wib - 2) * MT + t) * 4 + i) * 64 + lane] = acc[t][i];
+    __syncthreads();
+    if (wib >= 2) return;
+    const int n = (2 * grp + wib) * 16 + col;  // the gate column, and the output's
+    const bt_operand &out = h.out;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int m = 16 * t + 4 * g + i;
+        if (m >= h.m) continue;
+        const float gv = bf16_value(bf16_packed(acc[t][i]));
+        const float uv = bf16_value(bf16_packed(up[((wib * MT + t) * 4 + i) * 64 + lane]));
+        ((uint16_t *)out.ptr)[(int64_t)m * out.sr + n] = (uint16_t)bf16_packed(gv / (1.0f + expf(-gv)) * uv);
+      }
+  }
+}
+
 template <int FMT, int DT, int WM, int WN, int S>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gemm2_kernel(const MatmulArgs args, int mblocks, int nblocks) {
@@ -1976,6 +2126,55 @@ static bool launch_parts(Runtime *r, const MatmulArgs &args, int fmt, bool swi) 
   return true;
 }
 
+// The streaming kernels for 5 to 32 rows of one A with K a multiple of 512: false when the product doesn't fit them
+// (then the split-K or one-launch kernels run it). With at least 256 groups of 4 runs, one split whose epilogue
+// stores the result; otherwise splits of whole stages, as many as bring the grid nearest 512 blocks, summed by
+// parts_reduce_kernel in split order. SiLU x up needs the gate and up halves to split into pairs of runs.
+template <int FMT, int MT>
+static void launch_stream_m(const MatmulArgs &args, int epi, int dt, int groups, int splits, int stages, float *part,
+                            hipStream_t s) {
+  const unsigned blocks = (unsigned)(groups * splits);
+  if (epi == 0) skinny_stream_kernel<FMT, MT, 0, BT_FP32><<<blocks, 256, 0, s>>>(args, groups, stages, part);
+  else if (epi == 2) skinny_stream_kernel<FMT, MT, 2, BT_BF16><<<blocks, 256, 0, s>>>(args, groups, stages, part);
+  else if (dt == BT_FP32) skinny_stream_kernel<FMT, MT, 1, BT_FP32><<<blocks, 256, 0, s>>>(args, groups, stages, part);
+  else skinny_stream_kernel<FMT, MT, 1, BT_BF16><<<blocks, 256, 0, s>>>(args, groups, stages, part);
+}
+static bool launch_stream(Runtime *r, const MatmulArgs &args, int fmt, bool swi) {
+  const bt_operand &a = args.a;
+  if (args.batch != 1 || args.m < 5 || args.m > 32 || args.k % 512 || a.sc != 1 || a.ptr % 16 || a.sr % 8 ||
+      ((int64_t)(args.m - 1) * a.sr + args.k) * 2 >= (1ll << 32) ||
+      (int64_t)args.chunks * Tile<BT_BF16>::bytes >= (1ll << 32) || (swi && args.nruns % 4))
+    return false;
+  const int mt = args.m > 16 ? 2 : 1, total = args.chunks / 8;
+  const int groups = swi ? args.nruns / 4 : (args.nruns + 3) / 4;
+  int splits = 1;
+  if (groups < 256) {  // the divisor of the stages that brings groups * splits nearest 512
+    for (int d = 1; d <= total; d++)
+      if (total % d == 0 && std::abs(groups * d - 512) < std::abs(groups * splits - 512)) splits = d;
+  }
+  float *part = nullptr;
+  if (splits > 1) {
+    part = (float *)runtime_scratch(r, (size_t)splits * 16 * mt * args.n * 4);
+    if (!part) return false;
+  }
+  const int epi = splits > 1 ? 0 : swi ? 2 : 1, dt = args.prog.dtype == BT_FP32 ? BT_FP32 : BT_BF16;
+  const int stages = total / splits;
+  if (fmt == BT_BF16 && mt == 2) launch_stream_m<BT_BF16, 2>(args, epi, dt, groups, splits, stages, part, r->stream);
+  else if (fmt == BT_BF16) launch_stream_m<BT_BF16, 1>(args, epi, dt, groups, splits, stages, part, r->stream);
+  else if (fmt == BT_BFP8 && mt == 2) launch_stream_m<BT_BFP8, 2>(args, epi, dt, groups, splits, stages, part, r->stream);
+  else if (fmt == BT_BFP8) launch_stream_m<BT_BFP8, 1>(args, epi, dt, groups, splits, stages, part, r->stream);
+  else if (mt == 2) launch_stream_m<BT_BFP4, 2>(args, epi, dt, groups, splits, stages, part, r->stream);
+  else launch_stream_m<BT_BFP4, 1>(args, epi, dt, groups, splits, stages, part, r->stream);
+  if (splits > 1) {
+    const int64_t outs = (int64_t)args.m * (swi ? args.n / 2 : args.n);
+    const unsigned rb = (unsigned)((outs + 255) / 256);
+    if (swi) parts_reduce_kernel<BT_BF16, true><<<rb, 256, 0, r->stream>>>(args, splits, 16 * mt, part);
+    else if (dt == BT_FP32) parts_reduce_kernel<BT_FP32, false><<<rb, 256, 0, r->stream>>>(args, splits, 16 * mt, part);
+    else parts_reduce_kernel<BT_BF16, false><<<rb, 256, 0, r->stream>>>(args, splits, 16 * mt, part);
+  }
+  return true;
+}
+
 // The deepest pipeline (3 or 2 chunks) whose LDS fits the 160 KB of a CU.
 template <int FMT, int DT, int WM, int WN> constexpr int gemm2_stages() {
   return Gemm2<FMT, DT, WM, WN, 3>::LDS <= 160 * 1024 ? 3 : 2;
@@ -2138,7 +2337,7 @@ extern "C" int bt_matmul(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_
       b_fmt = BT_BF16;
     }
   }
-  if (launch_parts(r, args, b_fmt, false)) {
+  if (launch_stream(r, args, b_fmt, false) || launch_parts(r, args, b_fmt, false)) {
     BT_LAUNCHED("matmul");
     return BT_OK;
   }
@@ -2280,7 +2479,7 @@ extern "C" int bt_matmul_swiglu(bt_runtime *rt, const bt_operand *a, int b_fmt, 
   const int mb = (int)((m + 255) / 256), nb = (int)((n / 2 + 127) / 128);
   const int64_t gemm_blocks = ((m + 127) / 128) * ((n + 127) / 128);
   if ((m <= 64 || (m <= 256 && gemm_blocks < 128)) && a->sr % 8 == 0 && a->ptr % 16 == 0 && ((31 * a->sr + 2 * k + 1024) * 2 < (1ll << 32))) {
-    if (launch_parts(r, args, b_fmt, true)) {
+    if (launch_stream(r, args, b_fmt, true) || launch_parts(r, args, b_fmt, true)) {
       BT_LAUNCHED("matmul_swiglu");
       return BT_OK;
     }

@@ -234,13 +234,14 @@ def test_short_k_rows_with_a_in_lds(rt, fmt, m, k, n):
 
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bfp4"])
 @pytest.mark.parametrize("m,k,n,out", [(32, 4096, 4096, "fp32"), (20, 1024, 1000, "bf16"), (5, 14336, 512, "fp32"),
-                                       (17, 896, 3000, "bf16"), (32, 4096, 28672, "bf16")])
+                                       (17, 896, 3000, "bf16"), (32, 4096, 28672, "bf16"), (12, 2048, 16384, "fp32")])
 def test_split_k_rows(rt, fmt, m, k, n, out):
-  # 5 to 32 rows against K of more than 12 chunks (a multiple of 64): K cut into splits of 8 or 16 chunks, each block
-  # staging its split of A in LDS, then the splits summed in order with the epilogue. Within the reference's bound
-  # of the oracle; a block-float product bit for bit the bf16 product of its values (the splits depend on the shape
-  # alone); the epilogue program (relu, or the residual add into fp32) bit for bit the plain result put through it.
-  # Partial runs (1000, 3000), partial splits (896 = 14 chunks), one tile of rows (5, 16) and two (17 to 32).
+  # 5 to 32 rows against a long K. K a multiple of 512: the streaming kernel, A through a two-stage LDS ring, either
+  # one split with the epilogue in the kernel (28672 and 16384 columns: 256 groups of runs or more) or splits of whole
+  # stages summed in order by a second launch. Otherwise (896 = 14 chunks) splits of 8 or 16 chunks, each block staging
+  # its split of A. Within the reference's bound of the oracle; a block-float product bit for bit the bf16 product of
+  # its values (the kernel and splits depend on the shape alone); the epilogue program (relu, or the residual add into
+  # fp32) bit for bit the plain result put through it. Partial runs (1000, 3000), one tile of rows (5, 12) and two.
   rng = np.random.default_rng(m * n + k)
   x, w = rng.normal(0, 1, (m, k)), rng.normal(0, 0.05, (k, n)).astype(np.float32)
   if fmt == "bf16":

@@ -438,13 +438,15 @@ def test_rms_rows(rt, rows, k):
 
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bfp4"])
 @pytest.mark.parametrize("m,k,f", [(300, 256, 272), (32, 576, 1536), (5, 256, 272), (48, 4096, 352), (32, 4096, 352),
-                                   (9, 1024, 1008), (2048, 64, 4224), (32, 4096, 384), (9, 1024, 1024)])
+                                   (9, 1024, 1008), (2048, 64, 4224), (32, 4096, 384), (9, 1024, 1024),
+                                   (32, 4096, 14336), (7, 512, 8192)])
 def test_matmul_swiglu(rt, fmt, m, k, f):
   # silu(x @ gate) * (x @ up) with the SiLU-mul as the product's epilogue (bt_matmul_swiglu): against the unfused
   # product's gate and up values put through the documented formula, to a bf16 rounding. 300 rows run the tiled GEMM
   # (2048 x 4224: 264 blocks of 256 rows, whose last column goes to a second launch of 128-row blocks);
   # fewer, the kernel that takes a gate run and its up run a wave (48 x 4096: K split over two slices); up to 32 rows
-  # with K over 12 chunks, the split-K kernels with SiLU x up in the reduction (f a multiple of 64 or not)
+  # with K over 12 chunks, the split-K kernels with SiLU x up in the reduction (f a multiple of 64 or not), or, with
+  # K a multiple of 512 and at least 8192 columns of gate, the streaming kernel with SiLU x up in its own epilogue
   rng = np.random.default_rng(11)
   x = Tensor.of(rt, rng.normal(0, 1, (m, k)).astype(np.float32))
   wt, _ = _weights(rt, k, 2 * f, fmt, 3)
