@@ -1234,116 +1234,106 @@ __global__ void __launch_bounds__(256) parts_reduce_kernel(const MatmulArgs args
   }
 }
 
-// 5 to 32 rows of one A (K a multiple of 512) against B streamed once. Block (group, split) takes 4 runs of B, a wave
-// each, over its split's stages of 8 chunks (512 rows of K). A's rows for a stage go into one half of a two-stage LDS
-// ring by direct loads while the other half is multiplied, and each wave's weights for the next stage are in flight
-// while it multiplies this one, so a block covers any length of K with the same LDS. Every run sums its chunks in the
+// 5 to 32 rows of one A (K a multiple of 256) against B streamed once. Block (group, split) takes 4 runs of B, a wave
+// each, over its split's stages of 4 chunks (256 rows of K). Every load goes straight into LDS, whole and aligned: a
+// stage of a run's tiles is one contiguous stretch (4 x 576 bytes for bfp4), loaded 1 KB a wave instruction, and each
+// 512-byte row of A for the stage half an instruction, each 16-byte unit of row r placed at unit u ^ (r % 16) so that
+// the fragment reads of 16 rows fall in distinct banks. A ring of D stages keeps the next D - 1 in flight while one is
+// multiplied; the loads are issued as assembly, which the compiler doesn't count, and waited for here, once a stage
+// (loads complete in order). A wave decodes its B values and exponents out of LDS. Every run sums its chunks in the
 // same order as the other kernels (a chunk's lower 32 rows, then its upper 32), in one accumulator over the split.
 // EPI 0 writes fp32 partial tiles for parts_reduce_kernel (more than one split); 1 stores through the matmul's
 // epilogue (one split); 2 is SiLU x up (one split): waves 0 and 1 take gate runs 2j and 2j + 1, waves 2 and 3 the up
 // runs at the same columns of the other half, and the up tiles reach the gate waves through LDS.
+template <int FMT> struct Stream {
+  static constexpr int C = 4, TB = Tile<FMT>::bytes, BW = C * TB;  // a wave's B bytes a stage
+  static constexpr int BL = (BW + 1023) / 1024, BLAST = (BW - (BL - 1) * 1024) / 16;  // its loads; the last one's lanes
+  static constexpr int D = FMT == BT_BFP4 ? 3 : 2;  // ring stages: at most 80 KB, two blocks a CU
+};
 template <int FMT, int MT, int EPI, int DT>
 __global__ void __launch_bounds__(256) skinny_stream_kernel(const MatmulArgs args, int groups, int stages, float *part) {
-  constexpr int C = 8, TB = Tile<FMT>::bytes, KP = C * 64 + 8, ROWS = 16 * MT, APW = ROWS / 4;
-  constexpr int NQ = FMT == BT_BF16 ? 8 : FMT == BT_BFP8 ? 4 : 2, NE = FMT == BT_BFP4 ? 4 : 1;
-  constexpr int LOADS = APW + 2 * C;  // loads a wave issues for one stage, A's and its weights'
-  __shared__ __attribute__((aligned(16))) uint16_t la[2][ROWS * KP];
+  using S = Stream<FMT>;
+  constexpr int C = S::C, TB = S::TB, ROWS = 16 * MT, ABYTES = ROWS * 512, STAGE = ABYTES + 4 * S::BW, D = S::D;
+  constexpr int AL = ROWS / 8;      // a wave's A loads a stage (two rows each)
+  constexpr int L = AL + S::BL;     // a wave's loads a stage
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[D * STAGE];
   const Head h = early_head(args);
   const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
   const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = (int)blockIdx.x % groups, sp = (int)blockIdx.x / groups;
-  const int run = EPI == 2 ? (wib < 2 ? 0 : h.nruns / 2) + 2 * grp + (wib & 1) : grp * 4 + wib;
-  const bool in = run < h.nruns;
+  const int pos = 2 * grp + (wib & 1);  // SiLU x up: the gate run (waves 0, 1) whose up run waves 2, 3 take
+  const int run = EPI == 2 ? pos + (wib < 2 ? 0 : h.nruns / 2) : grp * 4 + wib;
+  const bool in = EPI == 2 ? pos < h.nruns / 2 : run < h.nruns;
   const int first = sp * stages * C;  // the split's first chunk
   const uint32_t abytes = (uint32_t)(((int64_t)(h.m - 1) * h.a.sr + h.k) * 2);
   const i32x4 ar = buffer_words((const void *)h.a.ptr, abytes);
-  const __amdgpu_buffer_rsrc_t tr =
-      buffer(h.b + (int64_t)(in ? run : 0) * h.chunks * TB, in ? (uint32_t)h.chunks * TB : 0u);
-  uint32_t bq[2][C][NQ], ew[2][C][NE];
-  // stage st: A's rows (a row's 1 KB a load, the block's waves in turn; rows past the last read zeros), and the wave's
-  // 8 chunks of weights
-  auto issue = [&](int st, uint16_t *buf, uint32_t(&q)[C][NQ], uint32_t(&e)[C][NE]) {
+  const i32x4 br = buffer_words(h.b + (int64_t)(in ? run : 0) * h.chunks * TB, in ? (uint32_t)h.chunks * TB : 0u);
+  // stage st into ring slot st % D: this wave's A rows (load j: rows 2q, 2q + 1 with q = wib + 4j; lane l takes
+  // row 2q + l / 32, unit (l % 32) ^ (row % 16) of its 32) and its run's C tiles
+  auto issue = [&](int st) {
+    uint8_t *slot = lds + (st % D) * STAGE;
     const int c0 = first + st * C;
 #pragma unroll
-    for (int j = 0; j < APW; j++) {
-      const int r = wib + 4 * j;
-      const uint32_t voff = r < h.m ? (uint32_t)(((int64_t)r * h.a.sr + (int64_t)c0 * 64) * 2) + 16u * lane : abytes;
-      lds_load16(ar, voff, buf + r * KP);
+    for (int j = 0; j < AL; j++) {
+      const int r = 2 * (wib + 4 * j) + (lane >> 5);
+      const uint32_t unit = (uint32_t)((lane & 31) ^ (r & 15));
+      const uint32_t voff = r < h.m ? (uint32_t)(((int64_t)r * h.a.sr + (int64_t)c0 * 64) * 2) + 16u * unit : abytes;
+      lds_load16(ar, voff, slot + 2 * (wib + 4 * j) * 512);
     }
+    uint8_t *bs = slot + ABYTES + wib * S::BW;
 #pragma unroll
-    for (int i = 0; i < C; i++) {
-      const uint32_t at = (uint32_t)(c0 + i) * TB;
-      if (FMT == BT_BF16) {
-        const auto lo = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 32 * lane, 0, 0);
-        const auto hi = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 32 * lane + 16, 0, 0);
-#pragma unroll
-        for (int w = 0; w < 4; w++) q[i][w] = lo[w], q[i][4 + w] = hi[w];
-      } else if (FMT == BT_BFP8) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 64 + 16 * lane, 0, 0);
-#pragma unroll
-        for (int w = 0; w < 4; w++) q[i][w] = v[w];
-        e[i][0] = __builtin_amdgcn_raw_buffer_load_b32(tr, at + 4 * col, 0, 0);
-      } else {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(tr, at + 64 + 8 * lane, 0, 0);
-        q[i][0] = v[0], q[i][1] = v[1];
-        const auto x = __builtin_amdgcn_raw_buffer_load_b128(tr, at + 16 * g, 0, 0);
-#pragma unroll
-        for (int w = 0; w < 4; w++) e[i][w] = x[w];
-      }
+    for (int j = 0; j < S::BL; j++) {
+      const uint32_t voff = (uint32_t)c0 * TB + 1024u * j + 16u * lane;
+      if (j < S::BL - 1 || S::BLAST == 64 || lane < S::BLAST) lds_load16(br, voff, bs + 1024 * j);
     }
   };
   f32x4 acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; t++) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  auto multiply = [&](const uint16_t *buf, const uint32_t(&q)[C][NQ], const uint32_t(&e)[C][NE]) {
+  auto multiply = [&](int st) {
+    const uint8_t *slot = lds + (st % D) * STAGE;
+    const uint8_t *bs = slot + ABYTES + wib * S::BW;
 #pragma unroll
     for (int i = 0; i < C; i++) {
+      const uint8_t *tile = bs + i * TB;
       bf16x8 bv[2];
       if (FMT == BT_BF16) {
-        const uint4 lo = make_uint4(q[i][0], q[i][1], q[i][2], q[i][3]), hi = make_uint4(q[i][4], q[i][5], q[i][6], q[i][7]);
-        bv[0] = *(const bf16x8 *)&lo;
-        bv[1] = *(const bf16x8 *)&hi;
+        bv[0] = *(const bf16x8 *)(tile + 32 * lane);
+        bv[1] = *(const bf16x8 *)(tile + 32 * lane + 16);
       } else if (FMT == BT_BFP8) {
-        uint32_t ex[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) ex[k] = (uint32_t)__shfl((int)e[i][0], 4 * g + k, 64);
-        bv[0] = q8_to_bf16<true>(make_uint2(q[i][0], q[i][1]), make_uint2(ex[0], ex[1]));
-        bv[1] = q8_to_bf16<true>(make_uint2(q[i][2], q[i][3]), make_uint2(ex[2], ex[3]));
+        const uint4 q = *(const uint4 *)(tile + 64 + 16 * lane);
+        const uint4 e = *(const uint4 *)(tile + 16 * g);
+        bv[0] = q8_to_bf16<true>(make_uint2(q.x, q.y), make_uint2(e.x, e.y));
+        bv[1] = q8_to_bf16<true>(make_uint2(q.z, q.w), make_uint2(e.z, e.w));
       } else {
-        bv[0] = q4_to_bf16_gaps(q[i][0], e[i][0] ^ 0x7F7F7F7Fu, e[i][1] ^ 0x7F7F7F7Fu);
-        bv[1] = q4_to_bf16_gaps(q[i][1], e[i][2] ^ 0x7F7F7F7Fu, e[i][3] ^ 0x7F7F7F7Fu);
+        const uint2 q = *(const uint2 *)(tile + 64 + 8 * lane);
+        const uint4 e = *(const uint4 *)(tile + 16 * g);
+        bv[0] = q4_to_bf16_gaps(q.x, e.x ^ 0x7F7F7F7Fu, e.y ^ 0x7F7F7F7Fu);
+        bv[1] = q4_to_bf16_gaps(q.y, e.z ^ 0x7F7F7F7Fu, e.w ^ 0x7F7F7F7Fu);
       }
 #pragma unroll
       for (int t = 0; t < MT; t++) {
-        const uint16_t *at = buf + (16 * t + col) * KP + 64 * i + 8 * g;
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)at, bv[0], acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)(at + 32), bv[1], acc[t], 0, 0, 0);
+        const int r = 16 * t + col;
+        const uint8_t *row = slot + r * 512;
+        const uint32_t u0 = (uint32_t)((8 * i + g) ^ (r & 15)), u1 = (uint32_t)((8 * i + g + 4) ^ (r & 15));
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)(row + 16 * u0), bv[0], acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)(row + 16 * u1), bv[1], acc[t], 0, 0, 0);
       }
     }
   };
-  // stage st is multiplied from ring half st % 2 while stage st + 1 loads into the other; loads complete in order, so
-  // with the next stage's LOADS issued, at most LOADS outstanding means this stage's have all landed
-  issue(0, la[0], bq[0], ew[0]);
-  for (int st = 0; st < stages; st += 2) {
-    if (st + 1 < stages) {
-      issue(st + 1, la[1], bq[1], ew[1]);
-      wait_vm<LOADS>();
-    } else {
-      wait_vm<0>();
-    }
+  // the first D - 1 stages; then for each stage: wait for its loads (those of the later stages already issued may
+  // stay out), a barrier (every wave's loads have landed, and every wave is done with the previous stage), the stage
+  // D - 1 ahead into the slot the previous stage freed, and the multiply
+#pragma unroll
+  for (int st = 0; st < D - 1; st++)
+    if (st < stages) issue(st);
+  for (int st = 0; st < stages; st++) {
+    const int later = min(D - 2, stages - 1 - st);
+    if (D == 3 && later == 1) wait_vm<L>();
+    else wait_vm<0>();
     __syncthreads();
-    multiply(la[0], bq[0], ew[0]);
-    __syncthreads();
-    if (st + 1 >= stages) break;
-    if (st + 2 < stages) {
-      issue(st + 2, la[0], bq[0], ew[0]);
-      wait_vm<LOADS>();
-    } else {
-      wait_vm<0>();
-    }
-    __syncthreads();
-    multiply(la[1], bq[1], ew[1]);
-    __syncthreads();
+    if (st + D - 1 < stages) issue(st + D - 1);
+    multiply(st);
   }
   if constexpr (EPI == 0) {
     const int n = run * 16 + col;
@@ -1360,15 +1350,16 @@ __global__ void __launch_bounds__(256) skinny_stream_kernel(const MatmulArgs arg
 #pragma unroll
     for (int t = 0; t < MT; t++) store_tile<DT>(args, h, acc[t], 0, t, run, g, col);
   } else {
-    float *up = (float *)&la[0][0];  // free after the last barrier: the up waves' tiles, for the gate waves
+    __syncthreads();  // every wave is done with the ring
+    float *up = (float *)lds;  // the up waves' tiles, for the gate waves
     if (wib >= 2)
 #pragma unroll
       for (int t = 0; t < MT; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) up[(((wib - 2) * MT + t) * 4 + i) * 64 + lane] = acc[t][i];
     __syncthreads();
-    if (wib >= 2) return;
-    const int n = (2 * grp + wib) * 16 + col;  // the gate column, and the output's
+    if (wib >= 2 || !in) return;
+    const int n = pos * 16 + col;  // the gate column, and the output's
     const bt_operand &out = h.out;
 #pragma unroll
     for (int t = 0; t < MT; t++)
@@ -2126,10 +2117,11 @@ static bool launch_parts(Runtime *r, const MatmulArgs &args, int fmt, bool swi) 
   return true;
 }
 
-// The streaming kernels for 5 to 32 rows of one A with K a multiple of 512: false when the product doesn't fit them
-// (then the split-K or one-launch kernels run it). With at least 256 groups of 4 runs, one split whose epilogue
-// stores the result; otherwise splits of whole stages, as many as bring the grid nearest 512 blocks, summed by
-// parts_reduce_kernel in split order. SiLU x up needs the gate and up halves to split into pairs of runs.
+// The streaming kernels for 5 to 32 rows of one A with K a multiple of 256 and over 12 chunks (shorter K stages A
+// whole in LDS, skinny_lds_kernel): false when the product doesn't fit them (then the split-K or one-launch kernels
+// run it). Splits of whole stages, as many as bring the grid nearest 512
+// blocks (two a CU, by LDS), summed by parts_reduce_kernel in split order; one split stores the result through the
+// epilogue itself.
 template <int FMT, int MT>
 static void launch_stream_m(const MatmulArgs &args, int epi, int dt, int groups, int splits, int stages, float *part,
                             hipStream_t s) {
@@ -2141,17 +2133,18 @@ static void launch_stream_m(const MatmulArgs &args, int epi, int dt, int groups,
 }
 static bool launch_stream(Runtime *r, const MatmulArgs &args, int fmt, bool swi) {
   const bt_operand &a = args.a;
-  if (args.batch != 1 || args.m < 5 || args.m > 32 || args.k % 512 || a.sc != 1 || a.ptr % 16 || a.sr % 8 ||
+  if (args.batch != 1 || args.m < 5 || args.m > 32 || args.k % 256 || args.chunks <= 12 || a.sc != 1 || a.ptr % 16 ||
+      a.sr % 8 ||
       ((int64_t)(args.m - 1) * a.sr + args.k) * 2 >= (1ll << 32) ||
-      (int64_t)args.chunks * Tile<BT_BF16>::bytes >= (1ll << 32) || (swi && args.nruns % 4))
+      (int64_t)args.chunks * Tile<BT_BF16>::bytes >= (1ll << 32))
     return false;
-  const int mt = args.m > 16 ? 2 : 1, total = args.chunks / 8;
-  const int groups = swi ? args.nruns / 4 : (args.nruns + 3) / 4;
-  int splits = 1;
-  if (groups < 256) {  // the divisor of the stages that brings groups * splits nearest 512
-    for (int d = 1; d <= total; d++)
-      if (total % d == 0 && std::abs(groups * d - 512) < std::abs(groups * splits - 512)) splits = d;
-  }
+  const int mt = args.m > 16 ? 2 : 1, total = args.chunks / 4;
+  // (SiLU x up takes the same groups and splits as the plain product of its shape, so both sum alike: half the runs
+  // are gate runs, paired two to a block in one split, or partial sums per run with more)
+  const int groups = (args.nruns + 3) / 4;
+  int splits = 1;  // the divisor of the stages that brings the grid nearest 512 blocks
+  for (int d = 1; d <= total; d++)
+    if (total % d == 0 && std::abs(groups * d - 512) < std::abs(groups * splits - 512)) splits = d;
   float *part = nullptr;
   if (splits > 1) {
     part = (float *)runtime_scratch(r, (size_t)splits * 16 * mt * args.n * 4);

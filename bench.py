@@ -475,7 +475,76 @@ def attention_leg(check=True):
   return res, cpu
 
 
-def layer_leg(check=True, cpu_seconds=10.0):
+def _layer_prefill(rt, llama, L, Tensor, c, rc, p, w, ref, shapes, xh, cos, sin, turn, size, tokens, check):
+  """The 2048-token prefill of layer_leg: timed, and checked on key rows against the oracle."""
+  dim, heads, kv, hd = 4096, 32, 8, 128
+  x = Tensor.of(rt, xh[None], "fp32")
+  cache = Tensor.zeros(rt, size, hd, batch=2 * kv)
+  places = Tensor.of(rt, [list(range(tokens))], "int32")
+  rot = (w["cos"].gather(places), w["sin"].gather(places), w["turn"])
+  column = places.reshape(1, tokens, 1)
+  run = lambda: llama.layer(x, p, c, rot, column, cache, places).realize()
+  run()
+  rt.wait()
+  reps, t0 = 5, time.perf_counter()
+  for _ in range(reps): run()
+  rt.wait()
+  eager = (time.perf_counter() - t0) / reps * 1e6
+  us, y = replay_us(rt, run, 5)
+  flops = 2 * tokens * sum(a * b for a, b in shapes.values()) + 4 * heads * hd * tokens * (tokens + 1) // 2
+  entry = {"us": round(us, 1), "TFLOP/s": round(flops / us / 1e6, 1),
+           "frac_mfma_peak": round(flops / us / 1e6 / 2500.0, 4), "flops": flops, "eager_us": round(eager, 1)}
+  if check:  # key rows against the oracle's layer, which still computes every row's keys and values
+    rows = [0, 1, 255, 1024, 2047]
+    got = np.frombuffer(y, np.float32).reshape(tokens, dim)[rows]
+    mask = np.where(np.arange(tokens) > np.arange(tokens)[:, None], np.float32(-1e9), np.float32(0))
+    t0 = time.perf_counter()
+    want = L.layer(xh, ref, rc, (cos[:tokens], sin[:tokens], turn), mask, np.zeros((2 * kv, tokens, hd)),
+                   range(tokens), only=rows)
+    log("layer prefill oracle rows in", round(time.perf_counter() - t0, 1), "s")
+    change, err = np.abs(want - xh[rows]).max(), np.abs(got - want).max()
+    entry.update({"parity": bool(err < 0.03 * change), "parity_rows": rows, "max_err_over_change": round(float(err / change), 5)})
+  log("layer prefill", entry)
+  return entry
+
+
+def _layer_decode(rt, llama, L, B, Tensor, c, rc, p, w, ref, wbytes, cos, sin, turn, rng, check):
+  """The batch-32 decode step of layer_leg: timed, and checked on key slots against the oracle."""
+  dim, heads, kv, hd, size, slots = 4096, 32, 8, 128, 4096, 32
+  K = B.bf16(rng.standard_normal((slots * kv, size, hd), dtype=np.float32))
+  V = B.bf16(rng.standard_normal((slots * kv, size, hd), dtype=np.float32))
+  K[:, size - 1:], V[:, size - 1:] = 0, 0
+  keys, values = Tensor.of(rt, K), Tensor.of(rt, V)
+  xs_h = rng.standard_normal((slots, dim), dtype=np.float32)
+  xs = Tensor.of(rt, xs_h[None], "fp32")
+  at = Tensor.of(rt, [[size - 1] * slots], "int32")
+  rot = (w["cos"].gather(at), w["sin"].gather(at), w["turn"])
+  place = Tensor.of(rt, [[size - 1]], "int32")
+  step = lambda: llama.slots_layer(xs, p, c, rot, keys, values, place).realize()
+  step()
+  rt.wait()
+  reps, t0 = 20, time.perf_counter()
+  for _ in range(reps): step()
+  rt.wait()
+  eager = (time.perf_counter() - t0) / reps * 1e6
+  us, y = replay_us(rt, step, 20)
+  nbytes = wbytes + slots * size * kv * hd * 2 * 2
+  entry = {"us": round(us, 1), "GB/s": round(nbytes / us / 1e3, 1), "frac_hbm_peak": round(nbytes / us / 1e3 / PEAK_GBS, 4),
+           "bytes": nbytes, "tok/s": round(slots / us * 1e6, 1), "eager_us": round(eager, 1)}
+  if check:  # key slots against the oracle's layer run on each slot alone
+    got = np.frombuffer(y, np.float32).reshape(slots, dim)
+    worst, sl = 0.0, [0, 13, 31]
+    for s_ in sl:
+      cache_s = np.concatenate([K[s_ * kv:(s_ + 1) * kv], V[s_ * kv:(s_ + 1) * kv]]).astype(np.float64)
+      want = L.layer(xs_h[s_:s_ + 1], ref, rc, (cos[[size - 1]], sin[[size - 1]], turn), np.zeros((1, size), np.float32),
+                     cache_s, [size - 1])[0]
+      worst = max(worst, float(np.abs(got[s_] - want).max() / np.abs(want - xs_h[s_]).max()))
+    entry.update({"parity": worst < 0.03, "parity_slots": sl, "max_err_over_change": round(worst, 5)})
+  log("layer decode", entry)
+  return entry, K, V, xs_h
+
+
+def layer_leg(check=True, cpu_seconds=10.0, parts=("prefill", "decode")):
   """one Llama-3-8B-shaped block (4096 wide, 32 query and 8 key heads of 128, SwiGLU 14336) with
   every projection N(0, 0.02) in bfp4 and bf16 norms: a 2048-token prefill from position 0 (matrix-core bound;
   flops 2 * 2048 * 218,103,808 for the projections plus the causal attention), then one batch-32 decode step, each
@@ -512,70 +581,12 @@ def layer_leg(check=True, cpu_seconds=10.0):
     w["cos"], w["sin"], w["turn"] = Tensor.of(rt, cos), Tensor.of(rt, sin), Tensor.of(rt, turn).columns()
     p = llama.block(w, 0)
     wbytes = sum(shape[0] * shape[1] for shape in shapes.values()) * 576 // 1024
-    # prefill
     xh = rng.standard_normal((tokens, dim), dtype=np.float32)
-    x = Tensor.of(rt, xh[None], "fp32")
-    cache = Tensor.zeros(rt, size, hd, batch=2 * kv)
-    places = Tensor.of(rt, [list(range(tokens))], "int32")
-    rot = (w["cos"].gather(places), w["sin"].gather(places), w["turn"])
-    column = places.reshape(1, tokens, 1)
-    run = lambda: llama.layer(x, p, c, rot, column, cache, places).realize()
-    run()
-    rt.wait()
-    reps, t0 = 5, time.perf_counter()
-    for _ in range(reps): run()
-    rt.wait()
-    eager = (time.perf_counter() - t0) / reps * 1e6
-    us, y = replay_us(rt, run, 5)
-    flops = 2 * tokens * sum(a * b for a, b in shapes.values()) + 4 * heads * hd * tokens * (tokens + 1) // 2
-    entry = {"us": round(us, 1), "TFLOP/s": round(flops / us / 1e6, 1),
-             "frac_mfma_peak": round(flops / us / 1e6 / 2500.0, 4), "flops": flops, "eager_us": round(eager, 1)}
-    if check:  # key rows against the oracle's layer, which still computes every row's keys and values
-      rows = [0, 1, 255, 1024, 2047]
-      got = np.frombuffer(y, np.float32).reshape(tokens, dim)[rows]
-      mask = np.where(np.arange(tokens) > np.arange(tokens)[:, None], np.float32(-1e9), np.float32(0))
-      t0 = time.perf_counter()
-      want = L.layer(xh, ref, rc, (cos[:tokens], sin[:tokens], turn), mask, np.zeros((2 * kv, tokens, hd)),
-                     range(tokens), only=rows)
-      log("layer prefill oracle rows in", round(time.perf_counter() - t0, 1), "s")
-      change, err = np.abs(want - xh[rows]).max(), np.abs(got - want).max()
-      entry.update({"parity": bool(err < 0.03 * change), "parity_rows": rows, "max_err_over_change": round(float(err / change), 5)})
-    res["prefill_2048"] = entry
-    log("layer prefill", entry)
-    del y, cache
-    # batch-32 decode at position 4095 of each slot's cache
-    K = B.bf16(rng.standard_normal((slots * kv, size, hd), dtype=np.float32))
-    V = B.bf16(rng.standard_normal((slots * kv, size, hd), dtype=np.float32))
-    K[:, size - 1:], V[:, size - 1:] = 0, 0
-    keys, values = Tensor.of(rt, K), Tensor.of(rt, V)
-    xs_h = rng.standard_normal((slots, dim), dtype=np.float32)
-    xs = Tensor.of(rt, xs_h[None], "fp32")
-    at = Tensor.of(rt, [[size - 1] * slots], "int32")
-    rot = (w["cos"].gather(at), w["sin"].gather(at), w["turn"])
-    place = Tensor.of(rt, [[size - 1]], "int32")
-    step = lambda: llama.slots_layer(xs, p, c, rot, keys, values, place).realize()
-    step()
-    rt.wait()
-    reps, t0 = 20, time.perf_counter()
-    for _ in range(reps): step()
-    rt.wait()
-    eager = (time.perf_counter() - t0) / reps * 1e6
-    us, y = replay_us(rt, step, 20)
-    nbytes = wbytes + slots * size * kv * hd * 2 * 2
-    entry = {"us": round(us, 1), "GB/s": round(nbytes / us / 1e3, 1), "frac_hbm_peak": round(nbytes / us / 1e3 / PEAK_GBS, 4),
-             "bytes": nbytes, "tok/s": round(slots / us * 1e6, 1), "eager_us": round(eager, 1)}
-    if check:  # key slots against the oracle's layer run on each slot alone
-      got = np.frombuffer(y, np.float32).reshape(slots, dim)
-      worst, sl = 0.0, [0, 13, 31]
-      for s_ in sl:
-        cache_s = np.concatenate([K[s_ * kv:(s_ + 1) * kv], V[s_ * kv:(s_ + 1) * kv]]).astype(np.float64)
-        want = L.layer(xs_h[s_:s_ + 1], ref, rc, (cos[[size - 1]], sin[[size - 1]], turn), np.zeros((1, size), np.float32),
-                       cache_s, [size - 1])[0]
-        worst = max(worst, float(np.abs(got[s_] - want).max() / np.abs(want - xs_h[s_]).max()))
-      entry.update({"parity": worst < 0.03, "parity_slots": sl, "max_err_over_change": round(worst, 5)})
-    res["decode_B32_ctx4096"] = entry
-    log("layer decode", entry)
-    if check:  # the oracle's layer on the host: a 128-token prefill, and one slot's decode token
+    if "prefill" in parts: res["prefill_2048"] = _layer_prefill(rt, llama, L, Tensor, c, rc, p, w, ref, shapes, xh, cos,
+                                                                sin, turn, size, tokens, check)
+    if "decode" in parts: res["decode_B32_ctx4096"], K, V, xs_h = _layer_decode(rt, llama, L, B, Tensor, c, rc, p, w, ref,
+                                                                                 wbytes, cos, sin, turn, rng, check)
+    if check and parts == ("prefill", "decode"):  # the oracle's layer on the host: a 128-token prefill, one slot's token
       n = 128
       mask = np.where(np.arange(n) > np.arange(n)[:, None], np.float32(-1e9), np.float32(0))
       per, reps = timed_cpu(lambda: L.layer(xh[:n], ref, rc, (cos[:n], sin[:n], turn), mask,
@@ -615,7 +626,8 @@ def main():
   ap.add_argument("--cpu-seconds", type=float, default=10.0)
   ap.add_argument("--no-cpu", action="store_true")
   ap.add_argument("--only", default=None,
-                  help="one part: a GEMV configuration (bfp4_B1 ...), gemv, c1, attention, layer or decode")
+                  help="one part: a GEMV configuration (bfp4_B1 ...), gemv, c1, attention, layer (or layer_prefill, "
+                  "layer_decode) or decode")
   ap.add_argument("--no-decode", action="store_true", help="skip the SmolLM decode (BASELINE config 3)")
   ap.add_argument("--eager", action="store_true", help="decode without graph replay (for kernel-trace profiles)")
   args = ap.parse_args()
@@ -645,12 +657,14 @@ def main():
     log("c1", extra["c1"])
   if args.only in (None, "attention"):
     extra["attention"], extra["attention_cpu_baseline"] = attention_leg(check=not args.no_cpu)
-  if args.only in (None, "layer"):
-    extra["layer"], extra["layer_cpu_baseline"] = layer_leg(check=not args.no_cpu, cpu_seconds=args.cpu_seconds)
+  if args.only in (None, "layer", "layer_prefill", "layer_decode"):
+    parts = {"layer_prefill": ("prefill",), "layer_decode": ("decode",)}.get(args.only, ("prefill", "decode"))
+    extra["layer"], extra["layer_cpu_baseline"] = layer_leg(check=not args.no_cpu, cpu_seconds=args.cpu_seconds,
+                                                            parts=parts)
   if not args.no_decode and args.only in (None, "decode"):
     extra["decode"], extra["decode_cpu_baseline"] = decode_leg(check=not args.no_cpu, replay=not args.eager)
     log("decode", extra["decode"])
-  if args.only in ("c1", "attention", "layer", "decode"):
+  if args.only in ("c1", "attention", "layer", "layer_prefill", "layer_decode", "decode"):
     print(json.dumps(extra), flush=True)
     return
   head = configs.get("bfp4_B1") or next(iter(configs.values()))
