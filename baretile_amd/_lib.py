@@ -89,6 +89,7 @@ SIGNATURES = {
   "bt_matmul": [RT, POINTER(Operand), c_int, U64, I64, I64, I64, I64, I64, POINTER(Program), POINTER(Operand)],
   "bt_attention": [RT, POINTER(AttentionArgs)],
   "bt_attention_scratch": [POINTER(AttentionArgs), POINTER(c_uint64)],
+  "bt_attention_noalloc": [RT, POINTER(AttentionArgs)],
   "bt_matmul_row": [RT, POINTER(RowArgs)], "bt_rope_put": [RT, POINTER(RopeArgs)],
   "bt_put_bfp": [RT, c_int, U64, U64, I64, I64, I64, I64, I64, U64, I64, U64, I64, I64],
   "bt_matmul_row_rope": [RT, POINTER(RowArgs), POINTER(RopeArgs)],

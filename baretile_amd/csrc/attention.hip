@@ -21,6 +21,7 @@
 // visible keys, written as fp32 partial sums to scratch and combined by a second kernel. Prefill: the block's waves take 4 consecutive tiles and share each block
 // of 64 keys and values through LDS, double-buffered.
 #include "common.h"
+#include <mutex>
 #include <algorithm>
 
 namespace bt {
@@ -863,6 +864,46 @@ static int plan_attention(const bt_attention_args *a, AttnPlan *p) {
   return BT_OK;
 }
 
+// The working memory of bt_attention_noalloc: one array a GPU, the split decode's partial sums. Host code never passes
+// the array's name to a kernel (on the host it stands for no device address): at bt_open, with the device current,
+// hipGetSymbolAddress gives each device's own copy's address, kept here per device.
+static __device__ __align__(256) uint8_t scratch[BT_ATTENTION_NOALLOC_BYTES];
+static std::mutex noalloc_lock;
+static void *noalloc_ptr[BT_MAX_DEVICES];
+static hipError_t noalloc_error[BT_MAX_DEVICES];
+
+void attention_noalloc_init(int device) {
+  if (device < 0 || device >= BT_MAX_DEVICES) return;
+  std::lock_guard<std::mutex> hold(noalloc_lock);
+  if (noalloc_ptr[device]) return;
+  void *p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) (void)hipGetLastError();
+  noalloc_error[device] = e;
+  if (e == hipSuccess) noalloc_ptr[device] = p;
+}
+
+static int run_attention(Runtime *r, const bt_attention_args *a, const AttnPlan &p, float *scratch) {
+  const int kvh = a->heads / a->rep;
+  if (p.decode) {
+    const unsigned blocks = (unsigned)(kvh * p.tiles * p.parts);
+    launch_decode(*a, blocks, p.tiles, p.parts, scratch, r->stream);
+    BT_LAUNCHED("attention");
+    if (p.parts > 1) {
+      const unsigned cb = (unsigned)(kvh * p.tiles);
+      if (a->head_dim == 64) attention_combine_kernel<64><<<cb, 256, 0, r->stream>>>(*a, p.tiles, p.parts, scratch);
+      else attention_combine_kernel<128><<<cb, 256, 0, r->stream>>>(*a, p.tiles, p.parts, scratch);
+      BT_LAUNCHED("attention combine");
+    }
+  } else {
+    const int rblocks = (a->rep * a->rows + 127) / 128;
+    const unsigned blocks = (unsigned)(kvh * rblocks);
+    launch_prefill(*a, blocks, rblocks, kvh, r->stream);
+    BT_LAUNCHED("attention");
+  }
+  return BT_OK;
+}
+
 }  // namespace bt
 
 using namespace bt;
@@ -885,25 +926,27 @@ int bt_attention(bt_runtime *rt, const bt_attention_args *a) {
   if (p.scratch_bytes && (!a->scratch || a->scratch_bytes < p.scratch_bytes || a->scratch % 16))
     return fail(BT_EINVAL, "attention in %d parts needs %llu bytes of 16-byte aligned scratch", p.parts,
                 (unsigned long long)p.scratch_bytes);
-  const int kvh = a->heads / a->rep;
-  float *scratch = (float *)(uintptr_t)a->scratch;
-  if (p.decode) {
-    const unsigned blocks = (unsigned)(kvh * p.tiles * p.parts);
-    launch_decode(*a, blocks, p.tiles, p.parts, scratch, r->stream);
-    BT_LAUNCHED("attention");
-    if (p.parts > 1) {
-      const unsigned cb = (unsigned)(kvh * p.tiles);
-      if (a->head_dim == 64) attention_combine_kernel<64><<<cb, 256, 0, r->stream>>>(*a, p.tiles, p.parts, scratch);
-      else attention_combine_kernel<128><<<cb, 256, 0, r->stream>>>(*a, p.tiles, p.parts, scratch);
-      BT_LAUNCHED("attention combine");
-    }
-  } else {
-    const int rblocks = (a->rep * a->rows + 127) / 128;
-    const unsigned blocks = (unsigned)(kvh * rblocks);
-    launch_prefill(*a, blocks, rblocks, kvh, r->stream);
-    BT_LAUNCHED("attention");
+  return run_attention(r, a, p, (float *)(uintptr_t)a->scratch);
+}
+
+int bt_attention_noalloc(bt_runtime *rt, const bt_attention_args *a) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  AttnPlan p;
+  if (int s = plan_attention(a, &p)) return s;
+  if (p.scratch_bytes > BT_ATTENTION_NOALLOC_BYTES)
+    return fail(BT_EINVAL, "attention in %d parts needs %llu bytes of working memory, and bt_attention_noalloc has %u: "
+                "take fewer parts, or bt_attention with a workspace", p.parts, (unsigned long long)p.scratch_bytes,
+                (unsigned)BT_ATTENTION_NOALLOC_BYTES);
+  void *ptr = nullptr;
+  {
+    std::lock_guard<std::mutex> hold(noalloc_lock);
+    if (r->device < BT_MAX_DEVICES) ptr = noalloc_ptr[r->device];
   }
-  return BT_OK;
+  if (!ptr)
+    return fail(BT_ESTATE, "bt_attention_noalloc's working memory on device %d has no address: %s", r->device,
+                r->device < BT_MAX_DEVICES ? hipGetErrorString(noalloc_error[r->device]) : "device index too large");
+  return run_attention(r, a, p, (float *)ptr);
 }
 
 }  // extern "C"

@@ -46,6 +46,11 @@ struct Runtime {
 // takes a way that needs none), or when the device is out of memory.
 void *runtime_scratch(Runtime *r, size_t bytes);
 
+// Looks up, with `device` current, the address of that device's copy of bt_attention_noalloc's working memory
+// (attention.hip); bt_open calls it once per runtime.
+#define BT_MAX_DEVICES 64
+void attention_noalloc_init(int device);
+
 // Checks a runtime handle and makes its device current.
 int enter(bt_runtime *rt, Runtime **out);
 

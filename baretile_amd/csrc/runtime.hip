@@ -132,6 +132,7 @@ int bt_open(int device, bt_runtime **out) {
   BT_HIP(hipGetDeviceProperties(&p, device));
   if (std::string(p.gcnArchName).rfind("gfx950", 0) != 0)
     return fail(BT_ESTATE, "this library is built for gfx950, and device %d is %s", device, p.gcnArchName);
+  attention_noalloc_init(device);  // the no-alloc attention's working memory on this device (a static array)
   Runtime *r = new Runtime;
   r->device = device;
   hipError_t s = hipStreamCreateWithFlags(&r->stream, hipStreamNonBlocking);

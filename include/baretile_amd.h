@@ -288,6 +288,14 @@ typedef struct {
 int bt_attention(bt_runtime *rt, const bt_attention_args *args);
 /* The scratch bytes bt_attention needs for args (0 when it runs in one part). */
 int bt_attention_scratch(const bt_attention_args *args, uint64_t *bytes);
+/* No counterpart in the reference: bt_attention for callers that cannot allocate device memory (code under graph
+ * capture, serving loops that must not call hipMalloc, harnesses that forbid it). The same kernels and results, with
+ * args->scratch and scratch_bytes ignored: the split decode's partial sums go to a static array of
+ * BT_ATTENTION_NOALLOC_BYTES on each GPU, held until the process ends, and nothing is allocated or freed. BT_EINVAL
+ * when the plan needs more than that (bt_attention_scratch tells); nothing in it needs to start at zero. Every call
+ * on one GPU shares that GPU's array, so calls that overlap on one GPU (other streams, other threads) race. */
+#define BT_ATTENTION_NOALLOC_BYTES (8u << 20)
+int bt_attention_noalloc(bt_runtime *rt, const bt_attention_args *args);
 
 /* ---- rows in and out of a cache: replaces gather_kernel (kernels.py:1007-1049) and put_kernel
  * (kernels.py:1083-1168) ------------------------------------------------------------------------------------------ */
