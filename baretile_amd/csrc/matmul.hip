@@ -1524,15 +1524,24 @@ gemm2_kernel(const MatmulArgs args, int mblocks, int nblocks) {
 constexpr int GEMM_PLAIN = 0, GEMM_RES = 1, GEMM_SWIGLU = 2;
 // BM: the block's rows, 256 or 128 (a wave BM / 2 of them by 64 columns), for products whose 256-row blocks would
 // leave CUs idle.
-template <int DT, int S, int MODE = GEMM_PLAIN, int BM = 256>
+// FMT 4 (bfp4 B) stages a chunk (64 rows of K) at a time, CS = 3 deep: A as BM rows of 128 bytes (unit u of row r at
+// u ^ (r % 8), so the fragment reads of 8 neighbouring rows meet different banks) and the block's 16 tiles as they are
+// stored, 576 bytes each (36 lanes of a direct load). Each wave reads its 4 tiles' value and exponent bytes once a
+// chunk and decodes each half into bf16 fragments in registers (q * 2^(e - 129) by subtracting exponent gaps, the
+// values the unpacker gives), so B crosses HBM and LDS at 0.28 of its bf16 size and needs no unpacking pass. The
+// sums run in the same order, so the result is the same bits as the bf16 GEMM on B's unpacked tiles.
+template <int FMT, int DT, int S, int MODE = GEMM_PLAIN, int BM = 256>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand res, int nb_off = 0) {
+  static_assert(FMT == BT_BF16 || FMT == BT_BFP4, "gemm3 takes bf16 or bfp4 B");
   constexpr bool RES = MODE == GEMM_RES;
   constexpr int BN = 256, A_BYTES = BM * 64, STAGE = A_BYTES + 16384, WM = BM / 32, WN = 4, WR = BM / 2;
   constexpr int AL = BM / 128;  // A loads a wave issues a step
+  constexpr int CS = 3, QTB = 576, QA = BM * 128, QSTAGE = QA + 16 * QTB, QAL = BM / 64;  // bfp4: chunk stages
+  constexpr int RING = FMT == BT_BF16 ? S * STAGE : CS * QSTAGE;
   constexpr int ESZ = DT == BT_FP32 ? 4 : 2, ES = BN * ESZ + 16;
   constexpr int HALF = (DT == BT_FP32 ? 128 : 256) < BM ? (DT == BT_FP32 ? 128 : 256) : BM;
-  constexpr int LDS = RES ? S * STAGE : S * STAGE > HALF * ES ? S * STAGE : HALF * ES;
+  constexpr int LDS = RES ? RING : RING > HALF * ES ? RING : HALF * ES;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS];
   const Head h = early_head(args);
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, col = lane & 15;
@@ -1550,8 +1559,26 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
   const uint16_t *abase = (const uint16_t *)h.a.ptr + operand_matrix(h.a, b) * h.a.sb;
   const i32x4 ar = buffer_words(abase, (uint32_t)(((int64_t)(h.m - 1) * h.a.sr + h.k) * 2));
   const uint8_t *bbase = h.b + (h.b_matrix_bytes ? b * h.b_matrix_bytes : 0);
-  const i32x4 br = buffer_words(bbase, (uint32_t)((int64_t)h.nruns * h.chunks * 2048));
   constexpr uint32_t NOWHERE = 0xFFFFFFF0u;  // an offset past every buffer: the load writes zeros
+  // the run of B whose tile the block's tile li (0..15) is, and whether it exists
+  auto b_run = [&](int li, bool &in) {
+    int run = n0 / 16 + li;
+    in = run < h.nruns;
+    if (MODE == GEMM_SWIGLU) {  // tiles 0..7: gate columns from 128 bn, 8..15: the same up columns
+      const int f = h.n / 2, c0 = bn * 128 + 16 * (li & 7);
+      run = ((li < 8 ? 0 : f) + c0) / 16;
+      in = c0 < f;
+    }
+    return run;
+  };
+  f32x4 acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; i++)
+#pragma unroll
+    for (int j = 0; j < WN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (FMT == BT_BF16) {
+  const i32x4 br = buffer_words(bbase, (uint32_t)((int64_t)h.nruns * h.chunks * 2048));
+
   // each lane's source for the wave's 2 A and 2 B loads of step 0 (a step adds 64 bytes to A's; B's move by half a
   // tile, then to the next chunk)
   uint32_t asrc[2], bsrc[2];
@@ -1560,13 +1587,8 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
     const int li = wib + 8 * j;  // rows 16 li .. 16 li + 15 of A (li < BM / 16), tile li of B
     const int r = 16 * li + lane / 4, c = (lane & 3) ^ ((r >> 1) & 3);
     asrc[j] = j < AL && m0 + r < h.m ? (uint32_t)(((int64_t)(m0 + r) * h.a.sr + 8 * c) * 2) : NOWHERE;
-    int run = n0 / 16 + li;
-    bool in = run < h.nruns;
-    if (MODE == GEMM_SWIGLU) {  // tiles 0..7: gate columns from 128 bn, 8..15: the same up columns
-      const int f = h.n / 2, c0 = bn * 128 + 16 * (li & 7);
-      run = ((li < 8 ? 0 : f) + c0) / 16;
-      in = c0 < f;
-    }
+    bool in;
+    const int run = b_run(li, in);
     bsrc[j] = in ? (uint32_t)((int64_t)run * h.chunks * 2048 + 32 * lane) : NOWHERE;
   }
   auto issue = [&](int t) {  // step t's loads into stage t % S
@@ -1579,11 +1601,6 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
       lds_load16(br, bsrc[j] == NOWHERE ? NOWHERE : bsrc[j] + bo, st + A_BYTES + li * 1024);
     }
   };
-  f32x4 acc[WM][WN];
-#pragma unroll
-  for (int i = 0; i < WM; i++)
-#pragma unroll
-    for (int j = 0; j < WN; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const int steps = h.k / 32;
 #pragma unroll
   for (int t = 0; t < S - 1; t++)
@@ -1607,6 +1624,70 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
     for (int i = 0; i < WM; i++)
 #pragma unroll
       for (int j = 0; j < WN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+  }
+  } else {
+    const i32x4 br = buffer_words(bbase, (uint32_t)((int64_t)h.nruns * h.chunks * QTB));
+    // each lane's source for the wave's QAL A loads (8 rows of 128 bytes each; lane l takes row l / 8, unit
+    // (l % 8) ^ (row % 8)) and 2 B tiles (tiles wib and wib + 8, lanes 0..35) of chunk 0; a chunk adds 128 bytes to
+    // A's, one tile to B's
+    uint32_t aq[QAL], bq[2];
+#pragma unroll
+    for (int j = 0; j < QAL; j++) {
+      const int r = 8 * (wib + 8 * j) + (lane >> 3), u = (lane & 7) ^ (r & 7);
+      aq[j] = m0 + r < h.m ? (uint32_t)(((int64_t)(m0 + r) * h.a.sr + 8 * u) * 2) : NOWHERE;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      bool in;
+      const int run = b_run(wib + 8 * j, in);
+      bq[j] = in ? (uint32_t)((int64_t)run * h.chunks * QTB + 16 * lane) : NOWHERE;
+    }
+    auto issue = [&](int c) {  // chunk c's loads into stage c % CS
+      uint8_t *st = lds + (c % CS) * QSTAGE;
+      const uint32_t ao = (uint32_t)c * 128, bo = (uint32_t)c * QTB;
+#pragma unroll
+      for (int j = 0; j < QAL; j++) lds_load16(ar, aq[j] == NOWHERE ? NOWHERE : aq[j] + ao, st + (wib + 8 * j) * 1024);
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+        if (lane < QTB / 16) lds_load16(br, bq[j] == NOWHERE ? NOWHERE : bq[j] + bo, st + QA + (wib + 8 * j) * QTB);
+    };
+    const int chunks = h.k / 64;
+#pragma unroll
+    for (int c = 0; c < CS - 1; c++)
+      if (c < chunks) issue(c);
+    for (int c = 0; c < chunks; c++) {
+      if (c + CS - 2 < chunks) wait_vm<(QAL + 2) * (CS - 2)>();
+      else wait_vm<0>();
+      __syncthreads();
+      if (c + CS - 1 < chunks) issue(c + CS - 1);  // into the stage chunk c - 1 used
+      const uint8_t *st = lds + (c % CS) * QSTAGE;
+      uint2 q[WN];
+      uint4 e[WN];
+#pragma unroll
+      for (int j = 0; j < WN; j++) {
+        const uint8_t *tile = st + QA + (wn * 4 + j) * QTB;
+        q[j] = *(const uint2 *)(tile + 64 + 8 * lane);
+        e[j] = *(const uint4 *)(tile + 16 * g);
+      }
+#pragma unroll
+      for (int hh = 0; hh < 2; hh++) {
+        bf16x8 fa[WM], fb[WN];
+#pragma unroll
+        for (int i = 0; i < WM; i++) {
+          const int r = wm * WR + 16 * i + col;
+          fa[i] = *(const bf16x8 *)(st + r * 128 + 16 * ((g + 4 * hh) ^ (r & 7)));
+        }
+#pragma unroll
+        for (int j = 0; j < WN; j++)
+          fb[j] = q4_to_bf16_gaps(hh ? q[j].y : q[j].x, (hh ? e[j].z : e[j].x) ^ 0x7F7F7F7Fu,
+                                  (hh ? e[j].w : e[j].y) ^ 0x7F7F7F7Fu);
+#pragma unroll
+        for (int i = 0; i < WM; i++)
+#pragma unroll
+          for (int j = 0; j < WN; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      }
+    }
   }
   if constexpr (RES) {
     // lanes 0..15 of a row group write 16 neighbouring columns: 64 bytes
@@ -2204,6 +2285,16 @@ static bool residual_program(const MatmulArgs &args, bt_operand *res) {
   return true;
 }
 
+// gemm3's block rows: 256 or 128, whichever fills the CUs' rounds better, 128-row blocks counted at 0.85 of the
+// speed.
+static int gemm3_rows(const MatmulArgs &args) {
+  auto fill = [&](int bm) {
+    const int64_t blocks = (int64_t)args.batch * ((args.m + bm - 1) / bm) * ((args.n + 255) / 256);
+    return (double)blocks / (double)((blocks + 255) / 256 * 256);
+  };
+  return fill(256) >= 0.85 * fill(128) ? 256 : 128;
+}
+
 // The block shape for a GEMM: the largest tile whose grid still keeps the chip's 256 CUs busy through its last round.
 template <int FMT, int DT>
 static void launch_gemm_dt(const MatmulArgs &args, hipStream_t s) {
@@ -2221,23 +2312,20 @@ static void launch_gemm_dt(const MatmulArgs &args, hipStream_t s) {
     const double sc = opts[o].eff * (double)blocks / (double)(rounds * 256);
     if (sc > score + 1e-9) score = sc, best = o;
   }
-  if constexpr (FMT == BT_BF16) {
+  if constexpr (FMT == BT_BF16 || FMT == BT_BFP4) {
     bt_operand res{};
-    if (args.m > 128 && args.k % 32 == 0 && (DT == BT_BF16 || residual_program(args, &res))) {
-      // 256 or 128 rows a block: whichever fills the CUs' rounds better, 128-row blocks counted at 0.85 of the speed
-      auto fill = [&](int bm) {
-        const int64_t blocks = (int64_t)args.batch * ((args.m + bm - 1) / bm) * ((args.n + 255) / 256);
-        return (double)blocks / (double)((blocks + 255) / 256 * 256);
-      };
-      const int bm = fill(256) >= 0.85 * fill(128) ? 256 : 128;
+    const bool fits = FMT == BT_BF16 ? args.m > 128 && args.k % 32 == 0
+                                     : args.m >= 512 && args.k % 64 == 0 && (int64_t)args.chunks * args.nruns * 576 < (1ll << 32);
+    if (fits && (DT == BT_BF16 || residual_program(args, &res))) {
+      const int bm = gemm3_rows(args);
       const int mb = (args.m + bm - 1) / bm, nb = (args.n + 255) / 256;
       const unsigned blocks = (unsigned)((int64_t)mb * nb * args.batch);
       if constexpr (DT == BT_BF16) {
-        if (bm == 256) gemm3_kernel<DT, 4><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
-        else gemm3_kernel<DT, 4, GEMM_PLAIN, 128><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
+        if (bm == 256) gemm3_kernel<FMT, DT, 4><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
+        else gemm3_kernel<FMT, DT, 4, GEMM_PLAIN, 128><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
       } else {
-        if (bm == 256) gemm3_kernel<DT, 4, GEMM_RES><<<blocks, 512, 0, s>>>(args, mb, nb, res);
-        else gemm3_kernel<DT, 4, GEMM_RES, 128><<<blocks, 512, 0, s>>>(args, mb, nb, res);
+        if (bm == 256) gemm3_kernel<FMT, DT, 4, GEMM_RES><<<blocks, 512, 0, s>>>(args, mb, nb, res);
+        else gemm3_kernel<FMT, DT, 4, GEMM_RES, 128><<<blocks, 512, 0, s>>>(args, mb, nb, res);
       }
       return;
     }
@@ -2313,11 +2401,13 @@ extern "C" int bt_matmul(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_
   }
   args.n_inst = args.prog.n_inst;
   args.out = *out;
-  // A prefill-sized product with block-float B and bf16 out: B unpacked once into bf16 tiles in the runtime's scratch
-  // (the same values bit for bit), then the bf16 GEMM, whose pipeline the in-LDS conversion would stall
+  // A prefill-sized product with bfp8 B (or bfp4 with K not in whole chunks) and bf16 out: B unpacked once into bf16
+  // tiles in the runtime's scratch (the same values bit for bit), then the bf16 GEMM. bfp4 B in whole chunks goes to
+  // the same GEMM reading it as it is stored, decoded in registers.
   const bool bf16_out = out->dtype == BT_BF16 && (!epilogue || epilogue->dtype != BT_FP32);
-  if (b_fmt != BT_BF16 && (bf16_out || residual_program(args, nullptr)) && m >= 512 &&
-      k % 32 == 0 && a->sc == 1 && (int64_t)args.chunks * args.nruns * 2048 < (1ll << 32)) {
+  if (b_fmt != BT_BF16 && !(b_fmt == BT_BFP4 && k % 64 == 0 && gemm3_rows(args) == 256) &&
+      (bf16_out || residual_program(args, nullptr)) &&
+      m >= 512 && k % 32 == 0 && a->sc == 1 && (int64_t)args.chunks * args.nruns * 2048 < (1ll << 32)) {
     const int64_t tiles = (int64_t)args.chunks * args.nruns * (b_batch > 1 ? b_batch : 1);
     void *bt16 = runtime_scratch(r, (size_t)tiles * 2048);
     if (bt16) {
@@ -2491,7 +2581,10 @@ extern "C" int bt_matmul_swiglu(bt_runtime *rt, const bt_operand *a, int b_fmt, 
     BT_LAUNCHED("matmul_swiglu");
     return BT_OK;
   }
-  if (b_fmt != BT_BF16) {  // unpacked once into bf16 tiles in the runtime's scratch
+  // bfp4 B with K in whole chunks: read as it is stored by the GEMM itself; other block floats unpacked once into bf16
+  // tiles in the runtime's scratch
+  const bool q4 = b_fmt == BT_BFP4 && k % 64 == 0;
+  if (b_fmt != BT_BF16 && !q4) {
     const int64_t tiles = (int64_t)args.chunks * args.nruns;
     void *bt16 = runtime_scratch(r, (size_t)tiles * 2048);
     if (!bt16) return fail(BT_ESTATE, "matmul_swiglu: no scratch for B's bf16 tiles (inside a capture, or out of memory)");
@@ -2511,13 +2604,17 @@ extern "C" int bt_matmul_swiglu(bt_runtime *rt, const bt_operand *a, int b_fmt, 
     for (int t = 1; t < nb && mb128 * t <= 256; t++)
       if ((mb * (nb - t)) % 256 == 0) { tail = t; break; }
   }
-  gemm3_kernel<BT_BF16, 4, GEMM_SWIGLU><<<(unsigned)((int64_t)mb * (nb - tail)), 512, 0, r->stream>>>(args, mb, nb - tail,
-                                                                                                  bt_operand{}, 0);
+  const unsigned blocks = (unsigned)((int64_t)mb * (nb - tail));
+  if (q4) gemm3_kernel<BT_BFP4, BT_BF16, 4, GEMM_SWIGLU><<<blocks, 512, 0, r->stream>>>(args, mb, nb - tail, bt_operand{}, 0);
+  else gemm3_kernel<BT_BF16, BT_BF16, 4, GEMM_SWIGLU><<<blocks, 512, 0, r->stream>>>(args, mb, nb - tail, bt_operand{}, 0);
   BT_LAUNCHED("matmul_swiglu");
   if (tail) {
     const int mb128 = (int)((m + 127) / 128);
-    gemm3_kernel<BT_BF16, 4, GEMM_SWIGLU, 128><<<(unsigned)((int64_t)mb128 * tail), 512, 0, r->stream>>>(
-        args, mb128, tail, bt_operand{}, nb - tail);
+    const unsigned tb = (unsigned)((int64_t)mb128 * tail);
+    if (q4)
+      gemm3_kernel<BT_BFP4, BT_BF16, 4, GEMM_SWIGLU, 128><<<tb, 512, 0, r->stream>>>(args, mb128, tail, bt_operand{}, nb - tail);
+    else
+      gemm3_kernel<BT_BF16, BT_BF16, 4, GEMM_SWIGLU, 128><<<tb, 512, 0, r->stream>>>(args, mb128, tail, bt_operand{}, nb - tail);
     BT_LAUNCHED("matmul_swiglu");
   }
   return BT_OK;

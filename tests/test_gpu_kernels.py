@@ -267,9 +267,10 @@ def test_split_k_rows(rt, fmt, m, k, n, out):
 # (rows, K, N, output): rows > 64 run the tiled GEMM, except up to 256 rows when its 128 x 128 blocks would be fewer
 # than 128 (then the skinny kernel: 96 x 1536 here). With bf16 B (block floats unpacked to it from 512 rows up) and
 # K in 32s, 2048 x 8192 takes 256 x 256 blocks, 2048 x 4096 (fp32 with the residual) and 1000 x 4096 blocks of 128
-# rows; 1000 and 520 leave partial blocks, chunks of K and runs of N.
+# rows; 1000 and 520 leave partial blocks, chunks of K and runs of N. bfp4 B with K in whole chunks (256, 192, 640)
+# is read by the GEMM as it is stored from 512 rows up.
 GEMM_CASES = [(300, 1000, 520, "bf16"), (96, 576, 1536, "fp32"), (2048, 256, 8192, "bf16"), (2048, 192, 4096, "fp32"),
-              (160, 320, 8192, "bf16"), (1000, 224, 4096, "bf16")]
+              (160, 320, 8192, "bf16"), (1000, 224, 4096, "bf16"), (520, 640, 1296, "fp32")]
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bfp4"])
@@ -299,6 +300,43 @@ def test_gemm_equals_row_slices(rt, fmt, case):
   else: assert np.array_equal(got, (plain + res).astype(np.float32))
   xw = B.bf16(x)
   assert np.all(np.abs(plain - ops.matmul(xw, wq)) <= ops.matmul_bound(xw, wq))
+
+
+@pytest.mark.parametrize("m,k,n,out", [(520, 640, 1296, "fp32"), (2048, 192, 4096, "bf16")])
+def test_gemm_under_capture_reads_bfp4_as_stored(chip, m, k, n, out):
+  # A fresh runtime has no scratch, and a capture can't grow it, so a prefill-sized bfp4 product recorded in a graph
+  # takes the GEMM that decodes B's tiles as it stages them (128-row blocks here, which the eager product gives to
+  # the GEMM on B unpacked to bf16): the replay equals the eager product bit for bit
+  from baretile_amd.runtime import Runtime
+  rt = Runtime(chip)
+  try:
+    rng = np.random.default_rng(m + n)
+    x, w = rng.normal(0, 1, (m, k)), rng.normal(0, 0.05, (k, n)).astype(np.float32)
+    exps, vals = pack(rt, w, "bfp4")
+    cols = columns(rt, exps, vals, "bfp4", 1, k, n)
+    a = _lib.operand(up(rt, B.bf16_bits(x)), "bf16", m * k, k, 1)
+    size = 2 if out == "bf16" else 4
+    o = rt.dram_alloc(m * n * size)
+    rt.wait()
+    g = ctypes.c_void_p()
+    _lib.call("graph_begin", rt.handle)
+    try:
+      _lib.call("matmul", rt.handle, ctypes.byref(a), _lib.BFP4, cols, 1, 1, m, k, n, None,
+                ctypes.byref(_lib.operand(o, out, m * n, n, 1)))
+    finally:
+      _lib.call("graph_end", rt.handle, ctypes.byref(g))
+    try:
+      for _ in range(2):
+        rt.upload(o, b"\xff" * (m * n * size))
+        _lib.call("graph_launch", rt.handle, g)
+        rt.wait()
+        got = down(rt, o, (m, n), np.uint16 if out == "bf16" else np.float32).copy()
+        want = matmul(rt, x, cols, "bfp4", 1, n, out=out)[0]
+        assert np.array_equal(bits_to_float(got) if out == "bf16" else got, want)
+    finally:
+      _lib.call("graph_destroy", g)
+  finally:
+    rt.close()
 
 
 def test_epilogue_reads_other_inputs(rt):
