@@ -854,9 +854,12 @@ static int plan_attention(const bt_attention_args *a, AttnPlan *p) {
     int parts = a->parts;
     // bf16: one block a CU (MI355X's 256), each wave's loads a block ahead through all of its share of the keys;
     // block floats: two a CU, so one block's decoding overlaps the other's loads. Measured faster than more,
-    // shorter-lived blocks at 1-32 batch entries and 4096-16384 keys.
+    // shorter-lived blocks at 1-32 batch entries and 4096-16384 keys. A part's keys are a chain of dependent loads,
+    // so up to 32 blocks of 64 keys, parts of two blocks (and the combine's launch) beat longer ones; beyond, four;
+    // up to 4 blocks, one part (no combine) is the fastest.
     const int target = a->kv_fmt == BT_BF16 ? 256 : 512;
-    if (parts == 0) parts = std::min((target + kvh * p->tiles / 2) / (kvh * p->tiles), (nblk + 3) / 4);
+    const int per_part = nblk <= 4 ? nblk : nblk <= 32 ? 2 : 4;
+    if (parts == 0) parts = std::min((target + kvh * p->tiles / 2) / (kvh * p->tiles), std::max(1, nblk / per_part));
     p->parts = std::max(1, std::min(std::min(parts, nblk), MAX_PARTS));
     const int pf = 32 + 16 * a->head_dim;
     if (p->parts > 1) p->scratch_bytes = (uint64_t)kvh * p->tiles * p->parts * pf * 4;
