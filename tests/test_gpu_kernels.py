@@ -187,12 +187,12 @@ def test_bfp_matmul_is_bf16_matmul_of_its_values(rt, fmt):
 @pytest.mark.parametrize("fmt", ["bfp8", "bfp4"])
 @pytest.mark.parametrize("rows", [1, 4, 16])
 def test_decode_gemv_lm_head_shape(rt, fmt, rows):
-  # BASELINE config 2's GEMV, x [B, 576] @ W [576, N] with N cut to 8192 to keep the oracle quick
+  # BASELINE config 2's GEMV at its full size, x [B, 576] @ W [576, 49152]
   rng = np.random.default_rng(0)
-  x, w = rng.normal(0, 1, (rows, 576)), rng.normal(0, 0.02, (576, 8192)).astype(np.float32)
+  x, w = rng.normal(0, 1, (rows, 576)), rng.standard_normal((576, 49152), dtype=np.float32) * np.float32(0.02)
   exps, vals = pack(rt, w, fmt)
-  cols = columns(rt, exps, vals, fmt, 1, 576, 8192)
-  got = matmul(rt, x, cols, fmt, 1, 8192)[0]
+  cols = columns(rt, exps, vals, fmt, 1, 576, 49152)
+  got = matmul(rt, x, cols, fmt, 1, 49152)[0]
   xw, wq = B.bf16(x), B.bfp(w, fmt)
   assert np.all(np.abs(got - ops.matmul(xw, wq)) <= ops.matmul_bound(xw, wq))
 
@@ -453,6 +453,35 @@ def test_attention_matches_oracle(rt, case):
   got = attend(rt, q, k, v, places, window, parts)
   want = ops.attention(q, k, v, places[..., None], window, rep)
   assert np.allclose(got, want, rtol=0.011, atol=0.011), (case, np.abs(got - want).max())
+
+
+@pytest.mark.parametrize("keys", [512, 4096, 16384])
+def test_attention_config4_batch8_decode(rt, keys):
+  # BASELINE config 4's decode at batch 8 (32 query and 8 key heads of 128 a batch entry, the entries as extra heads
+  # of one call, each over its own full cache), against the oracle entry by entry
+  rng = np.random.default_rng(keys)
+  q = B.bf16(rng.standard_normal((256, 1, 128), dtype=np.float32) / np.float32(np.sqrt(128)))
+  k = B.bf16(rng.standard_normal((64, keys, 128), dtype=np.float32))
+  v = B.bf16(rng.standard_normal((64, keys, 128), dtype=np.float32))
+  places = np.full((256, 1), keys - 1)
+  got = attend(rt, q, k, v, places)
+  for e in range(8):
+    want = ops.attention(q[32 * e:32 * e + 32], k[8 * e:8 * e + 8], v[8 * e:8 * e + 8], places[:32, :, None], 0, 4)
+    assert np.allclose(got[32 * e:32 * e + 32], want, rtol=0.011, atol=0.011), (e, np.abs(got[32 * e:32 * e + 32] - want).max())
+
+
+def test_attention_config4_causal_prefill(rt):
+  # BASELINE config 4's prefill: 2048 rows over their own 2048 keys, causal, 32 query and 8 key heads of 128, against
+  # the oracle one key head (and its 4 query heads) at a time
+  rng = np.random.default_rng(2048)
+  q = B.bf16(rng.standard_normal((32, 2048, 128), dtype=np.float32) / np.float32(np.sqrt(128)))
+  k = B.bf16(rng.standard_normal((8, 2048, 128), dtype=np.float32))
+  v = B.bf16(rng.standard_normal((8, 2048, 128), dtype=np.float32))
+  places = np.broadcast_to(np.arange(2048), (32, 2048))
+  got = attend(rt, q, k, v, places)
+  for h in range(8):
+    want = ops.attention(q[4 * h:4 * h + 4], k[h:h + 1], v[h:h + 1], places[4 * h:4 * h + 4, :, None], 0, 4)
+    assert np.allclose(got[4 * h:4 * h + 4], want, rtol=0.011, atol=0.011), (h, np.abs(got[4 * h:4 * h + 4] - want).max())
 
 
 @pytest.mark.parametrize("slots,rep,part", [(4, 3, 100), (8, 4, 256), (16, 4, 64)])
