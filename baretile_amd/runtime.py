@@ -13,7 +13,9 @@ from baretile_amd import _lib
 
 class Bound(int):
   """A launch argument that a replay can replace, such as the address of a jit input (runtime.py:476-482). key names
-  it in a binding."""
+  it in a binding. Kept for code written against the reference's runtime; this backend's jit needs no bound arguments,
+  since a HIP graph's kernel arguments are fixed at capture: a replay copies each input into the recording's own
+  buffer instead."""
   def __new__(cls, value, key):
     self = super().__new__(cls, value)
     self.key = key

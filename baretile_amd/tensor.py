@@ -16,7 +16,6 @@ import array, ctypes, functools, math, operator, struct, weakref
 import numpy as np
 from baretile_amd import _lib
 from baretile_amd.program import Program
-from baretile_amd.runtime import Bound
 
 FIDELITY = 4  # the reference's default phase count: exact bf16 products, which the matrix cores always give
 DIMS = 5
