@@ -302,6 +302,22 @@ def test_gemm_equals_row_slices(rt, fmt, case):
   assert np.all(np.abs(plain - ops.matmul(xw, wq)) <= ops.matmul_bound(xw, wq))
 
 
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4"])
+def test_batched_gemm_block_float_b(rt, fmt):
+  # a batch of two products, each against its own block-float B (bfp4: the GEMM reads B's tiles as stored, matrix b
+  # at b times a matrix's tile bytes), equals bit for bit the batched product with the bf16 values of B
+  rng = np.random.default_rng(31)
+  b, m, k, n = 2, 768, 256, 4096
+  x, w = rng.normal(0, 1, (b, m, k)), rng.normal(0, 0.05, (b, k, n)).astype(np.float32)
+  exps, vals = pack(rt, w, fmt)
+  got = matmul(rt, x, columns(rt, exps, vals, fmt, b, k, n), fmt, b, n)
+  want = matmul(rt, x, bf16_columns(rt, bfp_values(w, fmt)), "bf16", b, n)
+  assert np.array_equal(got, want)
+  xw = B.bf16(x)
+  for i in range(b):
+    assert np.all(np.abs(got[i] - ops.matmul(xw[i], bfp_values(w[i], fmt))) <= ops.matmul_bound(xw[i], bfp_values(w[i], fmt)))
+
+
 @pytest.mark.parametrize("m,k,n,out", [(520, 640, 1296, "fp32"), (2048, 192, 4096, "bf16")])
 def test_gemm_under_capture_reads_bfp4_as_stored(chip, m, k, n, out):
   # A fresh runtime has no scratch, and a capture can't grow it, so a prefill-sized bfp4 product recorded in a graph
