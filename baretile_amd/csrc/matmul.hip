@@ -1530,12 +1530,16 @@ constexpr int GEMM_PLAIN = 0, GEMM_RES = 1, GEMM_SWIGLU = 2;
 // chunk and decodes each half into bf16 fragments in registers (q * 2^(e - 129) by subtracting exponent gaps, the
 // values the unpacker gives), so B crosses HBM and LDS at 0.28 of its bf16 size and needs no unpacking pass. The
 // sums run in the same order, so the result is the same bits as the bf16 GEMM on B's unpacked tiles.
-template <int FMT, int DT, int S, int MODE = GEMM_PLAIN, int BM = 256>
+// BN: the block's columns, 256 or 192 (each wave BN / 4 of them; the stages keep room for 16 tiles either way, and the
+// slots of missing tiles take loads that read nothing, so every wave issues the same loads), for products whose
+// 256-column blocks would leave a round of the CUs part empty (6144 columns: 256 blocks of 256 x 192 instead of 192).
+template <int FMT, int DT, int S, int MODE = GEMM_PLAIN, int BM = 256, int BN = 256>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand res, int nb_off = 0) {
   static_assert(FMT == BT_BF16 || FMT == BT_BFP4, "gemm3 takes bf16 or bfp4 B");
+  static_assert(BN == 256 || (BN == 192 && MODE != GEMM_SWIGLU), "gemm3 blocks are 256 or 192 columns");
   constexpr bool RES = MODE == GEMM_RES;
-  constexpr int BN = 256, A_BYTES = BM * 64, STAGE = A_BYTES + 16384, WM = BM / 32, WN = 4, WR = BM / 2;
+  constexpr int A_BYTES = BM * 64, STAGE = A_BYTES + 16384, WM = BM / 32, WN = BN / 64, WR = BM / 2, T = BN / 16;
   constexpr int AL = BM / 128;  // A loads a wave issues a step
   constexpr int CS = 3, QTB = 576, QA = BM * 128, QSTAGE = QA + 16 * QTB, QAL = BM / 64;  // bfp4: chunk stages
   constexpr int RING = FMT == BT_BF16 ? S * STAGE : CS * QSTAGE;
@@ -1563,7 +1567,7 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
   // the run of B whose tile the block's tile li (0..15) is, and whether it exists
   auto b_run = [&](int li, bool &in) {
     int run = n0 / 16 + li;
-    in = run < h.nruns;
+    in = li < T && run < h.nruns;
     if (MODE == GEMM_SWIGLU) {  // tiles 0..7: gate columns from 128 bn, 8..15: the same up columns
       const int f = h.n / 2, c0 = bn * 128 + 16 * (li & 7);
       run = ((li < 8 ? 0 : f) + c0) / 16;
@@ -1619,7 +1623,7 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
       fa[i] = *(const bf16x8 *)(st + r * 64 + 16 * (g ^ ((r >> 1) & 3)));
     }
 #pragma unroll
-    for (int j = 0; j < WN; j++) fb[j] = *(const bf16x8 *)(st + A_BYTES + (wn * 4 + j) * 1024 + lane * 16);
+    for (int j = 0; j < WN; j++) fb[j] = *(const bf16x8 *)(st + A_BYTES + (wn * WN + j) * 1024 + lane * 16);
 #pragma unroll
     for (int i = 0; i < WM; i++)
 #pragma unroll
@@ -1665,7 +1669,7 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
       uint4 e[WN];
 #pragma unroll
       for (int j = 0; j < WN; j++) {
-        const uint8_t *tile = st + QA + (wn * 4 + j) * QTB;
+        const uint8_t *tile = st + QA + (wn * WN + j) * QTB;
         q[j] = *(const uint2 *)(tile + 64 + 8 * lane);
         e[j] = *(const uint4 *)(tile + 16 * g);
       }
@@ -1700,7 +1704,7 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
         if (m >= h.m) continue;
 #pragma unroll
         for (int j = 0; j < WN; j++) {
-          const int n = n0 + wn * 64 + 16 * j + col;
+          const int n = n0 + wn * 16 * WN + 16 * j + col;
           if (n >= h.n) continue;
           float v = acc[i][j][r];
           if (res.ptr) v += ((const float *)res.ptr)[rb + (int64_t)m * res.sr + (int64_t)n * res.sc];
@@ -1720,7 +1724,7 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
         for (int j = 0; j < WN; j++)
 #pragma unroll
           for (int r = 0; r < 4; r++) {
-            uint8_t *at = lds + ((BM == HALF ? wm * WR : 0) + 16 * i + 4 * g + r) * ES + (wn * 64 + 16 * j + col) * ESZ;
+            uint8_t *at = lds + ((BM == HALF ? wm * WR : 0) + 16 * i + 4 * g + r) * ES + (wn * 16 * WN + 16 * j + col) * ESZ;
             if (DT == BT_FP32) *(float *)at = acc[i][j][r];
             else *(uint16_t *)at = (uint16_t)bf16_packed(acc[i][j][r]);
           }
@@ -2285,14 +2289,20 @@ static bool residual_program(const MatmulArgs &args, bt_operand *res) {
   return true;
 }
 
-// gemm3's block rows: 256 or 128, whichever fills the CUs' rounds better, 128-row blocks counted at 0.85 of the
-// speed.
-static int gemm3_rows(const MatmulArgs &args) {
-  auto fill = [&](int bm) {
-    const int64_t blocks = (int64_t)args.batch * ((args.m + bm - 1) / bm) * ((args.n + 255) / 256);
-    return (double)blocks / (double)((blocks + 255) / 256 * 256);
-  };
-  return fill(256) >= 0.85 * fill(128) ? 256 : 128;
+// gemm3's block shape: 256 x 256, 256 x 192 or 128 x 256, whichever fills the CUs' rounds best, a full round of the
+// smaller blocks counted at 0.9 and 0.85 of the speed of one of 256 x 256.
+struct Gemm3Shape { int bm, bn; };
+static Gemm3Shape gemm3_shape(const MatmulArgs &args) {
+  const Gemm3Shape opts[3] = {{256, 256}, {256, 192}, {128, 256}};
+  const double eff[3] = {1.0, 0.9, 0.85};
+  int best = 0;
+  double score = -1.0;
+  for (int o = 0; o < 3; o++) {
+    const int64_t blocks = (int64_t)args.batch * ((args.m + opts[o].bm - 1) / opts[o].bm) * ((args.n + opts[o].bn - 1) / opts[o].bn);
+    const double sc = eff[o] * (double)blocks / (double)((blocks + 255) / 256 * 256);
+    if (sc > score + 1e-9) score = sc, best = o;
+  }
+  return opts[best];
 }
 
 // The block shape for a GEMM: the largest tile whose grid still keeps the chip's 256 CUs busy through its last round.
@@ -2317,15 +2327,17 @@ static void launch_gemm_dt(const MatmulArgs &args, hipStream_t s) {
     const bool fits = FMT == BT_BF16 ? args.m > 128 && args.k % 32 == 0
                                      : args.m >= 512 && args.k % 64 == 0 && (int64_t)args.chunks * args.nruns * 576 < (1ll << 32);
     if (fits && (DT == BT_BF16 || residual_program(args, &res))) {
-      const int bm = gemm3_rows(args);
-      const int mb = (args.m + bm - 1) / bm, nb = (args.n + 255) / 256;
+      const Gemm3Shape sh = gemm3_shape(args);
+      const int mb = (args.m + sh.bm - 1) / sh.bm, nb = (args.n + sh.bn - 1) / sh.bn;
       const unsigned blocks = (unsigned)((int64_t)mb * nb * args.batch);
       if constexpr (DT == BT_BF16) {
-        if (bm == 256) gemm3_kernel<FMT, DT, 4><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
-        else gemm3_kernel<FMT, DT, 4, GEMM_PLAIN, 128><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
+        if (sh.bm == 128) gemm3_kernel<FMT, DT, 4, GEMM_PLAIN, 128><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
+        else if (sh.bn == 192) gemm3_kernel<FMT, DT, 4, GEMM_PLAIN, 256, 192><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
+        else gemm3_kernel<FMT, DT, 4><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
       } else {
-        if (bm == 256) gemm3_kernel<FMT, DT, 4, GEMM_RES><<<blocks, 512, 0, s>>>(args, mb, nb, res);
-        else gemm3_kernel<FMT, DT, 4, GEMM_RES, 128><<<blocks, 512, 0, s>>>(args, mb, nb, res);
+        if (sh.bm == 128) gemm3_kernel<FMT, DT, 4, GEMM_RES, 128><<<blocks, 512, 0, s>>>(args, mb, nb, res);
+        else if (sh.bn == 192) gemm3_kernel<FMT, DT, 4, GEMM_RES, 256, 192><<<blocks, 512, 0, s>>>(args, mb, nb, res);
+        else gemm3_kernel<FMT, DT, 4, GEMM_RES><<<blocks, 512, 0, s>>>(args, mb, nb, res);
       }
       return;
     }
@@ -2405,7 +2417,7 @@ extern "C" int bt_matmul(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_
   // tiles in the runtime's scratch (the same values bit for bit), then the bf16 GEMM. bfp4 B in whole chunks goes to
   // the same GEMM reading it as it is stored, decoded in registers.
   const bool bf16_out = out->dtype == BT_BF16 && (!epilogue || epilogue->dtype != BT_FP32);
-  if (b_fmt != BT_BF16 && !(b_fmt == BT_BFP4 && k % 64 == 0 && gemm3_rows(args) == 256) &&
+  if (b_fmt != BT_BF16 && !(b_fmt == BT_BFP4 && k % 64 == 0 && gemm3_shape(args).bm == 256) &&
       (bf16_out || residual_program(args, nullptr)) &&
       m >= 512 && k % 32 == 0 && a->sc == 1 && (int64_t)args.chunks * args.nruns * 2048 < (1ll << 32)) {
     const int64_t tiles = (int64_t)args.chunks * args.nruns * (b_batch > 1 ? b_batch : 1);

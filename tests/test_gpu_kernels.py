@@ -268,9 +268,11 @@ def test_split_k_rows(rt, fmt, m, k, n, out):
 # than 128 (then the skinny kernel: 96 x 1536 here). With bf16 B (block floats unpacked to it from 512 rows up) and
 # K in 32s, 2048 x 8192 takes 256 x 256 blocks, 2048 x 4096 (fp32 with the residual) and 1000 x 4096 blocks of 128
 # rows; 1000 and 520 leave partial blocks, chunks of K and runs of N. bfp4 B with K in whole chunks (256, 192, 640)
-# is read by the GEMM as it is stored from 512 rows up.
+# is read by the GEMM as it is stored from 512 rows up. 2048 x 6144 takes blocks of 256 x 192 (256 of them, one round
+# of the CUs, where 256 x 256 would leave a quarter idle).
 GEMM_CASES = [(300, 1000, 520, "bf16"), (96, 576, 1536, "fp32"), (2048, 256, 8192, "bf16"), (2048, 192, 4096, "fp32"),
-              (160, 320, 8192, "bf16"), (1000, 224, 4096, "bf16"), (520, 640, 1296, "fp32")]
+              (160, 320, 8192, "bf16"), (1000, 224, 4096, "bf16"), (520, 640, 1296, "fp32"), (2048, 320, 6144, "bf16"),
+              (2048, 192, 6144, "fp32")]
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bfp4"])
