@@ -460,6 +460,56 @@ __global__ void __launch_bounds__(256) rope_put_kernel(const bt_rope_args a) {
   dst[j + half] = (uint16_t)bf16_packed(y2);
 }
 
+// The same, 8 neighbouring pairs a thread with 16-byte loads and stores and 32-bit index arithmetic: for head widths
+// a multiple of 16 with every row and head on a 16-byte boundary. Element by element the arithmetic of
+// rope_put_kernel. hq divides by the head's 8-pair groups, nh by the heads.
+__global__ void __launch_bounds__(256) rope_put8_kernel(const bt_rope_args a, const FastDiv hq, const FastDiv nh,
+                                                        uint32_t threads) {
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  if (t >= threads) return;
+  const int half = a.head_dim / 2;
+  const uint32_t th = fdiv(t, hq), ti = fdiv(th, nh);
+  const int j = 8 * (int)(t - th * hq.d), hh = (int)(th - ti * nh.d), i = (int)ti;
+  const uint16_t *x = (const uint16_t *)(uintptr_t)a.qkv + (int64_t)i * a.qkv_sr + (int64_t)hh * a.head_dim;
+  const uint16_t *cs = (const uint16_t *)(uintptr_t)a.cos + (int64_t)i * a.cs_sr + (int64_t)hh * a.head_dim;
+  const uint16_t *sn = (const uint16_t *)(uintptr_t)a.sin + (int64_t)i * a.cs_sr + (int64_t)hh * a.head_dim;
+  const uint4 xa = *(const uint4 *)(x + j), xb = *(const uint4 *)(x + j + half);
+  const uint4 ca = *(const uint4 *)(cs + j), cb = *(const uint4 *)(cs + j + half);
+  const uint4 sa = *(const uint4 *)(sn + j), sb = *(const uint4 *)(sn + j + half);
+  const uint32_t xw[2][4] = {{xa.x, xa.y, xa.z, xa.w}, {xb.x, xb.y, xb.z, xb.w}};
+  const uint32_t cw[2][4] = {{ca.x, ca.y, ca.z, ca.w}, {cb.x, cb.y, cb.z, cb.w}};
+  const uint32_t sw[2][4] = {{sa.x, sa.y, sa.z, sa.w}, {sb.x, sb.y, sb.z, sb.w}};
+  uint32_t o[2][4];
+#pragma unroll
+  for (int w = 0; w < 4; w++) {
+    o[0][w] = o[1][w] = 0u;
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      const int sh = 16 * e;
+      const float x1 = bf16_value(xw[0][w] >> sh & 0xFFFFu), x2 = bf16_value(xw[1][w] >> sh & 0xFFFFu);
+      const float y1 = __fsub_rn(__fmul_rn(x1, bf16_value(cw[0][w] >> sh & 0xFFFFu)),
+                                 __fmul_rn(x2, bf16_value(sw[0][w] >> sh & 0xFFFFu)));
+      const float y2 = __fadd_rn(__fmul_rn(x2, bf16_value(cw[1][w] >> sh & 0xFFFFu)),
+                                 __fmul_rn(x1, bf16_value(sw[1][w] >> sh & 0xFFFFu)));
+      o[0][w] |= bf16_packed(y1) << sh;
+      o[1][w] |= bf16_packed(y2) << sh;
+    }
+  }
+  uint16_t *dst;
+  if (hh < a.heads) {
+    dst = (uint16_t *)(uintptr_t)a.q + (int64_t)i * a.q_sr + (int64_t)hh * a.head_dim;
+  } else {
+    const int place = ((const int32_t *)(uintptr_t)a.places)[a.one_place ? 0 : i];
+    if (place < 0 || place >= a.cache_rows) return;
+    const int hk = hh - a.heads;
+    const bool own = a.vcache && hk >= a.kv;
+    dst = (uint16_t *)(uintptr_t)(own ? a.vcache : a.cache) + (int64_t)(own ? hk - a.kv : hk) * a.cache_sh +
+          (int64_t)i * a.cache_tsh + (int64_t)place * a.cache_sr;
+  }
+  *(uint4 *)(dst + j) = make_uint4(o[0][0], o[0][1], o[0][2], o[0][3]);
+  *(uint4 *)(dst + j + half) = make_uint4(o[1][0], o[1][1], o[1][2], o[1][3]);
+}
+
 }  // namespace bt
 
 extern "C" int bt_rope_put(bt_runtime *rt, const bt_rope_args *args) {
@@ -473,7 +523,15 @@ extern "C" int bt_rope_put(bt_runtime *rt, const bt_rope_args *args) {
     return fail(BT_EINVAL, "rope_put shape: %d rows, %d heads, %d key heads of %d", a.rows, a.heads, a.kv, a.head_dim);
   const int64_t threads = (int64_t)a.rows * (a.heads + 2 * a.kv) * (a.head_dim / 2);
   if (threads >= (1ll << 31)) return fail(BT_EINVAL, "rope_put too large");
-  rope_put_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, r->stream>>>(a);
+  const bool aligned = a.head_dim % 16 == 0 && (a.qkv | a.cos | a.sin | a.q | a.cache | a.vcache) % 16 == 0 &&
+                       (a.qkv_sr | a.cs_sr | a.q_sr | a.cache_sh | a.cache_sr | a.cache_tsh) % 8 == 0;
+  if (aligned) {
+    const uint32_t t8 = (uint32_t)(threads / 8);
+    rope_put8_kernel<<<(t8 + 255) / 256, 256, 0, r->stream>>>(a, make_fastdiv((uint32_t)(a.head_dim / 16)),
+                                                               make_fastdiv((uint32_t)(a.heads + 2 * a.kv)), t8);
+  } else {
+    rope_put_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, r->stream>>>(a);
+  }
   BT_LAUNCHED("rope_put");
   return BT_OK;
 }

@@ -335,6 +335,30 @@ def test_rope_put(rt, hd):
   assert not np.any(got_c[:, others])
 
 
+def test_rope_put_aligned_and_unaligned_rows_agree(rt):
+  # 16-byte aligned rows take the kernel that moves 8 pairs a thread; rows 4 values longer than their heads (a view
+  # of a wider tensor: row strides that aren't a multiple of 8) take the one pair a thread kernel. Same bits.
+  from baretile_amd.models import llama
+  heads, kv, hd, rows, size = 8, 2, 128, 37, 64
+  nh = heads + 2 * kv
+  c = llama.model(dim=heads * hd, heads=heads, kv=kv, layers=1, eps=1e-5, theta=10000.0, head_dim=hd)
+  cos, sin, _ = llama.rotary(c, size)
+  rng = np.random.default_rng(9)
+  x = rng.normal(0, 1, (rows, nh * hd)).astype(np.float32)
+  places = [int(p) for p in rng.permutation(size)[:rows]]
+  wide = lambda a: np.concatenate([a, np.zeros((rows, 4), a.dtype)], 1)
+  out = []
+  for pad in (False, True):
+    xs, cs, sn = x, cos[places], sin[places]
+    tx = Tensor.of(rt, wide(xs) if pad else xs)
+    tc, ts = Tensor.of(rt, wide(cs) if pad else cs), Tensor.of(rt, wide(sn) if pad else sn)
+    if pad: tx, tc, ts = tx[:, :nh * hd], tc[:, :nh * hd], ts[:, :nh * hd]
+    cache = Tensor.zeros(rt, size, hd, batch=2 * kv)
+    q = tx.rope_put(tc, ts, cache, Tensor.of(rt, [places], "int32"), heads, kv)
+    out.append((q.tobytes(), cache.tobytes()))
+  assert out[0] == out[1]
+
+
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bfp4"])
 @pytest.mark.parametrize("k,hd,heads,kv", [(576, 64, 9, 3), (2048, 128, 8, 2), (320, 64, 2, 1)])
 def test_matmul_row_rope_equals_two_calls(rt, fmt, k, hd, heads, kv):
