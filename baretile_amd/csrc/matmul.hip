@@ -130,10 +130,18 @@ __device__ __forceinline__ bf16x8 q4_to_bf16(uint32_t w) {  // q * 2^-9 as bf16,
 // a columns tile stores d = e - 120 as a byte, and 247 - e = 127 - d = d ^ 0x7F bytewise. Exact for run exponents e in
 // 3..247, where every result is a normal bf16.
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t gap_sub(uint32_t bits, uint32_t x, uint32_t sel) {
-  const uint32_t gap = __builtin_amdgcn_perm(0u, x, sel) << 7;  // two gaps, one in each 16-bit half's exponent field
+__device__ __forceinline__ uint32_t sub_placed(uint32_t bits, uint32_t placed) {  // placed: two gaps << 7
   return __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, bits),
-                                                                    __builtin_bit_cast(u16x2, gap)));
+                                                                    __builtin_bit_cast(u16x2, placed)));
+}
+__device__ __forceinline__ uint32_t gap_sub(uint32_t bits, uint32_t x, uint32_t sel) {
+  return sub_placed(bits, __builtin_amdgcn_perm(0u, x, sel) << 7);  // two gaps, one in each half's exponent field
+}
+// A columns tile's exponent bytes d (4 a word) as the gaps 127 - d of values (0, 1) and (2, 3), each pair two 16-bit
+// halves already shifted into the bf16 exponent field: what q4_to_bf16_placed takes.
+__device__ __forceinline__ uint2 place_gaps(uint32_t d) {
+  const uint32_t x = d ^ 0x7F7F7F7Fu;
+  return make_uint2(__builtin_amdgcn_perm(0u, x, 0x0C010C00u) << 7, __builtin_amdgcn_perm(0u, x, 0x0C030C02u) << 7);
 }
 __device__ __forceinline__ bf16x8 q4_to_bf16_gaps(uint32_t w, uint32_t x0, uint32_t x1) {
   uint32_t lo, hi;
@@ -144,6 +152,17 @@ __device__ __forceinline__ bf16x8 q4_to_bf16_gaps(uint32_t w, uint32_t x0, uint3
   const uint32_t c3 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 0x1p127f, true));
   uint4 v = make_uint4(gap_sub(c0, x0, 0x0C010C00u), gap_sub(c1, x0, 0x0C030C02u), gap_sub(c2, x1, 0x0C010C00u),
                        gap_sub(c3, x1, 0x0C030C02u));
+  return *(const bf16x8 *)&v;
+}
+// The same with the gaps of values (0, 1), (2, 3), (4, 5), (6, 7) placed beforehand (place_gaps), in p.x .. p.w.
+__device__ __forceinline__ bf16x8 q4_to_bf16_placed(uint32_t w, uint4 p) {
+  uint32_t lo, hi;
+  q4_to_fp8(w, lo, hi);
+  const uint32_t c0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 0x1p127f, false));
+  const uint32_t c1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 0x1p127f, true));
+  const uint32_t c2 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 0x1p127f, false));
+  const uint32_t c3 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 0x1p127f, true));
+  uint4 v = make_uint4(sub_placed(c0, p.x), sub_placed(c1, p.y), sub_placed(c2, p.z), sub_placed(c3, p.w));
   return *(const bf16x8 *)&v;
 }
 
@@ -1541,7 +1560,8 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
   constexpr bool RES = MODE == GEMM_RES;
   constexpr int A_BYTES = BM * 64, STAGE = A_BYTES + 16384, WM = BM / 32, WN = BN / 64, WR = BM / 2, T = BN / 16;
   constexpr int AL = BM / 128;  // A loads a wave issues a step
-  constexpr int CS = 3, QTB = 576, QA = BM * 128, QSTAGE = QA + 16 * QTB, QAL = BM / 64;  // bfp4: chunk stages
+  // bfp4: chunk stages of A's rows, the 16 tiles as stored, then the tiles' exponents as placed gaps (128 B a tile)
+  constexpr int CS = 3, QTB = 576, QA = BM * 128, QG = QA + 16 * QTB, QSTAGE = QG + 16 * 128, QAL = BM / 64;
   constexpr int RING = FMT == BT_BF16 ? S * STAGE : CS * QSTAGE;
   constexpr int ESZ = DT == BT_FP32 ? 4 : 2, ES = BN * ESZ + 16;
   constexpr int HALF = (DT == BT_FP32 ? 128 : 256) < BM ? (DT == BT_FP32 ? 128 : 256) : BM;
@@ -1662,17 +1682,18 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
     for (int c = 0; c < chunks; c++) {
       if (c + CS - 2 < chunks) wait_vm<(QAL + 2) * (CS - 2)>();
       else wait_vm<0>();
+      uint8_t *st = lds + (c % CS) * QSTAGE;
+      // the exponent bytes of the wave's own two tiles have landed (its loads wrote them): placed as gaps once here,
+      // for every wave that reads the tiles, instead of by each of them (lanes 16 s .. 16 s + 15: tile wib + 8 s)
+      if (lane < 32) {
+        const int s = wib + 8 * (lane >> 4), w = lane & 15;
+        *(uint2 *)(st + QG + s * 128 + 8 * w) = place_gaps(*(const uint32_t *)(st + QA + s * QTB + 4 * w));
+      }
       __syncthreads();
       if (c + CS - 1 < chunks) issue(c + CS - 1);  // into the stage chunk c - 1 used
-      const uint8_t *st = lds + (c % CS) * QSTAGE;
       uint2 q[WN];
-      uint4 e[WN];
 #pragma unroll
-      for (int j = 0; j < WN; j++) {
-        const uint8_t *tile = st + QA + (wn * WN + j) * QTB;
-        q[j] = *(const uint2 *)(tile + 64 + 8 * lane);
-        e[j] = *(const uint4 *)(tile + 16 * g);
-      }
+      for (int j = 0; j < WN; j++) q[j] = *(const uint2 *)(st + QA + (wn * WN + j) * QTB + 64 + 8 * lane);
 #pragma unroll
       for (int hh = 0; hh < 2; hh++) {
         bf16x8 fa[WM], fb[WN];
@@ -1682,9 +1703,9 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
           fa[i] = *(const bf16x8 *)(st + r * 128 + 16 * ((g + 4 * hh) ^ (r & 7)));
         }
 #pragma unroll
-        for (int j = 0; j < WN; j++)
-          fb[j] = q4_to_bf16_gaps(hh ? q[j].y : q[j].x, (hh ? e[j].z : e[j].x) ^ 0x7F7F7F7Fu,
-                                  (hh ? e[j].w : e[j].y) ^ 0x7F7F7F7Fu);
+        for (int j = 0; j < WN; j++)  // values 8 hh .. 8 hh + 7 of lane group g: gaps 16 g + 8 hh ..
+          fb[j] = q4_to_bf16_placed(hh ? q[j].y : q[j].x,
+                                    *(const uint4 *)(st + QG + (wn * WN + j) * 128 + 32 * g + 16 * hh));
 #pragma unroll
         for (int i = 0; i < WM; i++)
 #pragma unroll
