@@ -551,12 +551,14 @@ __global__ void __launch_bounds__(256) rms_rows_kernel(const float *x, int64_t k
   uint16_t *o = out + (int64_t)blockIdx.x * out_sr;
   constexpr int NV = 8;  // 16-byte groups a thread holds: 8 x 4 x 256 = 8192 columns
   float4 v[REGS ? NV : 1];
+  uint2 wv[REGS ? NV : 1];  // the weights, fetched with the row (one trip for both)
   float ss = 0.0f;
   if constexpr (REGS) {
 #pragma unroll
     for (int i = 0; i < NV; i++) {
       const int64_t c = ((int64_t)i * 256 + tid) * 4;
       v[i] = c < k ? *(const float4 *)(xr + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      wv[i] = c < k ? *(const uint2 *)(w + c) : make_uint2(0u, 0u);
     }
 #pragma unroll
     for (int i = 0; i < NV; i++) {
@@ -581,10 +583,9 @@ __global__ void __launch_bounds__(256) rms_rows_kernel(const float *x, int64_t k
     for (int i = 0; i < NV; i++) {
       const int64_t c = ((int64_t)i * 256 + tid) * 4;
       if (c < k) {
-        const uint2 wv = *(const uint2 *)(w + c);
         uint2 ov;
-        ov.x = bf16_packed(v[i].x * r * bf16_value(wv.x & 0xFFFFu)) | bf16_packed(v[i].y * r * bf16_value(wv.x >> 16)) << 16;
-        ov.y = bf16_packed(v[i].z * r * bf16_value(wv.y & 0xFFFFu)) | bf16_packed(v[i].w * r * bf16_value(wv.y >> 16)) << 16;
+        ov.x = bf16_packed(v[i].x * r * bf16_value(wv[i].x & 0xFFFFu)) | bf16_packed(v[i].y * r * bf16_value(wv[i].x >> 16)) << 16;
+        ov.y = bf16_packed(v[i].z * r * bf16_value(wv[i].y & 0xFFFFu)) | bf16_packed(v[i].w * r * bf16_value(wv[i].y >> 16)) << 16;
         *(uint2 *)(o + c) = ov;
       }
     }

@@ -1230,6 +1230,21 @@ __global__ void __launch_bounds__(256) skinny_part_kernel(const MatmulArgs args,
 
 // The sum of an output's splits, in split order, through the matmul's epilogue: one output a thread. SWI: the
 // product's columns are gate then up (n = 2f); the output is silu(g) * u for f columns, g and u rounded to bf16 first.
+// p[0] + p[stride] + ... + p[(splits - 1) * stride], added in that order; the loads of 8 splits at a time are all
+// issued before the first is added (a split past the last reloads the last one's value and isn't added)
+__device__ __forceinline__ float sum_splits(const float *p, int splits, int64_t stride) {
+  float v = 0.0f;
+  for (int s0 = 0; s0 < splits; s0 += 8) {
+    float t[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) t[i] = p[(int64_t)min(s0 + i, splits - 1) * stride];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      if (s0 + i < splits) v = s0 + i == 0 ? t[i] : v + t[i];
+  }
+  return v;
+}
+
 template <int DT, bool SWI>
 __global__ void __launch_bounds__(256) parts_reduce_kernel(const MatmulArgs args, int splits, int rows, const float *part) {
   const int nout = SWI ? args.n / 2 : args.n;
@@ -1238,18 +1253,22 @@ __global__ void __launch_bounds__(256) parts_reduce_kernel(const MatmulArgs args
   const int m = (int)(e / nout), n = (int)(e % nout);
   const int64_t stride = (int64_t)rows * args.n;
   const float *p = part + (int64_t)m * args.n + n;
-  float v = p[0];
-  for (int s = 1; s < splits; s++) v += p[s * stride];
   const bt_operand &out = args.out;
   if constexpr (SWI) {
-    float u = p[nout];
-    for (int s = 1; s < splits; s++) u += p[s * stride + nout];
+    const float v = sum_splits(p, splits, stride), u = sum_splits(p + nout, splits, stride);
     const float gv = bf16_value(bf16_packed(v)), uv = bf16_value(bf16_packed(u));
     ((uint16_t *)out.ptr)[(int64_t)m * out.sr + n] = (uint16_t)bf16_packed(gv / (1.0f + expf(-gv)) * uv);
   } else {
-    const uint32_t x = __float_as_uint(DT == BT_BF16 ? round_packed(v) : v);
-    const int64_t at = (int64_t)m * out.sr + (int64_t)n * out.sc;
-    store_value<DT>(out, at, args.n_inst ? run_program<DT, false>(args.prog, 0, m, n, x) : x);
+    // the epilogue's inputs (a residual) are fetched first, so their loads are in flight with the partials'
+    Coords<1> at;
+    at.b[0] = 0, at.r[0] = m, at.c[0] = n, at.ok[0] = true;
+    prefile pre[1];
+    const bool prog = args.n_inst != 0;
+    if (prog) fetch_inputs<DT, 1>(args.prog, at, pre);
+    const float v = sum_splits(p, splits, stride);
+    uint32_t x[1] = {__float_as_uint(DT == BT_BF16 ? round_packed(v) : v)};
+    if (prog) eval_program<DT, 1, false>(args.prog, pre, x);
+    store_value<DT>(out, (int64_t)m * out.sr + (int64_t)n * out.sc, x[0]);
   }
 }
 
@@ -1275,7 +1294,8 @@ __global__ void __launch_bounds__(256) skinny_stream_kernel(const MatmulArgs arg
   constexpr int C = S::C, TB = S::TB, ROWS = 16 * MT, ABYTES = ROWS * 512, STAGE = ABYTES + 4 * S::BW, D = S::D;
   constexpr int AL = ROWS / 8;      // a wave's A loads a stage (two rows each)
   constexpr int L = AL + S::BL;     // a wave's loads a stage
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[D * STAGE];
+  constexpr int GAPS = FMT == BT_BFP4 ? C * 128 : 0;  // bfp4: a wave's tiles' exponents as placed gaps
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[D * STAGE + 4 * GAPS];
   const Head h = early_head(args);
   const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
   const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1309,9 +1329,15 @@ __global__ void __launch_bounds__(256) skinny_stream_kernel(const MatmulArgs arg
   f32x4 acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; t++) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  uint8_t *gp = lds + D * STAGE + wib * GAPS;
   auto multiply = [&](int st) {
     const uint8_t *slot = lds + (st % D) * STAGE;
     const uint8_t *bs = slot + ABYTES + wib * S::BW;
+    if (FMT == BT_BFP4) {  // once for the wave's 64 lanes, not by each lane for its own 8 values (C = 4: lane l
+      static_assert(FMT != BT_BFP4 || C == 4, "one exponent word a lane");  // places tile l / 16's word l % 16)
+      *(uint2 *)(gp + (lane >> 4) * 128 + 8 * (lane & 15)) =
+          place_gaps(*(const uint32_t *)(bs + (lane >> 4) * TB + 4 * (lane & 15)));
+    }
 #pragma unroll
     for (int i = 0; i < C; i++) {
       const uint8_t *tile = bs + i * TB;
@@ -1326,9 +1352,8 @@ __global__ void __launch_bounds__(256) skinny_stream_kernel(const MatmulArgs arg
         bv[1] = q8_to_bf16<true>(make_uint2(q.z, q.w), make_uint2(e.z, e.w));
       } else {
         const uint2 q = *(const uint2 *)(tile + 64 + 8 * lane);
-        const uint4 e = *(const uint4 *)(tile + 16 * g);
-        bv[0] = q4_to_bf16_gaps(q.x, e.x ^ 0x7F7F7F7Fu, e.y ^ 0x7F7F7F7Fu);
-        bv[1] = q4_to_bf16_gaps(q.y, e.z ^ 0x7F7F7F7Fu, e.w ^ 0x7F7F7F7Fu);
+        bv[0] = q4_to_bf16_placed(q.x, *(const uint4 *)(gp + i * 128 + 32 * g));
+        bv[1] = q4_to_bf16_placed(q.y, *(const uint4 *)(gp + i * 128 + 32 * g + 16));
       }
 #pragma unroll
       for (int t = 0; t < MT; t++) {
