@@ -1272,7 +1272,7 @@ __global__ void __launch_bounds__(256) parts_reduce_kernel(const MatmulArgs args
   }
 }
 
-// 5 to 32 rows of one A (K a multiple of 256) against B streamed once. Block (group, split) takes 4 runs of B, a wave
+// 5 to 32 rows of one A (K a multiple of 256) against B streamed once. Block (group, split) takes W runs of B, a wave
 // each, over its split's stages of 4 chunks (256 rows of K). Every load goes straight into LDS, whole and aligned: a
 // stage of a run's tiles is one contiguous stretch (4 x 576 bytes for bfp4), loaded 1 KB a wave instruction, and each
 // 512-byte row of A for the stage half an instruction, each 16-byte unit of row r placed at unit u ^ (r % 16) so that
@@ -1281,43 +1281,48 @@ __global__ void __launch_bounds__(256) parts_reduce_kernel(const MatmulArgs args
 // (loads complete in order). A wave decodes its B values and exponents out of LDS. Every run sums its chunks in the
 // same order as the other kernels (a chunk's lower 32 rows, then its upper 32), in one accumulator over the split.
 // EPI 0 writes fp32 partial tiles for parts_reduce_kernel (more than one split); 1 stores through the matmul's
-// epilogue (one split); 2 is SiLU x up (one split): waves 0 and 1 take gate runs 2j and 2j + 1, waves 2 and 3 the up
-// runs at the same columns of the other half, and the up tiles reach the gate waves through LDS.
+// epilogue (one split); 2 is SiLU x up (one split): the first W / 2 waves take gate runs, the others the up runs at
+// the same columns of the other half, and the up tiles reach the gate waves through LDS.
 template <int FMT> struct Stream {
   static constexpr int C = 4, TB = Tile<FMT>::bytes, BW = C * TB;  // a wave's B bytes a stage
   static constexpr int BL = (BW + 1023) / 1024, BLAST = (BW - (BL - 1) * 1024) / 16;  // its loads; the last one's lanes
-  static constexpr int D = FMT == BT_BFP4 ? 3 : 2;  // ring stages: at most 80 KB, two blocks a CU
+  static constexpr int D = FMT == BT_BFP4 ? 3 : 2;  // ring stages
+  // waves (runs) a block: bfp4 8, so that each stage of A, whose bytes outweigh a run's tiles', serves twice the runs
+  // (one 107 KB block a CU); 4 otherwise (at most 80 KB, two blocks a CU)
+  static constexpr int W = FMT == BT_BFP4 ? 8 : 4;
 };
 template <int FMT, int MT, int EPI, int DT>
-__global__ void __launch_bounds__(256) skinny_stream_kernel(const MatmulArgs args, int groups, int stages, float *part) {
+__global__ void __launch_bounds__(64 * Stream<FMT>::W) skinny_stream_kernel(const MatmulArgs args, int groups, int stages,
+                                                                            float *part) {
   using S = Stream<FMT>;
-  constexpr int C = S::C, TB = S::TB, ROWS = 16 * MT, ABYTES = ROWS * 512, STAGE = ABYTES + 4 * S::BW, D = S::D;
-  constexpr int AL = ROWS / 8;      // a wave's A loads a stage (two rows each)
-  constexpr int L = AL + S::BL;     // a wave's loads a stage
+  constexpr int W = S::W, C = S::C, TB = S::TB, ROWS = 16 * MT, ABYTES = ROWS * 512, STAGE = ABYTES + W * S::BW;
+  constexpr int D = S::D;
+  constexpr int AL = ROWS / (2 * W);  // a wave's A loads a stage (two rows each)
+  constexpr int L = AL + S::BL;       // a wave's loads a stage
   constexpr int GAPS = FMT == BT_BFP4 ? C * 128 : 0;  // bfp4: a wave's tiles' exponents as placed gaps
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[D * STAGE + 4 * GAPS];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[D * STAGE + W * GAPS];
   const Head h = early_head(args);
   const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
   const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = (int)blockIdx.x % groups, sp = (int)blockIdx.x / groups;
-  const int pos = 2 * grp + (wib & 1);  // SiLU x up: the gate run (waves 0, 1) whose up run waves 2, 3 take
-  const int run = EPI == 2 ? pos + (wib < 2 ? 0 : h.nruns / 2) : grp * 4 + wib;
+  const int pos = W / 2 * grp + wib % (W / 2);  // SiLU x up: the gate run (the first W / 2 waves) whose up run the
+  const int run = EPI == 2 ? pos + (wib < W / 2 ? 0 : h.nruns / 2) : grp * W + wib;  // other waves take
   const bool in = EPI == 2 ? pos < h.nruns / 2 : run < h.nruns;
   const int first = sp * stages * C;  // the split's first chunk
   const uint32_t abytes = (uint32_t)(((int64_t)(h.m - 1) * h.a.sr + h.k) * 2);
   const i32x4 ar = buffer_words((const void *)h.a.ptr, abytes);
   const i32x4 br = buffer_words(h.b + (int64_t)(in ? run : 0) * h.chunks * TB, in ? (uint32_t)h.chunks * TB : 0u);
-  // stage st into ring slot st % D: this wave's A rows (load j: rows 2q, 2q + 1 with q = wib + 4j; lane l takes
+  // stage st into ring slot st % D: this wave's A rows (load j: rows 2q, 2q + 1 with q = wib + W j; lane l takes
   // row 2q + l / 32, unit (l % 32) ^ (row % 16) of its 32) and its run's C tiles
   auto issue = [&](int st) {
     uint8_t *slot = lds + (st % D) * STAGE;
     const int c0 = first + st * C;
 #pragma unroll
     for (int j = 0; j < AL; j++) {
-      const int r = 2 * (wib + 4 * j) + (lane >> 5);
+      const int r = 2 * (wib + W * j) + (lane >> 5);
       const uint32_t unit = (uint32_t)((lane & 31) ^ (r & 15));
       const uint32_t voff = r < h.m ? (uint32_t)(((int64_t)r * h.a.sr + (int64_t)c0 * 64) * 2) + 16u * unit : abytes;
-      lds_load16(ar, voff, slot + 2 * (wib + 4 * j) * 512);
+      lds_load16(ar, voff, slot + 2 * (wib + W * j) * 512);
     }
     uint8_t *bs = slot + ABYTES + wib * S::BW;
 #pragma unroll
@@ -1396,13 +1401,13 @@ __global__ void __launch_bounds__(256) skinny_stream_kernel(const MatmulArgs arg
   } else {
     __syncthreads();  // every wave is done with the ring
     float *up = (float *)lds;  // the up waves' tiles, for the gate waves
-    if (wib >= 2)
+    if (wib >= W / 2)
 #pragma unroll
       for (int t = 0; t < MT; t++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) up[(((wib - 2) * MT + t) * 4 + i) * 64 + lane] = acc[t][i];
+        for (int i = 0; i < 4; i++) up[(((wib - W / 2) * MT + t) * 4 + i) * 64 + lane] = acc[t][i];
     __syncthreads();
-    if (wib >= 2 || !in) return;
+    if (wib >= W / 2 || !in) return;
     const int n = pos * 16 + col;  // the gate column, and the output's
     const bt_operand &out = h.out;
 #pragma unroll
@@ -2250,17 +2255,20 @@ static bool launch_parts(Runtime *r, const MatmulArgs &args, int fmt, bool swi) 
 
 // The streaming kernels for 5 to 32 rows of one A with K a multiple of 256 and over 12 chunks (shorter K stages A
 // whole in LDS, skinny_lds_kernel): false when the product doesn't fit them (then the split-K or one-launch kernels
-// run it). Splits of whole stages, as many as bring the grid nearest 512
-// blocks (two a CU, by LDS), summed by parts_reduce_kernel in split order; one split stores the result through the
-// epilogue itself.
+// run it). Splits of whole stages, as many as bring a grid of 4-run blocks nearest 512 (two a CU, by LDS; bfp4's
+// blocks of 8 runs then number about 256, one a CU), summed by parts_reduce_kernel in split order; one split stores
+// the result through the epilogue itself.
 template <int FMT, int MT>
-static void launch_stream_m(const MatmulArgs &args, int epi, int dt, int groups, int splits, int stages, float *part,
+static void launch_stream_m(const MatmulArgs &args, int epi, int dt, int splits, int stages, float *part,
                             hipStream_t s) {
-  const unsigned blocks = (unsigned)(groups * splits);
-  if (epi == 0) skinny_stream_kernel<FMT, MT, 0, BT_FP32><<<blocks, 256, 0, s>>>(args, groups, stages, part);
-  else if (epi == 2) skinny_stream_kernel<FMT, MT, 2, BT_BF16><<<blocks, 256, 0, s>>>(args, groups, stages, part);
-  else if (dt == BT_FP32) skinny_stream_kernel<FMT, MT, 1, BT_FP32><<<blocks, 256, 0, s>>>(args, groups, stages, part);
-  else skinny_stream_kernel<FMT, MT, 1, BT_BF16><<<blocks, 256, 0, s>>>(args, groups, stages, part);
+  // groups of W runs (SiLU x up: W / 2 gate runs and their up runs), each over every split
+  constexpr int W = Stream<FMT>::W;
+  const int groups = (args.nruns + W - 1) / W;
+  const unsigned blocks = (unsigned)(groups * splits), threads = 64 * W;
+  if (epi == 0) skinny_stream_kernel<FMT, MT, 0, BT_FP32><<<blocks, threads, 0, s>>>(args, groups, stages, part);
+  else if (epi == 2) skinny_stream_kernel<FMT, MT, 2, BT_BF16><<<blocks, threads, 0, s>>>(args, groups, stages, part);
+  else if (dt == BT_FP32) skinny_stream_kernel<FMT, MT, 1, BT_FP32><<<blocks, threads, 0, s>>>(args, groups, stages, part);
+  else skinny_stream_kernel<FMT, MT, 1, BT_BF16><<<blocks, threads, 0, s>>>(args, groups, stages, part);
 }
 static bool launch_stream(Runtime *r, const MatmulArgs &args, int fmt, bool swi) {
   const bt_operand &a = args.a;
@@ -2270,8 +2278,9 @@ static bool launch_stream(Runtime *r, const MatmulArgs &args, int fmt, bool swi)
       (int64_t)args.chunks * Tile<BT_BF16>::bytes >= (1ll << 32))
     return false;
   const int mt = args.m > 16 ? 2 : 1, total = args.chunks / 4;
-  // (SiLU x up takes the same groups and splits as the plain product of its shape, so both sum alike: half the runs
-  // are gate runs, paired two to a block in one split, or partial sums per run with more)
+  // the splits follow from groups of 4 runs whatever the kernel's block, so every format of B sums K alike; SiLU x up
+  // takes those of the plain product of its shape (one split: each gate run beside its up run in a block; more:
+  // partial sums per run)
   const int groups = (args.nruns + 3) / 4;
   int splits = 1;  // the divisor of the stages that brings the grid nearest 512 blocks
   for (int d = 1; d <= total; d++)
@@ -2283,12 +2292,12 @@ static bool launch_stream(Runtime *r, const MatmulArgs &args, int fmt, bool swi)
   }
   const int epi = splits > 1 ? 0 : swi ? 2 : 1, dt = args.prog.dtype == BT_FP32 ? BT_FP32 : BT_BF16;
   const int stages = total / splits;
-  if (fmt == BT_BF16 && mt == 2) launch_stream_m<BT_BF16, 2>(args, epi, dt, groups, splits, stages, part, r->stream);
-  else if (fmt == BT_BF16) launch_stream_m<BT_BF16, 1>(args, epi, dt, groups, splits, stages, part, r->stream);
-  else if (fmt == BT_BFP8 && mt == 2) launch_stream_m<BT_BFP8, 2>(args, epi, dt, groups, splits, stages, part, r->stream);
-  else if (fmt == BT_BFP8) launch_stream_m<BT_BFP8, 1>(args, epi, dt, groups, splits, stages, part, r->stream);
-  else if (mt == 2) launch_stream_m<BT_BFP4, 2>(args, epi, dt, groups, splits, stages, part, r->stream);
-  else launch_stream_m<BT_BFP4, 1>(args, epi, dt, groups, splits, stages, part, r->stream);
+  if (fmt == BT_BF16 && mt == 2) launch_stream_m<BT_BF16, 2>(args, epi, dt, splits, stages, part, r->stream);
+  else if (fmt == BT_BF16) launch_stream_m<BT_BF16, 1>(args, epi, dt, splits, stages, part, r->stream);
+  else if (fmt == BT_BFP8 && mt == 2) launch_stream_m<BT_BFP8, 2>(args, epi, dt, splits, stages, part, r->stream);
+  else if (fmt == BT_BFP8) launch_stream_m<BT_BFP8, 1>(args, epi, dt, splits, stages, part, r->stream);
+  else if (mt == 2) launch_stream_m<BT_BFP4, 2>(args, epi, dt, splits, stages, part, r->stream);
+  else launch_stream_m<BT_BFP4, 1>(args, epi, dt, splits, stages, part, r->stream);
   if (splits > 1) {
     const int64_t outs = (int64_t)args.m * (swi ? args.n / 2 : args.n);
     const unsigned rb = (unsigned)((outs + 255) / 256);
