@@ -1378,7 +1378,8 @@ __global__ void __launch_bounds__(64 * Stream<FMT>::W) skinny_stream_kernel(cons
     if (st < stages) issue(st);
   for (int st = 0; st < stages; st++) {
     const int later = min(D - 2, stages - 1 - st);
-    if (D == 3 && later == 1) wait_vm<L>();
+    if (D == 4 && later == 2) wait_vm<2 * L>();
+    else if (D >= 3 && later == 1) wait_vm<L>();
     else wait_vm<0>();
     __syncthreads();
     if (st + D - 1 < stages) issue(st + D - 1);
@@ -1724,24 +1725,38 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
       uint2 q[WN];
 #pragma unroll
       for (int j = 0; j < WN; j++) q[j] = *(const uint2 *)(st + QA + (wn * WN + j) * QTB + 64 + 8 * lane);
+      // lane group g's 8 values of half hh: A's 16-byte unit g + 4 hh of each row, B's gaps 16 g + 8 hh ..
+      auto a_frag = [&](int i, int hh) {
+        const int r = wm * WR + 16 * i + col;
+        return *(const bf16x8 *)(st + r * 128 + 16 * ((g + 4 * hh) ^ (r & 7)));
+      };
+      auto gaps = [&](int j, int hh) { return *(const uint4 *)(st + QG + (wn * WN + j) * 128 + 32 * g + 16 * hh); };
+      bf16x8 fa[WM], fb[WN], fb1[WN];
+      uint4 gp[WN];
 #pragma unroll
-      for (int hh = 0; hh < 2; hh++) {
-        bf16x8 fa[WM], fb[WN];
+      for (int i = 0; i < WM; i++) fa[i] = a_frag(i, 0);
 #pragma unroll
-        for (int i = 0; i < WM; i++) {
-          const int r = wm * WR + 16 * i + col;
-          fa[i] = *(const bf16x8 *)(st + r * 128 + 16 * ((g + 4 * hh) ^ (r & 7)));
-        }
+      for (int j = 0; j < WN; j++) fb[j] = q4_to_bf16_placed(q[j].x, gaps(j, 0));
+      __builtin_amdgcn_sched_barrier(0);
+      // the first half's matrix instructions a row of tiles at a time, the second half's reads and decode between
+      // them, so that their VALU work issues while the matrix core is busy: after row i, A's fragment i of the second
+      // half (into the registers row i is done with), the gaps after row 0, and one tile's decode after each of the
+      // last WN rows; the order is held by scheduling barriers
 #pragma unroll
-        for (int j = 0; j < WN; j++)  // values 8 hh .. 8 hh + 7 of lane group g: gaps 16 g + 8 hh ..
-          fb[j] = q4_to_bf16_placed(hh ? q[j].y : q[j].x,
-                                    *(const uint4 *)(st + QG + (wn * WN + j) * 128 + 32 * g + 16 * hh));
+      for (int i = 0; i < WM; i++) {
 #pragma unroll
-        for (int i = 0; i < WM; i++)
+        for (int j = 0; j < WN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        fa[i] = a_frag(i, 1);
+        if (i == 0)
 #pragma unroll
-          for (int j = 0; j < WN; j++)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < WN; j++) gp[j] = gaps(j, 1);
+        if (i >= WM - WN) fb1[i - (WM - WN)] = q4_to_bf16_placed(q[i - (WM - WN)].y, gp[i - (WM - WN)]);
+        __builtin_amdgcn_sched_barrier(0);
       }
+#pragma unroll
+      for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int j = 0; j < WN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb1[j], acc[i][j], 0, 0, 0);
     }
   }
   if constexpr (RES) {
