@@ -2487,7 +2487,7 @@ extern "C" int bt_matmul(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_
   // tiles in the runtime's scratch (the same values bit for bit), then the bf16 GEMM. bfp4 B in whole chunks goes to
   // the same GEMM reading it as it is stored, decoded in registers.
   const bool bf16_out = out->dtype == BT_BF16 && (!epilogue || epilogue->dtype != BT_FP32);
-  if (b_fmt != BT_BF16 && !(b_fmt == BT_BFP4 && k % 64 == 0 && gemm3_shape(args).bm == 256) &&
+  if (b_fmt != BT_BF16 && !(b_fmt == BT_BFP4 && k % 64 == 0) &&
       (bf16_out || residual_program(args, nullptr)) &&
       m >= 512 && k % 32 == 0 && a->sc == 1 && (int64_t)args.chunks * args.nruns * 2048 < (1ll << 32)) {
     const int64_t tiles = (int64_t)args.chunks * args.nruns * (b_batch > 1 ? b_batch : 1);
