@@ -1761,22 +1761,36 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
   }
   if constexpr (RES) {
     // lanes 0..15 of a row group write 16 neighbouring columns: 64 bytes
+    // The residual may be the output itself (x += o), so a residual can't be loaded after a store the compiler can't
+    // tell apart from it: the residuals of GI row tiles are all loaded before any of their sums is stored, one trip
+    // to memory for the group instead of one for each value.
     const int64_t ob = operand_matrix(h.out, b) * h.out.sb, rb = res.ptr ? operand_matrix(res, b) * res.sb : 0;
+    constexpr int GI = WM < 4 ? WM : 4;
 #pragma unroll
-    for (int i = 0; i < WM; i++)
+    for (int i0 = 0; i0 < WM; i0 += GI) {
+      float rv[GI][4][WN];
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int m = m0 + wm * WR + 16 * i + 4 * g + r;
-        if (m >= h.m) continue;
+      for (int ii = 0; ii < GI; ii++)
 #pragma unroll
-        for (int j = 0; j < WN; j++) {
-          const int n = n0 + wn * 16 * WN + 16 * j + col;
-          if (n >= h.n) continue;
-          float v = acc[i][j][r];
-          if (res.ptr) v += ((const float *)res.ptr)[rb + (int64_t)m * res.sr + (int64_t)n * res.sc];
-          ((float *)h.out.ptr)[ob + (int64_t)m * h.out.sr + (int64_t)n * h.out.sc] = v;
-        }
-      }
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+          for (int j = 0; j < WN; j++) {
+            const int m = m0 + wm * WR + 16 * (i0 + ii) + 4 * g + r, n = n0 + wn * 16 * WN + 16 * j + col;
+            rv[ii][r][j] = res.ptr && m < h.m && n < h.n
+                               ? ((const float *)res.ptr)[rb + (int64_t)m * res.sr + (int64_t)n * res.sc] : 0.0f;
+          }
+#pragma unroll
+      for (int ii = 0; ii < GI; ii++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+          for (int j = 0; j < WN; j++) {
+            const int m = m0 + wm * WR + 16 * (i0 + ii) + 4 * g + r, n = n0 + wn * 16 * WN + 16 * j + col;
+            if (m < h.m && n < h.n)
+              ((float *)h.out.ptr)[ob + (int64_t)m * h.out.sr + (int64_t)n * h.out.sc] =
+                  res.ptr ? acc[i0 + ii][j][r] + rv[ii][r][j] : acc[i0 + ii][j][r];
+          }
+    }
     return;
   }
   __syncthreads();  // every wave is done with the stages
