@@ -532,7 +532,9 @@ template <int HD, typename Mid>
 __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf)[2][HD / 32], const uint16_t *kl,
                                            const uint16_t *vt, int kb, const int (&lo)[2], const int (&hi)[2],
                                            int lane, bool mask, Mid mid) {
-  constexpr int KS = HD + 8, VT = KB + 8;
+  // V^T rows of KB + 4 halfwords (34 dwords): the 16 rows one 8-byte read pass covers start 2 banks apart, so it
+  // hits 32 distinct banks (at KB + 8 rows n and n + 8 shared them)
+  constexpr int KS = HD + 8, VT = KB + 4;
   constexpr float L2E = 1.4426950408889634f;
   const int g = lane >> 4, n = lane & 15;
   f32x4 s[2][4];
@@ -643,7 +645,8 @@ __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf
 // and row block rblocks - 1 - u / kvhs.
 template <int HD, int KF>
 __global__ void __launch_bounds__(512, 1) attention_prefill_kernel(const bt_attention_args a, int rblocks, int kvhs) {
-  constexpr int KS = HD + 8, VT = KB + 8, KBUF = KB * KS, STG = KBUF + HD * VT;  // halfwords of one stage
+  constexpr int KS = HD + 8, VT = KB + 4, KBUF = KB * KS, STG = KBUF + HD * VT;  // halfwords of one stage (VT as in
+                                                                                 // fold_pairs)
   constexpr int KW = KB * HD / 8 / 256;  // 16-byte words of K each thread of a half moves per block
   constexpr int KPT = HD / 32;           // keys of V each thread of a half moves per block (8 columns of each)
   constexpr int NKG = KB / KPT;          // threads along the keys of V
