@@ -1592,7 +1592,7 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
   constexpr int A_BYTES = BM * 64, STAGE = A_BYTES + 16384, WM = BM / 32, WN = BN / 64, WR = BM / 2, T = BN / 16;
   constexpr int AL = BM / 128;  // A loads a wave issues a step
   // bfp4: chunk stages of A's rows, the 16 tiles as stored, then the tiles' exponents as placed gaps (128 B a tile)
-  constexpr int CS = 3, QTB = 576, QA = BM * 128, QG = QA + 16 * QTB, QSTAGE = QG + 16 * 128, QAL = BM / 64;
+  constexpr int CS = BM == 128 ? 4 : 3, QTB = 576, QA = BM * 128, QG = QA + 16 * QTB, QSTAGE = QG + 16 * 128, QAL = BM / 64;
   constexpr int RING = FMT == BT_BF16 ? S * STAGE : CS * QSTAGE;
   constexpr int ESZ = DT == BT_FP32 ? 4 : 2, ES = BN * ESZ + 16;
   constexpr int HALF = (DT == BT_FP32 ? 128 : 256) < BM ? (DT == BT_FP32 ? 128 : 256) : BM;
