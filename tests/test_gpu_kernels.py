@@ -488,6 +488,60 @@ def test_attention_config4_batch8_decode(rt, keys):
     assert np.allclose(got[32 * e:32 * e + 32], want, rtol=0.011, atol=0.011), (e, np.abs(got[32 * e:32 * e + 32] - want).max())
 
 
+def test_split_decode_is_the_same_call_after_call(rt):
+  # A decode split into parts and combined: the same call again, a call with other parts between (sharing the
+  # output), and replays of a recorded graph of two calls all give the first call's bits, within the reference's
+  # bound of the oracle
+  rng = np.random.default_rng(77)
+  E, kvh, keys, hd = 64, 16, 3000, 128  # two batch entries of 32 over 8 key heads
+  q = B.bf16(rng.standard_normal((E, 1, hd), dtype=np.float32) / np.float32(np.sqrt(hd)))
+  k, v = (B.bf16(rng.standard_normal((kvh, keys, hd), dtype=np.float32)) for _ in range(2))
+  places = rng.integers(keys // 2, keys, (E, 1))
+  dq, dk, dv = (up(rt, B.bf16_bits(t)) for t in (q, k, v))
+  dp = up(rt, np.asarray(places, np.int32))
+  o = rt.dram_alloc(E * hd * 2)
+
+  def make(parts):
+    args = _lib.AttentionArgs(dq, dk, dv, o, dp, hd, hd, keys * hd, hd, keys * hd, hd, hd, hd, 1, E, E // kvh, 1, keys,
+                              hd, 0, parts, 0, 0, 0)
+    need = ctypes.c_uint64()
+    _lib.call("attention_scratch", ctypes.byref(args), ctypes.byref(need))
+    assert need.value > 0  # split into parts
+    args.scratch, args.scratch_bytes = rt.dram_alloc(need.value), need.value
+    return args
+
+  def result():
+    rt.wait()
+    return down(rt, o, (E, 1, hd), np.uint16).copy()
+
+  auto, seven = make(0), make(7)
+  rt.run("attention", "attention", ctypes.byref(auto))
+  first = result()
+  want = np.concatenate([ops.attention(q[32 * b:32 * b + 32], k[8 * b:8 * b + 8], v[8 * b:8 * b + 8],
+                                       places[32 * b:32 * b + 32, :, None], 0, 4) for b in range(2)])
+  assert np.allclose(bits_to_float(first), want, rtol=0.011, atol=0.011)
+  for args in (auto, seven, auto):
+    rt.upload(o, b"\xff" * (E * hd * 2))
+    rt.run("attention", "attention", ctypes.byref(args))
+    got = result()
+    if args is auto: assert np.array_equal(got, first)
+    else: assert np.allclose(bits_to_float(got), want, rtol=0.011, atol=0.011)
+  g = ctypes.c_void_p()
+  _lib.call("graph_begin", rt.handle)
+  try:
+    _lib.call("attention", rt.handle, ctypes.byref(auto))
+    _lib.call("attention", rt.handle, ctypes.byref(auto))
+  finally:
+    _lib.call("graph_end", rt.handle, ctypes.byref(g))
+  try:
+    for _ in range(3):
+      rt.upload(o, b"\xff" * (E * hd * 2))
+      _lib.call("graph_launch", rt.handle, g)
+      assert np.array_equal(result(), first)
+  finally:
+    _lib.call("graph_destroy", g)
+
+
 def test_attention_config4_causal_prefill(rt):
   # BASELINE config 4's prefill: 2048 rows over their own 2048 keys, causal, 32 query and 8 key heads of 128, against
   # the oracle one key head (and its 4 query heads) at a time
