@@ -608,6 +608,55 @@ def layer_leg(check=True, cpu_seconds=10.0, parts=("prefill", "decode")):
   return res, cpu
 
 
+def gemm_lib_leg(calls=20):
+  """For scale, not a BASELINE configuration: the C5 prefill's four product shapes with bf16 B, this library's GEMM
+  (bt_matmul on B as bf16 columns tiles, calls replayed from a graph) beside hipBLASLt through torch.matmul (calls
+  back to back between two events on torch's stream), both bf16 in, fp32 accumulate, bf16 out. The two results
+  are compared (the summation orders differ, so within a relative 2^-7 of the largest output)."""
+  import torch
+  from baretile_amd import _lib
+  from baretile_amd.runtime import Runtime
+  rt = Runtime()
+  rng = np.random.default_rng(0)
+  out = {}
+  try:
+    for m, k, n in ((2048, 4096, 6144), (2048, 4096, 4096), (2048, 4096, 28672), (2048, 14336, 4096)):
+      x = rng.standard_normal((m, k), dtype=np.float32)
+      w = rng.standard_normal((k, n), dtype=np.float32) * np.float32(0.02)
+      xb, wb = bf16_bits(x), bf16_bits(w)
+      dx, dw, cols, do = rt.dram_alloc(m * k * 2), rt.dram_alloc(k * n * 2), rt.dram_alloc(k * n * 2), rt.dram_alloc(m * n * 2)
+      rt.upload(dx, xb.tobytes())
+      rt.upload(dw, wb.tobytes())
+      rt.run("columns", "bf16_columns", dw, 1, k, n, k * n, n, 1, cols)
+      a, o = _lib.operand(dx, "bf16", 0, k, 1), _lib.operand(do, "bf16", 0, n, 1)
+      us = graph_us(rt, lambda: _lib.call("matmul", rt.handle, byref(a), _lib.BF16, cols, 1, 1, m, k, n, None, byref(o)),
+                    calls)
+      got = np.frombuffer(rt.download(do, m * n * 2), np.uint16).astype(np.uint32) << 16
+      ta = torch.from_numpy(xb.view(np.int16).reshape(m, k).copy()).to("cuda").view(torch.bfloat16)
+      tb = torch.from_numpy(wb.view(np.int16).reshape(k, n).copy()).to("cuda").view(torch.bfloat16)
+      for _ in range(5): tc = ta @ tb
+      torch.cuda.synchronize()
+      start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+      start.record()
+      for _ in range(calls): tc = ta @ tb
+      end.record()
+      torch.cuda.synchronize()
+      lib_us = start.elapsed_time(end) * 1000 / calls
+      ref = tc.float().cpu().numpy()
+      mine = got.view(np.float32).reshape(m, n)
+      agree = bool(np.abs(mine - ref).max() <= np.abs(ref).max() * 2.0 ** -7)
+      flops = 2.0 * m * k * n
+      out[f"{m}x{k}x{n}"] = {"us": round(us, 1), "TFLOP/s": round(flops / us / 1e6, 1),
+                             "hipblaslt_us": round(lib_us, 1), "hipblaslt_TFLOP/s": round(flops / lib_us / 1e6, 1),
+                             "agree": agree}
+      log("gemm", f"{m}x{k}x{n}", out[f"{m}x{k}x{n}"])
+      for d in (dx, dw, cols, do): rt.dram_free(d)
+      del ta, tb, tc
+  finally:
+    rt.close()
+  return out
+
+
 def blas_threads():
   try:
     from threadpoolctl import threadpool_info
@@ -627,7 +676,8 @@ def main():
   ap.add_argument("--no-cpu", action="store_true")
   ap.add_argument("--only", default=None,
                   help="one part: a GEMV configuration (bfp4_B1 ...), gemv, c1, attention, layer (or layer_prefill, "
-                  "layer_decode) or decode")
+                  "layer_decode) or decode; or gemm_lib (not in the default run): the C5 product shapes in bf16, this "
+                  "library's GEMM beside hipBLASLt")
   ap.add_argument("--no-decode", action="store_true", help="skip the SmolLM decode (BASELINE config 3)")
   ap.add_argument("--eager", action="store_true", help="decode without graph replay (for kernel-trace profiles)")
   args = ap.parse_args()
@@ -635,6 +685,9 @@ def main():
     print(f"bench.py runs on one GPU: this build has no multi-GPU path, and --gpus {args.gpus} is not supported",
           file=sys.stderr)
     sys.exit(2)
+  if args.only == "gemm_lib":
+    print(json.dumps({"gemm_lib": gemm_lib_leg()}), flush=True)
+    return
   configs = {}
   for fmt in ("bfp4", "bfp8"):
     for rows in (1, 4, 16):
