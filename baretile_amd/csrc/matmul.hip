@@ -1574,12 +1574,14 @@ gemm2_kernel(const MatmulArgs args, int mblocks, int nblocks) {
 constexpr int GEMM_PLAIN = 0, GEMM_RES = 1, GEMM_SWIGLU = 2;
 // BM: the block's rows, 256 or 128 (a wave BM / 2 of them by 64 columns), for products whose 256-row blocks would
 // leave CUs idle.
-// FMT 4 (bfp4 B) stages a chunk (64 rows of K) at a time, CS = 3 deep: A as BM rows of 128 bytes (unit u of row r at
-// u ^ (r % 8), so the fragment reads of 8 neighbouring rows meet different banks) and the block's 16 tiles as they are
-// stored, 576 bytes each (36 lanes of a direct load). Each wave reads its 4 tiles' value and exponent bytes once a
-// chunk and decodes each half into bf16 fragments in registers (q * 2^(e - 129) by subtracting exponent gaps, the
-// values the unpacker gives), so B crosses HBM and LDS at 0.28 of its bf16 size and needs no unpacking pass. The
-// sums run in the same order, so the result is the same bits as the bf16 GEMM on B's unpacked tiles.
+// FMT 4 (bfp4 B) stages a chunk (64 rows of K) at a time, CS = 3 deep (4 for 128-row blocks): A as BM rows of 128
+// bytes (unit u of row r at u ^ (r % 8), so the fragment reads of 8 neighbouring rows meet different banks) and the
+// block's 16 tiles as they are stored, 576 bytes each (36 lanes of a direct load). The wave that loaded a tile places
+// its exponent bytes in LDS as 16-bit gaps before the chunk's barrier; each wave then reads its 4 tiles' value bytes
+// and gaps and decodes them into bf16 fragments in registers (q * 2^(e - 129) by subtracting the gaps, the values the
+// unpacker gives), the second half's decode between the first half's matrix instructions. So B crosses HBM and LDS
+// at 0.28 of its bf16 size and needs no unpacking pass. The sums run in the same order, so the result is the same
+// bits as the bf16 GEMM on B's unpacked tiles.
 // BN: the block's columns, 256 or 192 (each wave BN / 4 of them; the stages keep room for 16 tiles either way, and the
 // slots of missing tiles take loads that read nothing, so every wave issues the same loads), for products whose
 // 256-column blocks would leave a round of the CUs part empty (6144 columns: 256 blocks of 256 x 192 instead of 192).
