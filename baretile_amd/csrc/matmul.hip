@@ -1591,7 +1591,12 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
   static_assert(FMT == BT_BF16 || FMT == BT_BFP4, "gemm3 takes bf16 or bfp4 B");
   static_assert(BN == 256 || (BN == 192 && MODE != GEMM_SWIGLU), "gemm3 blocks are 256 or 192 columns");
   constexpr bool RES = MODE == GEMM_RES;
-  constexpr int A_BYTES = BM * 64, STAGE = A_BYTES + 16384, WM = BM / 32, WN = BN / 64, WR = BM / 2, T = BN / 16;
+  // the 8 waves as 2 x 4 (each BM / 2 rows by BN / 4 columns); bfp4 B in 128-row blocks as 1 x 8 (each all 128 rows
+  // by BN / 8 columns), so that each tile is decoded by one wave, not two, for as many matrix instructions
+  constexpr int WAVES_M = FMT == BT_BFP4 && BM == 128 ? 1 : 2, WAVES_N = 8 / WAVES_M;
+  constexpr int A_BYTES = BM * 64, STAGE = A_BYTES + 16384, WM = BM / (16 * WAVES_M), WN = BN / (16 * WAVES_N),
+                WR = BM / WAVES_M, T = BN / 16;
+  static_assert(WN * 16 * WAVES_N == BN, "the waves' columns cover the block");
   constexpr int AL = BM / 128;  // A loads a wave issues a step
   // bfp4: chunk stages of A's rows, the 16 tiles as stored, then the tiles' exponents as placed gaps (128 B a tile)
   constexpr int CS = BM == 128 ? 4 : 3, QTB = 576, QA = BM * 128, QG = QA + 16 * QTB, QSTAGE = QG + 16 * 128, QAL = BM / 64;
@@ -1602,7 +1607,7 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS];
   const Head h = early_head(args);
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, col = lane & 15;
-  const int wib = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wib >> 2, wn = wib & 3;
+  const int wib = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wib / WAVES_N, wn = wib % WAVES_N;
   const int per = mblocks * nblocks, total = per * h.batch, full = total / 8 * 8;
   int pid = blockIdx.x;
   if (pid < full) pid = (pid % 8) * (full / 8) + pid / 8;  // neighbouring blocks on one XCD
