@@ -1092,11 +1092,17 @@ __device__ __forceinline__ i32x4 buffer_words(const void *base, uint32_t bytes) 
 // that the compiler, which can't tell which LDS bytes such a load writes, doesn't wait for every one of them before
 // each LDS read; the kernel waits for them itself (wait_vm). Loads complete in order, so the compiler's own waits
 // on other loads stay correct (at worst they wait for these too).
+// The resource is wave-uniform; readfirstlane hands it to the assembly in scalar registers even where the compiler
+// would otherwise keep a copy in vector registers.
+__device__ __forceinline__ i32x4 uniform_words(const i32x4 &w) {
+  return i32x4{__builtin_amdgcn_readfirstlane(w.x), __builtin_amdgcn_readfirstlane(w.y),
+               __builtin_amdgcn_readfirstlane(w.z), __builtin_amdgcn_readfirstlane(w.w)};
+}
 __device__ __forceinline__ void lds_load16(const i32x4 &rsrc, uint32_t voff, const void *lds) {
   const uint32_t at = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds;
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :
-               : "v"(voff), "s"(rsrc), "s"(at)
+               : "v"(voff), "s"(uniform_words(rsrc)), "s"(at)
                : "memory", "m0");
 }
 
@@ -1105,7 +1111,7 @@ __device__ __forceinline__ void lds_load4(const i32x4 &rsrc, uint32_t voff, cons
   const uint32_t at = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)lds;
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
                :
-               : "v"(voff), "s"(rsrc), "s"(at)
+               : "v"(voff), "s"(uniform_words(rsrc)), "s"(at)
                : "memory", "m0");
 }
 
@@ -1591,9 +1597,9 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
   static_assert(FMT == BT_BF16 || FMT == BT_BFP4, "gemm3 takes bf16 or bfp4 B");
   static_assert(BN == 256 || (BN == 192 && MODE != GEMM_SWIGLU), "gemm3 blocks are 256 or 192 columns");
   constexpr bool RES = MODE == GEMM_RES;
-  // the 8 waves as 2 x 4 (each BM / 2 rows by BN / 4 columns); bfp4 B in 128-row blocks as 1 x 8 (each all 128 rows
-  // by BN / 8 columns), so that each tile is decoded by one wave, not two, for as many matrix instructions
-  constexpr int WAVES_M = FMT == BT_BFP4 && BM == 128 ? 1 : 2, WAVES_N = 8 / WAVES_M;
+  // the 8 waves as 2 x 4 (each BM / 2 rows by BN / 4 columns); bfp4 B, where the columns allow, as 1 x 8 (each all BM
+  // rows by BN / 8 columns), so that each tile is decoded by one wave, not two, for as many matrix instructions
+  constexpr int WAVES_M = FMT == BT_BFP4 && BN % 128 == 0 ? 1 : 2, WAVES_N = 8 / WAVES_M;
   constexpr int A_BYTES = BM * 64, STAGE = A_BYTES + 16384, WM = BM / (16 * WAVES_M), WN = BN / (16 * WAVES_N),
                 WR = BM / WAVES_M, T = BN / 16;
   static_assert(WN * 16 * WAVES_N == BN, "the waves' columns cover the block");
@@ -1806,17 +1812,18 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
   // the tile through LDS to the epilogue: 256 rows (bf16) or 128 at a time (fp32)
 #pragma unroll
   for (int half = 0; half < BM / HALF; half++) {
-    if (BM == HALF || wm == half) {
 #pragma unroll
-      for (int i = 0; i < WM; i++)
+    for (int i = 0; i < WM; i++) {
+      const int row0 = wm * WR + 16 * i;  // the row tile's first row in the block: written in its own half
+      if (row0 / HALF != half) continue;
 #pragma unroll
-        for (int j = 0; j < WN; j++)
+      for (int j = 0; j < WN; j++)
 #pragma unroll
-          for (int r = 0; r < 4; r++) {
-            uint8_t *at = lds + ((BM == HALF ? wm * WR : 0) + 16 * i + 4 * g + r) * ES + (wn * 16 * WN + 16 * j + col) * ESZ;
-            if (DT == BT_FP32) *(float *)at = acc[i][j][r];
-            else *(uint16_t *)at = (uint16_t)bf16_packed(acc[i][j][r]);
-          }
+        for (int r = 0; r < 4; r++) {
+          uint8_t *at = lds + (row0 % HALF + 4 * g + r) * ES + (wn * 16 * WN + 16 * j + col) * ESZ;
+          if (DT == BT_FP32) *(float *)at = acc[i][j][r];
+          else *(uint16_t *)at = (uint16_t)bf16_packed(acc[i][j][r]);
+        }
     }
     __syncthreads();
     if constexpr (MODE == GEMM_SWIGLU) {
