@@ -272,7 +272,7 @@ def test_split_k_rows(rt, fmt, m, k, n, out):
 # of the CUs, where 256 x 256 would leave a quarter idle).
 GEMM_CASES = [(300, 1000, 520, "bf16"), (96, 576, 1536, "fp32"), (2048, 256, 8192, "bf16"), (2048, 192, 4096, "fp32"),
               (160, 320, 8192, "bf16"), (1000, 224, 4096, "bf16"), (520, 640, 1296, "fp32"), (2048, 320, 6144, "bf16"),
-              (2048, 192, 6144, "fp32")]
+              (2048, 192, 6144, "fp32"), (2048, 128, 8192, "fp32")]
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bfp4"])
