@@ -1588,14 +1588,17 @@ constexpr int GEMM_PLAIN = 0, GEMM_RES = 1, GEMM_SWIGLU = 2;
 // unpacker gives), the second half's decode between the first half's matrix instructions. So B crosses HBM and LDS
 // at 0.28 of its bf16 size and needs no unpacking pass. The sums run in the same order, so the result is the same
 // bits as the bf16 GEMM on B's unpacked tiles.
-// BN: the block's columns, 256 or 192 (each wave BN / 4 of them; the stages keep room for 16 tiles either way, and the
-// slots of missing tiles take loads that read nothing, so every wave issues the same loads), for products whose
-// 256-column blocks would leave a round of the CUs part empty (6144 columns: 256 blocks of 256 x 192 instead of 192).
+// BN: the block's columns, 256 or 192 (the stages keep room for 16 tiles either way, and the slots of missing tiles
+// take loads that read nothing, so every wave issues the same loads), for products whose 256-column blocks would leave
+// a round of the CUs part empty; or, on bfp4 B, 128 x 384 (24 tiles a stage, three a wave): 6144 columns make 256
+// such blocks, one round, each tile decoded once and each A byte staged for 384 columns.
 template <int FMT, int DT, int S, int MODE = GEMM_PLAIN, int BM = 256, int BN = 256>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand res, int nb_off = 0) {
   static_assert(FMT == BT_BF16 || FMT == BT_BFP4, "gemm3 takes bf16 or bfp4 B");
-  static_assert(BN == 256 || (BN == 192 && MODE != GEMM_SWIGLU), "gemm3 blocks are 256 or 192 columns");
+  static_assert(BN == 256 || (BN == 192 && MODE != GEMM_SWIGLU) ||
+                    (BN == 384 && FMT == BT_BFP4 && BM == 128 && MODE != GEMM_SWIGLU),
+                "gemm3 blocks are 256 or 192 columns, or 128 x 384 on bfp4 B");
   constexpr bool RES = MODE == GEMM_RES;
   // the 8 waves as 2 x 4 (each BM / 2 rows by BN / 4 columns); bfp4 B, where the columns allow, as 1 x 8 (each all BM
   // rows by BN / 8 columns), so that each tile is decoded by one wave, not two, for as many matrix instructions
@@ -1605,7 +1608,9 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
   static_assert(WN * 16 * WAVES_N == BN, "the waves' columns cover the block");
   constexpr int AL = BM / 128;  // A loads a wave issues a step
   // bfp4: chunk stages of A's rows, the 16 tiles as stored, then the tiles' exponents as placed gaps (128 B a tile)
-  constexpr int CS = BM == 128 ? 4 : 3, QTB = 576, QA = BM * 128, QG = QA + 16 * QTB, QSTAGE = QG + 16 * 128, QAL = BM / 64;
+  // TT: tile slots a stage (16, or 24 for 384 columns), NB of them loaded by each wave
+  constexpr int TT = BN / 16 > 16 ? BN / 16 : 16, NB = TT / 8;
+  constexpr int CS = BM == 128 ? 4 : 3, QTB = 576, QA = BM * 128, QG = QA + TT * QTB, QSTAGE = QG + TT * 128, QAL = BM / 64;
   constexpr int RING = FMT == BT_BF16 ? S * STAGE : CS * QSTAGE;
   constexpr int ESZ = DT == BT_FP32 ? 4 : 2, ES = BN * ESZ + 16;
   constexpr int HALF = (DT == BT_FP32 ? 128 : 256) < BM ? (DT == BT_FP32 ? 128 : 256) : BM;
@@ -1700,14 +1705,14 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
     // each lane's source for the wave's QAL A loads (8 rows of 128 bytes each; lane l takes row l / 8, unit
     // (l % 8) ^ (row % 8)) and 2 B tiles (tiles wib and wib + 8, lanes 0..35) of chunk 0; a chunk adds 128 bytes to
     // A's, one tile to B's
-    uint32_t aq[QAL], bq[2];
+    uint32_t aq[QAL], bq[NB];
 #pragma unroll
     for (int j = 0; j < QAL; j++) {
       const int r = 8 * (wib + 8 * j) + (lane >> 3), u = (lane & 7) ^ (r & 7);
       aq[j] = m0 + r < h.m ? (uint32_t)(((int64_t)(m0 + r) * h.a.sr + 8 * u) * 2) : NOWHERE;
     }
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < NB; j++) {
       bool in;
       const int run = b_run(wib + 8 * j, in);
       bq[j] = in ? (uint32_t)((int64_t)run * h.chunks * QTB + 16 * lane) : NOWHERE;
@@ -1718,7 +1723,7 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
 #pragma unroll
       for (int j = 0; j < QAL; j++) lds_load16(ar, aq[j] == NOWHERE ? NOWHERE : aq[j] + ao, st + (wib + 8 * j) * 1024);
 #pragma unroll
-      for (int j = 0; j < 2; j++)
+      for (int j = 0; j < NB; j++)
         if (lane < QTB / 16) lds_load16(br, bq[j] == NOWHERE ? NOWHERE : bq[j] + bo, st + QA + (wib + 8 * j) * QTB);
     };
     const int chunks = h.k / 64;
@@ -1726,12 +1731,12 @@ gemm3_kernel(const MatmulArgs args, int mblocks, int nblocks, const bt_operand r
     for (int c = 0; c < CS - 1; c++)
       if (c < chunks) issue(c);
     for (int c = 0; c < chunks; c++) {
-      if (c + CS - 2 < chunks) wait_vm<(QAL + 2) * (CS - 2)>();
+      if (c + CS - 2 < chunks) wait_vm<(QAL + NB) * (CS - 2)>();
       else wait_vm<0>();
       uint8_t *st = lds + (c % CS) * QSTAGE;
       // the exponent bytes of the wave's own two tiles have landed (its loads wrote them): placed as gaps once here,
       // for every wave that reads the tiles, instead of by each of them (lanes 16 s .. 16 s + 15: tile wib + 8 s)
-      if (lane < 32) {
+      if (lane < 16 * NB) {
         const int s = wib + 8 * (lane >> 4), w = lane & 15;
         *(uint2 *)(st + QG + s * 128 + 8 * w) = place_gaps(*(const uint32_t *)(st + QA + s * QTB + 4 * w));
       }
@@ -2389,15 +2394,15 @@ static bool residual_program(const MatmulArgs &args, bt_operand *res) {
   return true;
 }
 
-// gemm3's block shape: 256 x 256, 256 x 192 or 128 x 256, whichever fills the CUs' rounds best, a full round of the
-// smaller blocks counted at 0.9 and 0.85 of the speed of one of 256 x 256.
+// gemm3's block shape: 256 x 256, 256 x 192 or 128 x 256 (and 128 x 384 on bfp4 B), whichever fills the CUs' rounds
+// best, a full round of the smaller blocks counted at 0.9, 0.85 and 0.95 of the speed of one of 256 x 256.
 struct Gemm3Shape { int bm, bn; };
-static Gemm3Shape gemm3_shape(const MatmulArgs &args) {
-  const Gemm3Shape opts[3] = {{256, 256}, {256, 192}, {128, 256}};
-  const double eff[3] = {1.0, 0.9, 0.85};
+static Gemm3Shape gemm3_shape(const MatmulArgs &args, bool bfp4) {
+  const Gemm3Shape opts[4] = {{256, 256}, {256, 192}, {128, 256}, {128, 384}};
+  const double eff[4] = {1.0, 0.9, 0.85, 0.95};
   int best = 0;
   double score = -1.0;
-  for (int o = 0; o < 3; o++) {
+  for (int o = 0; o < (bfp4 ? 4 : 3); o++) {
     const int64_t blocks = (int64_t)args.batch * ((args.m + opts[o].bm - 1) / opts[o].bm) * ((args.n + opts[o].bn - 1) / opts[o].bn);
     const double sc = eff[o] * (double)blocks / (double)((blocks + 255) / 256 * 256);
     if (sc > score + 1e-9) score = sc, best = o;
@@ -2427,14 +2432,26 @@ static void launch_gemm_dt(const MatmulArgs &args, hipStream_t s) {
     const bool fits = FMT == BT_BF16 ? args.m > 128 && args.k % 32 == 0
                                      : args.m >= 512 && args.k % 64 == 0 && (int64_t)args.chunks * args.nruns * 576 < (1ll << 32);
     if (fits && (DT == BT_BF16 || residual_program(args, &res))) {
-      const Gemm3Shape sh = gemm3_shape(args);
+      const Gemm3Shape sh = gemm3_shape(args, FMT == BT_BFP4);
       const int mb = (args.m + sh.bm - 1) / sh.bm, nb = (args.n + sh.bn - 1) / sh.bn;
       const unsigned blocks = (unsigned)((int64_t)mb * nb * args.batch);
       if constexpr (DT == BT_BF16) {
+        if constexpr (FMT == BT_BFP4) {
+          if (sh.bn == 384) {
+            gemm3_kernel<FMT, DT, 4, GEMM_PLAIN, 128, 384><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
+            return;
+          }
+        }
         if (sh.bm == 128) gemm3_kernel<FMT, DT, 4, GEMM_PLAIN, 128><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
         else if (sh.bn == 192) gemm3_kernel<FMT, DT, 4, GEMM_PLAIN, 256, 192><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
         else gemm3_kernel<FMT, DT, 4><<<blocks, 512, 0, s>>>(args, mb, nb, bt_operand{});
       } else {
+        if constexpr (FMT == BT_BFP4) {
+          if (sh.bn == 384) {
+            gemm3_kernel<FMT, DT, 4, GEMM_RES, 128, 384><<<blocks, 512, 0, s>>>(args, mb, nb, res);
+            return;
+          }
+        }
         if (sh.bm == 128) gemm3_kernel<FMT, DT, 4, GEMM_RES, 128><<<blocks, 512, 0, s>>>(args, mb, nb, res);
         else if (sh.bn == 192) gemm3_kernel<FMT, DT, 4, GEMM_RES, 256, 192><<<blocks, 512, 0, s>>>(args, mb, nb, res);
         else gemm3_kernel<FMT, DT, 4, GEMM_RES><<<blocks, 512, 0, s>>>(args, mb, nb, res);
