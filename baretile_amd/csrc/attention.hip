@@ -23,6 +23,7 @@
 #include "common.h"
 #include <mutex>
 #include <algorithm>
+#include <type_traits>
 
 namespace bt {
 
@@ -417,14 +418,18 @@ attention_decode_kernel(const bt_attention_args a, int tiles, int parts, float *
   };
   int kb = first + KB * wib;
   if (kb <= last) {
+    fetch_values(kb);  // values first, as in the loop: a block's values are waited for before its keys
     fetch_keys<HD, KF, WIDE>(kbytes, kr, kb, a.k_sr, lane);
-    fetch_values(kb);
   }
-  for (; kb <= last; kb += 4 * KB) {
-    const int next = kb + 4 * KB;
+  // a block's values go out as soon as the previous block's are in LDS (B = 8 at 1024 keys 13.1 -> 10.9 us, B = 32 at
+  // 4096 keys 95.5 -> 90-93 us), its keys once the previous scores are made; the last block's step is its own copy,
+  // so the loop's fetches carry no condition.
+  auto step = [&](int kb, auto more) {
+    constexpr bool MORE = decltype(more)::value;
     wave_lds_sync();  // the previous block's reads of vl are done
 #pragma unroll
     for (int i = 0; i < VI; i++) *(uint4 *)(vl + (vrow + RPI * i) * VS + vcol) = kv_value8<KF>(vq[i], vx[i]);
+    if constexpr (MORE) fetch_values(kb + 4 * KB);
     wave_lds_sync();
     f32x4 s[4];
     {
@@ -432,12 +437,11 @@ attention_decode_kernel(const bt_attention_args a, int tiles, int parts, float *
       decode_keys<HD, KF, WIDE>(kf, kbytes, lane);
       block_scores<HD>(s, kf, qf);
     }
-    if (next <= last) {
-      fetch_keys<HD, KF, WIDE>(kbytes, kr, next, a.k_sr, lane);
-      fetch_values(next);
-    }
+    if constexpr (MORE) fetch_keys<HD, KF, WIDE>(kbytes, kr, kb + 4 * KB, a.k_sr, lane);
     fold_scores<HD, VS>(st, s, vl, kb, pr, lane);
-  }
+  };
+  for (; kb + 4 * KB <= last; kb += 4 * KB) step(kb, std::true_type{});
+  if (kb <= last) step(kb, std::false_type{});
   __syncthreads();
   float *ws = (float *)lds;
   store_state<HD>(ws + wib * PF, st, lane);
