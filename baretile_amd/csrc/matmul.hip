@@ -1320,8 +1320,8 @@ __global__ void __launch_bounds__(64 * Stream<FMT>::W) skinny_stream_kernel(cons
   const i32x4 br = buffer_words(h.b + (int64_t)(in ? run : 0) * h.chunks * TB, in ? (uint32_t)h.chunks * TB : 0u);
   // stage st into ring slot st % D: this wave's A rows (load j: rows 2q, 2q + 1 with q = wib + W j; lane l takes
   // row 2q + l / 32, unit (l % 32) ^ (row % 16) of its 32) and its run's C tiles
-  auto issue = [&](int st) {
-    uint8_t *slot = lds + (st % D) * STAGE;
+  auto issue = [&](int st, int k) {  // k = st % D, a constant where the loop below is unrolled
+    uint8_t *slot = lds + k * STAGE;
     const int c0 = first + st * C;
 #pragma unroll
     for (int j = 0; j < AL; j++) {
@@ -1341,8 +1341,8 @@ __global__ void __launch_bounds__(64 * Stream<FMT>::W) skinny_stream_kernel(cons
 #pragma unroll
   for (int t = 0; t < MT; t++) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   uint8_t *gp = lds + D * STAGE + wib * GAPS;
-  auto multiply = [&](int st) {
-    const uint8_t *slot = lds + (st % D) * STAGE;
+  auto multiply = [&](int k) {
+    const uint8_t *slot = lds + k * STAGE;
     const uint8_t *bs = slot + ABYTES + wib * S::BW;
     if (FMT == BT_BFP4) {  // once for the wave's 64 lanes, not by each lane for its own 8 values (C = 4: lane l
       static_assert(FMT != BT_BFP4 || C == 4, "one exponent word a lane");  // places tile l / 16's word l % 16)
@@ -1381,15 +1381,22 @@ __global__ void __launch_bounds__(64 * Stream<FMT>::W) skinny_stream_kernel(cons
   // D - 1 ahead into the slot the previous stage freed, and the multiply
 #pragma unroll
   for (int st = 0; st < D - 1; st++)
-    if (st < stages) issue(st);
-  for (int st = 0; st < stages; st++) {
-    const int later = min(D - 2, stages - 1 - st);
-    if (D == 4 && later == 2) wait_vm<2 * L>();
-    else if (D >= 3 && later == 1) wait_vm<L>();
-    else wait_vm<0>();
-    __syncthreads();
-    if (st + D - 1 < stages) issue(st + D - 1);
-    multiply(st);
+    if (st < stages) issue(st, st);
+  // the stages D at a time, unrolled, so that each one's ring slot is a constant and the LDS addresses of its loads
+  // and fragment reads are fixed offsets from a few registers
+  for (int s0 = 0; s0 < stages; s0 += D) {
+#pragma unroll
+    for (int k = 0; k < D; k++) {
+      const int st = s0 + k;
+      if (st >= stages) break;
+      const int later = min(D - 2, stages - 1 - st);
+      if (D == 4 && later == 2) wait_vm<2 * L>();
+      else if (D >= 3 && later == 1) wait_vm<L>();
+      else wait_vm<0>();
+      __syncthreads();
+      if (st + D - 1 < stages) issue(st + D - 1, (k + D - 1) % D);
+      multiply(k);
+    }
   }
   if constexpr (EPI == 0) {
     const int n = run * 16 + col;
