@@ -603,18 +603,22 @@ __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf
       for (int i = 0; i < 4; i++) gr[q].l[i] *= sc[i];
     }
   }
+  float nb[2];
 #pragma unroll
-  for (int q = 0; q < 2; q++) {
-    const float nb = gr[q].m == -__builtin_inff() ? 0.0f : -gr[q].m;  // no key seen yet: every s is -inf, p 0
+  for (int q = 0; q < 2; q++) nb[q] = gr[q].m == -__builtin_inff() ? 0.0f : -gr[q].m;  // no key seen yet: p 0
+  auto exps = [&](int q, int kt) {
+    float p[4];
 #pragma unroll
-    for (int kt = 0; kt < 4; kt++) {
-      float p[4];
+    for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[q][kt][i], L2E, nb[q]));
+    pb[q][kt][0] = pack_rne(p[0], p[1]);
+    pb[q][kt][1] = pack_rne(p[2], p[3]);
+  };
+  // key tiles 0 and 1 first: the first step of P V needs them; tiles 2 and 3 are made between that step's matrix
+  // instructions (one group and tile after each of its first 4 column tiles: 68.6-69.6 -> 66.0-67.5 us at 2048 rows;
+  // spread over all 8 at HD 128, 67.7-68.8), so their VALU work issues while the matrix core is busy; the order is
+  // held by scheduling barriers
 #pragma unroll
-      for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[q][kt][i], L2E, nb));
-      pb[q][kt][0] = pack_rne(p[0], p[1]);
-      pb[q][kt][1] = pack_rne(p[2], p[3]);
-    }
-  }
+  for (int q = 0; q < 2; q++) exps(q, 0), exps(q, 1);
   __builtin_amdgcn_sched_barrier(0);
   const bf16x8 ones = as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
 #pragma unroll
@@ -631,6 +635,10 @@ __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf
       const bf16x8 vf = as_bf16x8(a0.x, a0.y, a1.x, a1.y);
       gr[0].o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], vf, gr[0].o[c], 0, 0, 0);
       gr[1].o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], vf, gr[1].o[c], 0, 0, 0);
+      if (ks == 0 && c < 4) {
+        exps(c / 2, 2 + c % 2);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     gr[0].l = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], ones, gr[0].l, 0, 0, 0);
     gr[1].l = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], ones, gr[1].l, 0, 0, 0);
