@@ -542,6 +542,27 @@ __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf
   constexpr float L2E = 1.4426950408889634f;
   const int g = lane >> 4, n = lane & 15;
   f32x4 s[2][4];
+  uint32_t pb[2][4][2];  // [group][key tile][pair of keys]: packed p
+  // p = 2^(s log2(e) - m) against the reference m before this block; if the block moves some pair's reference, those
+  // of key tiles 0 and 1 are made again below, so they can be made while the scores of tiles 2 and 3 are
+  float nb[2];
+#pragma unroll
+  for (int q = 0; q < 2; q++) nb[q] = gr[q].m == -__builtin_inff() ? 0.0f : -gr[q].m;  // no key seen yet: p 0
+  auto exps = [&](int q, int kt) {
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[q][kt][i], L2E, nb[q]));
+    pb[q][kt][0] = pack_rne(p[0], p[1]);
+    pb[q][kt][1] = pack_rne(p[2], p[3]);
+  };
+  auto mask_tile = [&](int q, int kt) {
+    if (!mask) return;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int j = kb + 16 * kt + 4 * g + i;
+      if (j < lo[q] || j > hi[q]) s[q][kt][i] = -__builtin_inff();
+    }
+  };
   bf16x8 kf[2][HD / 32];  // two key tiles' K fragments, the next read while the current one is multiplied
 #pragma unroll
   for (int kk = 0; kk < HD / 32; kk++) kf[0][kk] = *(const bf16x8 *)(kl + n * KS + 32 * kk + 8 * g);
@@ -558,24 +579,24 @@ __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf
       s[0][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kt & 1][kk], qf[0][kk], s[0][kt], 0, 0, 0);
       s[1][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kt & 1][kk], qf[1][kk], s[1][kt], 0, 0, 0);
     }
+    if (kt >= 1) {  // the previous tile's scores: masked, and tiles 0 and 1 turned into p, while this tile's run
+#pragma unroll
+      for (int q = 0; q < 2; q++) {
+        mask_tile(q, kt - 1);
+        if (kt - 1 < 2) exps(q, kt - 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
+#pragma unroll
+  for (int q = 0; q < 2; q++) mask_tile(q, 3);
   __builtin_amdgcn_sched_barrier(0);
   mid();
   __builtin_amdgcn_sched_barrier(0);
-  uint32_t pb[2][4][2];  // [group][key tile][pair of keys]: packed p
   bool need = false;
   float mnew[2];
 #pragma unroll
   for (int q = 0; q < 2; q++) {
-    if (mask) {
-#pragma unroll
-      for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int j = kb + 16 * kt + 4 * g + i;
-          if (j < lo[q] || j > hi[q]) s[q][kt][i] = -__builtin_inff();
-        }
-    }
     float mx = s[q][0][0];
 #pragma unroll
     for (int e = 1; e < 16; e += 2) mx = fmaxf(fmaxf(mx, s[q][e / 4][e % 4]), s[q][(e + 1) / 4 % 4][(e + 1) % 4]);
@@ -601,24 +622,14 @@ __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf
         for (int i = 0; i < 4; i++) gr[q].o[c][i] *= sc[i];
 #pragma unroll
       for (int i = 0; i < 4; i++) gr[q].l[i] *= sc[i];
+      nb[q] = gr[q].m == -__builtin_inff() ? 0.0f : -gr[q].m;
+      exps(q, 0);
+      exps(q, 1);
     }
   }
-  float nb[2];
-#pragma unroll
-  for (int q = 0; q < 2; q++) nb[q] = gr[q].m == -__builtin_inff() ? 0.0f : -gr[q].m;  // no key seen yet: p 0
-  auto exps = [&](int q, int kt) {
-    float p[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[q][kt][i], L2E, nb[q]));
-    pb[q][kt][0] = pack_rne(p[0], p[1]);
-    pb[q][kt][1] = pack_rne(p[2], p[3]);
-  };
-  // key tiles 0 and 1 first: the first step of P V needs them; tiles 2 and 3 are made between that step's matrix
-  // instructions (one group and tile after each of its first 4 column tiles: 68.6-69.6 -> 66.0-67.5 us at 2048 rows;
-  // spread over all 8 at HD 128, 67.7-68.8), so their VALU work issues while the matrix core is busy; the order is
-  // held by scheduling barriers
-#pragma unroll
-  for (int q = 0; q < 2; q++) exps(q, 0), exps(q, 1);
+  // key tiles 2 and 3 are made between the first P V step's matrix instructions (one group and tile after each of its
+  // first 4 column tiles: 68.6-69.6 -> 66.0-67.5 us at 2048 rows; spread over all 8 at HD 128, 67.7-68.8), so their
+  // VALU work issues while the matrix core is busy; the order is held by scheduling barriers
   __builtin_amdgcn_sched_barrier(0);
   const bf16x8 ones = as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
 #pragma unroll
