@@ -538,7 +538,6 @@ extern "C" int bt_rope_put(bt_runtime *rt, const bt_rope_args *args) {
 
 namespace bt {
 
-// RMSNorm of rows: a block a row, two passes over it (the second from cache).
 // RMSNorm of one row a block. Rows of up to 8192 columns (k a multiple of 4, 16-byte aligned rows) are fetched
 // whole into registers by 16-byte loads, all issued before the first is used, so a row costs one trip to memory;
 // longer or unaligned rows loop over the columns and read them twice.
