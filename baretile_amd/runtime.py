@@ -24,13 +24,13 @@ class Bound(int):
 
 class Runtime:
   """Queue work on a GPU. Runtime(chip) opens the chip's device with a stream of its own; a newer Runtime on the same
-  chip closes this one. start/end (Tensix rectangles) and ring are accepted for compatibility and unused."""
+  chip closes this one. Without a chip, the runtime uses this process's Chip on GPU 0, opening one if there is none.
+  start/end (Tensix rectangles) and ring are accepted for compatibility and unused."""
   def __init__(self, chip=None, start=None, end=None, ring=1 << 20, timing=False):
     if ring < 64 or ring & (ring - 1): raise ValueError("ring size must be a power of two, at least 64 bytes")
     if chip is None:
-      from baretile_amd.chip import Chip
-      from baretile_amd import pci
-      chip = Chip(pci.open_device())
+      from baretile_amd.chip import shared
+      chip = shared(0)
     self.chip, self.handle, self.closed = chip, None, False
     previous = chip.runtime() if chip.runtime is not None else None
     if previous is not None and not previous.closed: previous.close()

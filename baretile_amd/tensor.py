@@ -154,10 +154,31 @@ class Tensor:
     base = self.storage.addr
     return base + self.offset // 16, base + self.storage.vals + (self.offset if self.dtype == "bfp8" else self.offset // 2)
 
-  def _bfp_whole(self):  # a plain block float read as whole, contiguous matrices (for unpacking and re-laying)
+  def _bfp_whole(self):  # a plain block float read as whole, contiguous matrices (for re-laying by columns)
     if not self._contiguous():
-      raise ValueError("a block-float view reads back, casts or lays out by columns only as whole, contiguous matrices")
+      raise ValueError("a block-float view lays out by columns only as whole, contiguous matrices")
     return self
+
+  def _unpacked(self, why):
+    """A realized plain block float's values as a new bf16 tensor of its shape, exactly as the unpacker decodes them
+    (tensor.py:1093-1104). A view that isn't whole, contiguous matrices is read through its storage unpacked whole:
+    its runs are whole runs of the storage (_view keeps them so), so each value sits at the same index there."""
+    fmt = _lib.DTYPES[self.dtype]
+    if self._contiguous():
+      out = Tensor(self.rt, self.rows, self.cols, batch=self.batch, dtype="bf16")
+      e, v = self._bfp_planes()
+      self.rt.run(why, "bfp_unpack", fmt, e, v, self.batch, self.rows, self.cols, out.storage.addr,
+                  reads=_bytes(self))
+    else:
+      s = self.storage
+      n = (s.nbytes - s.vals) * (1 if self.dtype == "bfp8" else 2)  # every value the storage holds
+      flat = Tensor(self.rt, n // 16, 16, dtype="bf16")
+      self.rt.run(why, "bfp_unpack", fmt, s.addr, s.addr + s.vals, 1, n // 16, 16, flat.storage.addr,
+                  reads=s.nbytes)
+      out = flat._view(self.rows, self.cols, self.batch, self.offset, self.sb, self.sr, self.sc, self.rep,
+                       self.cyc)._copy()
+    out.lead = self.lead
+    return out
 
   @property
   def shape(self): return (*self.lead, self.rows, self.cols)
@@ -256,17 +277,13 @@ class Tensor:
     """Row-major bytes in the format frombytes takes; block floats come back as bf16, exactly as the unpacker
     decodes them (tensor.py:159-192)."""
     t = self.realize()
-    if t.dtype in BFP or t.layout == "columns":
+    if t.layout == "columns":
       out = Tensor(self.rt, t.rows, t.cols, batch=t.batch, dtype="bf16")
-      if t.layout == "columns":
-        fmt = _lib.DTYPES[t.dtype]
-        self.rt.run("readback", "columns_unpack", fmt, t.storage.addr, t.batch, t.rows, t.cols, out.storage.addr,
-                    reads=_bytes(t))
-      else:
-        e, v = t._bfp_whole()._bfp_planes()
-        self.rt.run("readback", "bfp_unpack", _lib.DTYPES[t.dtype], e, v, t.batch, t.rows, t.cols, out.storage.addr,
-                    reads=_bytes(t))
+      self.rt.run("readback", "columns_unpack", _lib.DTYPES[t.dtype], t.storage.addr, t.batch, t.rows, t.cols,
+                  out.storage.addr, reads=_bytes(t))
       t = out
+    elif t.dtype in BFP:
+      t = t._unpacked("readback")
     if not t._contiguous(): t = t._copy()
     return bytes(self.rt.download(t.addr, t.batch * t.rows * t.cols * t.itemsize))
 
@@ -517,15 +534,13 @@ class Tensor:
     if dtype == self.dtype and self.layout == "plain": return self
     if self.dtype in BFP or self.layout == "columns":
       x = self.realize()
-      out = Tensor(self.rt, x.rows, x.cols, batch=x.batch, dtype="bf16")
-      out.lead = x.lead
       if x.layout == "columns":
+        out = Tensor(self.rt, x.rows, x.cols, batch=x.batch, dtype="bf16")
+        out.lead = x.lead
         self.rt.run("storage", "columns_unpack", _lib.DTYPES[x.dtype], x.storage.addr, x.batch, x.rows, x.cols,
                     out.storage.addr, reads=_bytes(x))
       else:
-        e, v = x._bfp_whole()._bfp_planes()
-        self.rt.run("storage", "bfp_unpack", _lib.DTYPES[x.dtype], e, v, x.batch, x.rows, x.cols, out.storage.addr,
-                    reads=_bytes(x))
+        out = x._unpacked("storage")
       return out.cast(dtype)
     if dtype in BFP:
       x = self if self.dtype in ("bf16", "fp32") else self.float()
@@ -553,13 +568,10 @@ class Tensor:
     out.lead = x.lead
     if x.dtype in BFP:
       e, v = x._bfp_whole()._bfp_planes()
-      if self.rt.recording is None:  # a matmul reads exponents in a narrower range than a block float can hold
-        bad = Storage(self.rt, 4)
-        self.rt.run("range", "bfp_range", _lib.DTYPES[x.dtype], e, v, x.batch, x.rows, x.cols, bad.addr)
-        n = int.from_bytes(self.rt.download(bad.addr, 4), "little")
-        if n:
-          raise ValueError(f"{n} runs of this {x.dtype} tensor hold values under an exponent outside "
-                           f"{'5..255' if x.dtype == 'bfp8' else '3..247'}, which a matmul can't multiply exactly")
+      # a matmul reads exponents in a narrower range than a block float can hold: checked now, or, inside a jit
+      # recording (which can't read the count back), by the jit before each replay
+      if self.rt.recording is None: _check_range(x)
+      else: self.rt.recording.unchecked.add(id(x.storage))
       self.rt.run("columns", "bfp_columns", _lib.DTYPES[x.dtype], e, v, x.batch, x.rows, x.cols, out.storage.addr,
                   reads=_bytes(x))
     else:
@@ -749,6 +761,7 @@ class Tensor:
     if not (pl.dtype == "int32" and pl.batch * pl.rows * pl.cols == 1):
       raise ValueError("matmul_row with rope needs the token's place as one int32")
     q = Tensor(self.rt, 1, heads * d)
+    _written(cc.storage)
     args = _lib.RowArgs(a.addr, nw.addr, 0, 0, w.storage.addr, w.rows, w.cols, _lib.ROW_RMS, _lib.DTYPES[w.dtype],
                         _lib.DTYPES["bf16"], eps)
     tail = _lib.RopeArgs(0, c.addr, sn.addr, q.addr, cc.addr, pl.addr, 0, 0, q.sr, cc.sb, cc.sr, cc.rows, 1, heads, kv,
@@ -809,6 +822,8 @@ class Tensor:
     if not (pl.dtype == "int32" and pl.batch * pl.rows == 1 and pl.cols in (1, x.rows) and pl.sc == 1):
       raise ValueError("rope_put needs places as an int32 row, one for each row or one for all")
     q = Tensor(self.rt, x.rows, heads * d)
+    _written(cc.storage)
+    if vc is not None: _written(vc.storage)
     args = _lib.RopeArgs(x.addr, c.addr, sn.addr, q.addr, cc.addr, pl.addr, x.sr, c.sr, q.sr, cc.sb, cc.sr, cc.rows,
                          x.rows, heads, kv, d, vc.addr if vc is not None else 0, kv * cc.sb if vc is not None else 0,
                          int(pl.cols == 1 and x.rows > 1), 0)
@@ -1182,6 +1197,18 @@ def _realize_reduce(t, into):
            ctypes.byref(out._operand()), reads=_bytes(*low.keep))
 
 
+def _check_range(x):
+  """ValueError if a whole plain block float x holds a nonzero run whose exponent a matmul can't multiply exactly (bfp8
+  below 5, bfp4 outside 3..247): one counting launch, its count read back."""
+  e, v = x._bfp_whole()._bfp_planes()
+  bad = Storage(x.rt, 4)
+  x.rt.run("range", "bfp_range", _lib.DTYPES[x.dtype], e, v, x.batch, x.rows, x.cols, bad.addr)
+  n = int.from_bytes(x.rt.download(bad.addr, 4), "little")
+  if n:
+    raise ValueError(f"{n} runs of this {x.dtype} tensor hold values under an exponent outside "
+                     f"{'5..255' if x.dtype == 'bfp8' else '3..247'}, which a matmul can't multiply exactly")
+
+
 def _b_tiles(b):
   """(format, tiles address, batch, keep-alive) for a matmul's B: its columns tiles, made now if it has none. A block
   float's tiles are kept with its storage, per view, until something writes the storage; inside a jit recording they
@@ -1229,6 +1256,7 @@ class Recording:
   """Launches captured into a HIP graph for replay, holding the memory they allocated (tensor.py:1171-1229)."""
   def __init__(self, rt):
     self.rt, self.graph, self.storages, self.held, self.active = rt, None, [], [], False
+    self.unchecked = set()  # ids of block-float storages laid out as a matmul's B with no exponent check
 
   def __enter__(self):
     if self.rt.recording is not None: raise RuntimeError("cannot nest recordings on the same runtime")
@@ -1278,7 +1306,7 @@ def jit(f):
   writes (put, assign, realize into) is copied back after each call. A replay returns the recorded results, which the
   next call overwrites. Keep input shapes, dtypes and layouts fixed; a block-float or by-columns input is taken as a
   whole tensor, not a view."""
-  state = {"signature": None, "rec": None, "ins": None, "out": None, "wrote": ()}
+  state = {"signature": None, "rec": None, "ins": None, "out": None, "wrote": (), "check": ()}
 
   @functools.wraps(f)
   def run(*xs):
@@ -1306,10 +1334,13 @@ def jit(f):
       finally:
         written, rt.written = rt.written, None
       wrote = [i for i, t in enumerate(ins) if id(t.storage) in written]
-      state.update(rec=rec, ins=ins, out=out, wrote=wrote)
+      check = [i for i, t in enumerate(ins) if id(t.storage) in rec.unchecked]  # block-float inputs used as a B
+      state.update(rec=rec, ins=ins, out=out, wrote=wrote, check=check)
+      for i in check: _check_range(xs[i])
       rec.send()
     else:
       ins = state["ins"]
+      for i in state["check"]: _check_range(xs[i])
       for x, t in zip(xs, ins):
         if x.storage is not t.storage or x.offset != t.offset: _copy_whole(x, t)
       state["rec"].send()

@@ -8,8 +8,8 @@ Reference sources restated here:
   models/gpt2.py:19-30    bfp(a, dtype): the chip's cast, as values
   kernels.py:1074-1081    NIBBLE: the bfp4 rounding, "no sign on a zero"
   kernels.py:1108-1114    put_kernel's bfp8 rounding, same rule, "a 0 loses its sign"
-  tensix.py:6-7, 14-21    the 32x32 tile of four 16x16 faces; 64 exponents then values;
-                          bfp4 two to a byte, first in the low nibble
+  tensix.py:14-21         a run of 16 values shares one exponent; bfp8 sign+7 bits, bfp4 sign+3 bits read as
+                          the top 3 of bfp8's
   tensor.py:1093-1104     _bf16s: the unpacker's exact bfp -> bf16 bits, signed zero -> -inf
 
 How each function is pinned (tests/test_oracle.py):
@@ -22,8 +22,9 @@ How each function is pinned (tests/test_oracle.py):
   decode_bits    every bfp8 byte x 256 exponents against float arithmetic +-mag * 2^(e-133) where that
                  is a normal bf16; the -inf rule for a signed zero and the mod-256 wrap are "as restated"
                  (reachable only through inputs the packers never write)
-  tile_bytes     round trip: decode_tile(tile_bytes(a)) == bf16_bits(bfp(a)) and the element position
-                 formula against an explicit face walk
+
+The reference's 32x32 DRAM tile byte order (tensix.py:6-7) is not restated: the device layouts here are this
+library's own, and what crosses the boundary (tobytes, tolist) is bf16 values, which decode_bits pins.
 """
 import numpy as np
 
@@ -126,38 +127,3 @@ def decode_fields(top, q, dtype="bfp8"):
   """bf16 bits of a block float given as (top, q) from bfp_fields, via the unpacker rule."""
   e = np.repeat(np.asarray(top), RUN, axis=-1)
   return decode_bits(e, sign_magnitude(q, dtype), dtype)
-
-
-# The reference's DRAM tile: datum (r, c) of a 32x32 tile at (r // 16 * 2 + c // 16) * 256 + r % 16 * 16 + c % 16
-# (tensix.py:6-7). A block-float tile is 64 exponent bytes, one per face row, then the values (tensix.py:14-21).
-def tile_position(r, c):
-  r, c = np.asarray(r), np.asarray(c)
-  return (r // 16 * 2 + c // 16) * 256 + r % 16 * 16 + c % 16
-
-
-def tile_bytes(a, dtype="bfp8"):
-  """One 32x32 matrix a, cast to dtype, as the reference's tile bytes (64 exponents, then 1024 or 512 value bytes)."""
-  a = np.asarray(a)
-  if a.shape != (32, 32): raise ValueError("tile_bytes takes one 32 x 32 tile")
-  top, q = bfp_fields(a, dtype)  # top (32, 2): row r, column half h
-  sm = sign_magnitude(q, dtype)
-  flat = np.zeros(1024, np.int64)
-  rr, cc = np.meshgrid(np.arange(32), np.arange(32), indexing="ij")
-  flat[tile_position(rr, cc)] = sm
-  exps = np.zeros(64, np.int64)
-  for r in range(32):
-    for h in range(2): exps[tile_position(r, 16 * h) // 16] = top[r, h]
-  if dtype == "bfp8": vals = flat
-  else: vals = flat[0::2] | flat[1::2] << 4
-  return np.concatenate([exps, vals]).astype(np.uint8).tobytes()
-
-
-def decode_tile(tile, dtype="bfp8"):
-  """The reference tile bytes back to a (32, 32) array of bf16 bits, as _bf16s does (tensor.py:1093-1104)."""
-  t = np.frombuffer(tile, np.uint8).astype(np.int64)
-  exps, raw = t[:64], t[64:]
-  vals = raw if dtype == "bfp8" else np.stack([raw & 15, raw >> 4], -1).reshape(-1)
-  i = np.arange(1024)
-  bits = decode_bits(exps[i // 16], vals, dtype)
-  rr, cc = np.meshgrid(np.arange(32), np.arange(32), indexing="ij")
-  return bits[tile_position(rr, cc)]

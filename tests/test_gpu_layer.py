@@ -71,6 +71,30 @@ def test_prefill_matches_numpy(block):
   assert np.abs(got_kv[:, :n] - kv[:, :n]).max() < 0.03 * np.abs(kv[:, :n]).max() and not got_kv[:, n:].any()
 
 
+def test_prefill_2048_matches_numpy_on_rows(block):
+  # BASELINE config 5's prefill at its configured 2048 tokens: from 512 rows up the bfp4 products run on the GEMM that
+  # decodes B in registers (qkv on 128 x 384 blocks, o and down with the residual on 128 x 256, gate_up with SiLU x up
+  # on 256 x 256 and a 128-row tail), at the full K of 4096 and 14336. The oracle's layer gives the rows asked for
+  # (every row's keys and values still go into its cache); each within 3% of the block's change, and the cache rows
+  # the block put, all 2048 of them, within 3% of their largest.
+  rt, c, rc, dev, ref, (cos, sin, turn) = block
+  n = size = 2048
+  x = np.random.default_rng(4).standard_normal((n, DIM), dtype=np.float32)
+  cache = Tensor.zeros(rt, size, HD, batch=2 * KV)
+  places = Tensor.of(rt, [list(range(n))], "int32")
+  rot = (dev["cos"].gather(places), dev["sin"].gather(places), dev["turn"])
+  y = llama.layer(Tensor.of(rt, x[None], "fp32"), dev, c, rot, places.reshape(1, n, 1), cache, places)
+  got = np.frombuffer(y.tobytes(), np.float32).reshape(n, DIM)
+  rows = [0, 1, 255, 511, 512, 1024, 1500, 2047]
+  mask = np.where(np.arange(size) > np.arange(n)[:, None], np.float32(-1e9), np.float32(0))
+  kv = np.zeros((2 * KV, size, HD))
+  want = L.layer(x, ref, rc, (cos[:n], sin[:n], turn), mask, kv, range(n), only=rows)
+  change, err = np.abs(want - x[rows]).max(), np.abs(got[rows] - want).max()
+  assert change > 0.5 and err < 0.03 * change, (err, change)
+  got_kv = B.bf16_floats(np.frombuffer(cache.tobytes(), np.uint16)).reshape(2 * KV, size, HD)
+  assert np.abs(got_kv - kv).max() < 0.03 * np.abs(kv).max()
+
+
 def test_batch32_decode_matches_numpy_per_slot(block):
   rt, c, rc, dev, ref, (cos, sin, turn) = block
   S, size, place = 32, 4096, 4095

@@ -72,6 +72,27 @@ def test_smollm_full_size_decode_matches_numpy(rt):
     if top2[1] - top2[0] > 2 * err: assert got_toks[s] == want_toks[s], s
 
 
+@pytest.mark.parametrize("mode", ["bf16", "bfp8"])
+def test_chunked_prefill_matches_numpy(rt, mode):
+  # test_models.py:1531-1547: a 70-token prompt in chunks of 32, 32 and 6 (each chunk's scores a chunk by the cache),
+  # against the oracle's chunked prefill, then one decode step at place 70 from the caches the chunks filled, each
+  # within 3% of the largest logit; bad chunk arguments raise ValueError
+  c, ref, dc, dw = setup(rt, 2, 256, mode, places=96, seed=29)
+  prompt = [int(i) for i in np.random.default_rng(30).integers(0, 256, 70)]
+  for ids, chunk in (([], 32), (prompt, 0), (prompt, -1)):
+    with pytest.raises(ValueError, match="prefill"): llama.prefill(ids, dw, dc, llama.kv_cache(rt, dc, 96), chunk)
+  rcaches = L.kv_cache(c, 96)
+  want = L.prefill(prompt, ref, c, rcaches, 32)[0]
+  caches = llama.kv_cache(rt, dc, 96)
+  got = np.frombuffer(llama.prefill(prompt, dw, dc, caches, 32).tobytes(), np.float32)
+  assert np.abs(got - want).max() < 0.03 * np.abs(want).max(), np.abs(got - want).max()
+  nxt = int(want.argmax())
+  got = np.frombuffer(llama.forward(Tensor.of(rt, [[nxt]], "int32"), Tensor.of(rt, [[70]], "int32"), dw, dc,
+                                    caches).tobytes(), np.float32)
+  want = L.forward([nxt], [70], ref, c, rcaches)[0]
+  assert np.abs(got - want).max() < 0.03 * np.abs(want).max(), np.abs(got - want).max()
+
+
 def test_jit_decode_matches_eager(rt):
   c, ref, dc, dw = setup(rt, 2, 256, "bfp8", places=64)
   prompt = [3, 1, 4, 1, 5, 9, 2, 6]

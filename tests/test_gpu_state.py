@@ -71,13 +71,20 @@ def test_assign_overlapping_views(rt):
       x[:, left].assign(source + 1 if add else source)
       want[:, left] = a[:, right] + int(add)
       assert np.array_equal(value(x)[0], want), (left, add)
-  # a block float's view takes another block float's values (put row by row, each run rounded as a cast rounds it,
-  # which leaves values already on a block float's grid as they are)
+  # a block float's view takes the values of an overlapping view of itself, both ways (decoded whole first, then put
+  # row by row, each run rounded as a cast rounds it, which leaves values already on a block float's grid as they are)
+  for fmt in ("bfp8", "bfp4"):
+    for left, right in ((slice(32, None), slice(None, -32)), (slice(None, -32), slice(32, None))):
+      x = Tensor.of(rt, a.tolist()).cast(fmt).realize()
+      want = value(x)[0]
+      x[:, left].assign(x[:, right])
+      want[:, left] = want[:, right].copy()
+      assert np.array_equal(value(x)[0], want), (fmt, left)
+  # a strided block-float view reads back and casts as its values
   x = Tensor.of(rt, a.tolist()).cast("bfp8").realize()
-  want = value(x)[0]
-  x[:, 32:].assign(Tensor.of(rt, want[:, :-32].tolist()).cast("bfp8"))
-  want[:, 32:] = want[:, :-32].copy()
-  assert np.array_equal(value(x)[0], want)
+  whole = value(x)[0]
+  assert np.array_equal(value(x[8:40:2, 16:208])[0], whole[8:40:2, 16:208])
+  assert np.array_equal(value(x[:, 48:112].cast("bf16"))[0], whole[:, 48:112])
 
 
 def test_realize_overlapping_destination(rt):
@@ -131,6 +138,18 @@ def test_wait_times_out_and_the_stream_drains(rt):
   with pytest.raises(ValueError): rt.sleep(11)
 
 
+def test_open_device(chip):
+  # test_device.py:69 and docs/api.md:43-45: while a Chip holds the GPU, a second opener gets RuntimeError, so two live
+  # runtimes never share one device (nor the device's static working memory); a GPU that isn't there is a ValueError.
+  # A runtime made without a chip shares the open one.
+  from baretile_amd import pci
+  with pytest.raises(RuntimeError, match="already open"): pci.open_device()
+  with pytest.raises(ValueError, match="GPUs"): pci.open_device(64)
+  r = Runtime()
+  assert r.chip is chip
+  r.close()
+
+
 def test_takeover_and_closed_runtime(chip):
   # test_device.py:486 and docs/api.md:38-63: a new runtime on the chip takes over, and the old one's tensors and
   # recordings then raise RuntimeError, as does a closed runtime's
@@ -177,6 +196,33 @@ def test_matmul_refuses_exponents_it_cannot_read(rt, fmt):
   assert np.array_equal(value(w)[0], B.bfp(a, fmt))
   with pytest.raises(ValueError, match="exponent"): w.columns()
   with pytest.raises(ValueError, match="exponent"): (Tensor.of(rt, np.ones((2, 64)).tolist()) @ w).realize()
+  bad = w
   a[3, :16] = 1.0
   w = Tensor.of(rt, a.tolist()).cast(fmt).columns()
   assert np.array_equal(value(Tensor.of(rt, np.eye(64).tolist()) @ w)[0], B.bfp(a, fmt))
+  # a jit input used as B is checked on every call, the recorded and replayed ones too, which lay it out inside a
+  # capture that can't read the count back
+  x = Tensor.of(rt, np.eye(64).tolist())
+  good = Tensor.of(rt, a.tolist()).cast(fmt)
+  f = jit(lambda b: x @ b)
+  for i in range(4):
+    assert np.array_equal(value(f(good))[0], B.bfp(a, fmt)), i
+    with pytest.raises(ValueError, match="exponent"): f(bad)
+
+
+def test_jit_copies_back_a_cache_written_by_rope_put(rt):
+  # rope_put writes key and value rows into its cache: a jit whose input is that cache leaves the rows in the caller's
+  # tensor after each call, the replays included, as eager calls do
+  rng = np.random.default_rng(9)
+  heads, kv, d, size = 2, 1, 64, 16
+  nh = heads + 2 * kv
+  cos, sin = Tensor.of(rt, np.ones((1, nh * d)).tolist()), Tensor.of(rt, np.zeros((1, nh * d)).tolist())
+  f = jit(lambda x, cache, at: x.rope_put(cos, sin, cache, at, heads, kv))
+  for i in range(3):
+    rows = B.bf16(rng.normal(0, 1, (1, nh * d)))
+    cache = Tensor.zeros(rt, size, d, batch=2 * kv)
+    q = f(Tensor.of(rt, rows.tolist()), cache, Tensor.of(rt, [[i + 3]], "int32"))
+    want = np.zeros((2 * kv, size, d))
+    want[:, i + 3] = rows[0, heads * d:].reshape(2 * kv, d)
+    assert np.array_equal(value(cache), want), i
+    assert np.array_equal(value(q)[0], rows[:, :heads * d]), i

@@ -108,19 +108,6 @@ def test_decode_bits_against_float_arithmetic():
   assert np.array_equal(B.bf16_floats(b4)[9:16], (-np.arange(1, 8) * 2.0).astype(np.float32))
 
 
-@pytest.mark.parametrize("fmt", B.FORMATS)
-def test_reference_tile_bytes_round_trip(fmt):
-  rng = np.random.default_rng(7)
-  a = B.bf16(rng.normal(0, 1, (32, 32)) * np.exp(rng.normal(0, 2, (32, 32))))
-  tile = B.tile_bytes(a, fmt)
-  assert len(tile) == 64 + (1024 if fmt == "bfp8" else 512)
-  assert np.array_equal(B.bf16_floats(B.decode_tile(tile, fmt)), B.bfp(a, fmt).astype(np.float32))
-  # the face walk of tensix.py:6-7, done explicitly
-  for r, c in ((0, 0), (0, 17), (15, 15), (16, 0), (17, 31), (31, 16)):
-    face = (r // 16) * 2 + (c // 16)
-    assert B.tile_position(r, c) == face * 256 + (r % 16) * 16 + (c % 16)
-
-
 # ---- matmul and elementwise -------------------------------------------------------------------------------------
 
 def test_matmul_known_answers():
