@@ -308,6 +308,13 @@ int bt_graph_end(bt_runtime *rt, void **exec) {
   hipError_t e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
   hipGraphDestroy(g);
   if (e != hipSuccess) return fail(BT_ESTATE, "instantiating the graph: %s", hipGetErrorString(e));
+  // the executable graph's device-side state (its kernel packets and arguments) goes to the device now, queued on
+  // the stream, rather than as part of its first launch
+  e = hipGraphUpload(x, r->stream);
+  if (e != hipSuccess) {
+    (void)hipGraphExecDestroy(x);
+    return fail(BT_ESTATE, "uploading the graph: %s", hipGetErrorString(e));
+  }
   *exec = (void *)x;
   return BT_OK;
 }
