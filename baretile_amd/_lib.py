@@ -93,6 +93,9 @@ SIGNATURES = {
   "bt_matmul_row": [RT, POINTER(RowArgs)], "bt_rope_put": [RT, POINTER(RopeArgs)],
   "bt_put_bfp": [RT, c_int, U64, U64, I64, I64, I64, I64, I64, U64, I64, U64, I64, I64],
   "bt_matmul_row_rope": [RT, POINTER(RowArgs), POINTER(RopeArgs)],
+  "bt_matmul_rope_put": [RT, POINTER(Operand), c_int, U64, I64, I64, I64, POINTER(RopeArgs)],
+  "bt_matmul_residual_rms": [RT, POINTER(Operand), c_int, U64, I64, I64, I64, U64, I64, U64, I64, U64, c_float, U64,
+                             I64],
   "bt_matmul_swiglu": [RT, POINTER(Operand), c_int, U64, I64, I64, I64, POINTER(Operand)],
   "bt_rms_rows": [RT, U64, I64, I64, I64, U64, c_float, U64, I64],
   "bt_gather": [RT, c_int, U64, I64, I64, I64, U64, I64, U64, I64],

@@ -1,5 +1,6 @@
 // Fused elementwise programs, reductions, and the row gather and put that fill and read caches.
 #include "program.h"
+#include "rows.h"
 #include <algorithm>
 
 namespace bt {
@@ -476,38 +477,12 @@ __global__ void __launch_bounds__(256) rope_put8_kernel(const bt_rope_args a, co
   const uint4 xa = *(const uint4 *)(x + j), xb = *(const uint4 *)(x + j + half);
   const uint4 ca = *(const uint4 *)(cs + j), cb = *(const uint4 *)(cs + j + half);
   const uint4 sa = *(const uint4 *)(sn + j), sb = *(const uint4 *)(sn + j + half);
-  const uint32_t xw[2][4] = {{xa.x, xa.y, xa.z, xa.w}, {xb.x, xb.y, xb.z, xb.w}};
-  const uint32_t cw[2][4] = {{ca.x, ca.y, ca.z, ca.w}, {cb.x, cb.y, cb.z, cb.w}};
-  const uint32_t sw[2][4] = {{sa.x, sa.y, sa.z, sa.w}, {sb.x, sb.y, sb.z, sb.w}};
-  uint32_t o[2][4];
-#pragma unroll
-  for (int w = 0; w < 4; w++) {
-    o[0][w] = o[1][w] = 0u;
-#pragma unroll
-    for (int e = 0; e < 2; e++) {
-      const int sh = 16 * e;
-      const float x1 = bf16_value(xw[0][w] >> sh & 0xFFFFu), x2 = bf16_value(xw[1][w] >> sh & 0xFFFFu);
-      const float y1 = __fsub_rn(__fmul_rn(x1, bf16_value(cw[0][w] >> sh & 0xFFFFu)),
-                                 __fmul_rn(x2, bf16_value(sw[0][w] >> sh & 0xFFFFu)));
-      const float y2 = __fadd_rn(__fmul_rn(x2, bf16_value(cw[1][w] >> sh & 0xFFFFu)),
-                                 __fmul_rn(x1, bf16_value(sw[1][w] >> sh & 0xFFFFu)));
-      o[0][w] |= bf16_packed(y1) << sh;
-      o[1][w] |= bf16_packed(y2) << sh;
-    }
-  }
-  uint16_t *dst;
-  if (hh < a.heads) {
-    dst = (uint16_t *)(uintptr_t)a.q + (int64_t)i * a.q_sr + (int64_t)hh * a.head_dim;
-  } else {
-    const int place = ((const int32_t *)(uintptr_t)a.places)[a.one_place ? 0 : i];
-    if (place < 0 || place >= a.cache_rows) return;
-    const int hk = hh - a.heads;
-    const bool own = a.vcache && hk >= a.kv;
-    dst = (uint16_t *)(uintptr_t)(own ? a.vcache : a.cache) + (int64_t)(own ? hk - a.kv : hk) * a.cache_sh +
-          (int64_t)i * a.cache_tsh + (int64_t)place * a.cache_sr;
-  }
-  *(uint4 *)(dst + j) = make_uint4(o[0][0], o[0][1], o[0][2], o[0][3]);
-  *(uint4 *)(dst + j + half) = make_uint4(o[1][0], o[1][1], o[1][2], o[1][3]);
+  uint4 oa, ob;
+  rope8(xa, xb, ca, cb, sa, sb, oa, ob);
+  uint16_t *dst = rope_dst(a, i, hh);
+  if (!dst) return;
+  *(uint4 *)(dst + j) = oa;
+  *(uint4 *)(dst + j + half) = ob;
 }
 
 }  // namespace bt
@@ -538,58 +513,54 @@ extern "C" int bt_rope_put(bt_runtime *rt, const bt_rope_args *args) {
 
 namespace bt {
 
-// RMSNorm of one row a block. Rows of up to 8192 columns (k a multiple of 4, 16-byte aligned rows) are fetched
-// whole into registers by 16-byte loads, all issued before the first is used, so a row costs one trip to memory;
+// RMSNorm of one row a block. Rows of up to 8192 columns (k a multiple of 4, 16-byte aligned rows) are fetched whole
+// into registers by 16-byte loads, every load issued before the first is used, so a row costs one trip to memory;
 // longer or unaligned rows loop over the columns and read them twice.
 template <bool REGS>
-__global__ void __launch_bounds__(256) rms_rows_kernel(const float *x, int64_t k, int64_t x_sr, const uint16_t *w,
-                                                       float eps, uint16_t *out, int64_t out_sr) {
-  __shared__ float part[4];
-  const int tid = threadIdx.x, lane = tid & 63, wib = tid >> 6;
+__global__ void __launch_bounds__(RMS_THREADS) rms_rows_kernel(const float *x, int64_t k, int64_t x_sr,
+                                                               const uint16_t *w, float eps, uint16_t *out,
+                                                               int64_t out_sr) {
+  __shared__ float part[RMS_THREADS / 64];
+  const int tid = threadIdx.x;
   const float *xr = x + (int64_t)blockIdx.x * x_sr;
   uint16_t *o = out + (int64_t)blockIdx.x * out_sr;
-  constexpr int NV = 8;  // 16-byte groups a thread holds: 8 x 4 x 256 = 8192 columns
-  float4 v[REGS ? NV : 1];
-  uint2 wv[REGS ? NV : 1];  // the weights, fetched with the row (one trip for both)
-  float ss = 0.0f;
   if constexpr (REGS) {
+    float4 v[RMS_NV];
+    uint2 wv[RMS_NV];  // the weights, fetched with the row (one trip for both)
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-      const int64_t c = ((int64_t)i * 256 + tid) * 4;
+    for (int i = 0; i < RMS_NV; i++) {
+      const int64_t c = ((int64_t)i * RMS_THREADS + tid) * 4;
       v[i] = c < k ? *(const float4 *)(xr + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       wv[i] = c < k ? *(const uint2 *)(w + c) : make_uint2(0u, 0u);
     }
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
+    for (int i = 0; i < RMS_NV; i++) {
       v[i].x = round_packed(v[i].x), v[i].y = round_packed(v[i].y);
       v[i].z = round_packed(v[i].z), v[i].w = round_packed(v[i].w);
-      ss += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
+    }
+    const float r = rms_scale(v, k, eps, part);
+#pragma unroll
+    for (int i = 0; i < RMS_NV; i++) {
+      const int64_t c = ((int64_t)i * RMS_THREADS + tid) * 4;
+      if (c < k) *(uint2 *)(o + c) = rms_out(v[i], r, wv[i]);
     }
   } else {
-    for (int64_t c = tid; c < k; c += 256) {
+    const int lane = tid & 63, wib = tid >> 6;
+    float ss = 0.0f;
+    for (int64_t c = tid; c < k; c += RMS_THREADS) {
       const float e = round_packed(xr[c]);
       ss += e * e;
     }
-  }
 #pragma unroll
-  for (int s = 32; s > 0; s >>= 1) ss += __shfl_xor(ss, s, 64);
-  if (lane == 0) part[wib] = ss;
-  __syncthreads();
-  const float total = ((part[0] + part[1]) + part[2]) + part[3];
-  const float r = 1.0f / sqrtf(total / (float)k + eps);
-  if constexpr (REGS) {
+    for (int s = 32; s > 0; s >>= 1) ss += __shfl_xor(ss, s, 64);
+    if (lane == 0) part[wib] = ss;
+    __syncthreads();
+    float total = part[0];
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-      const int64_t c = ((int64_t)i * 256 + tid) * 4;
-      if (c < k) {
-        uint2 ov;
-        ov.x = bf16_packed(v[i].x * r * bf16_value(wv[i].x & 0xFFFFu)) | bf16_packed(v[i].y * r * bf16_value(wv[i].x >> 16)) << 16;
-        ov.y = bf16_packed(v[i].z * r * bf16_value(wv[i].y & 0xFFFFu)) | bf16_packed(v[i].w * r * bf16_value(wv[i].y >> 16)) << 16;
-        *(uint2 *)(o + c) = ov;
-      }
-    }
-  } else {
-    for (int64_t c = tid; c < k; c += 256) o[c] = (uint16_t)bf16_packed(round_packed(xr[c]) * r * bf16_value(w[c]));
+    for (int i = 1; i < RMS_THREADS / 64; i++) total += part[i];
+    const float r = 1.0f / sqrtf(total / (float)k + eps);
+    for (int64_t c = tid; c < k; c += RMS_THREADS)
+      o[c] = (uint16_t)bf16_packed(round_packed(xr[c]) * r * bf16_value(w[c]));
   }
 }
 
@@ -603,7 +574,7 @@ extern "C" int bt_rms_rows(bt_runtime *rt, uint64_t x, int64_t rows, int64_t k, 
   if (!x || !w || !out) return fail(BT_EINVAL, "rms_rows needs x, w and out");
   if (rows < 1 || rows >= (1ll << 31) || k < 1) return fail(BT_EINVAL, "rms_rows shape %lld x %lld", (long long)rows, (long long)k);
   const bool regs = k <= 8192 && k % 4 == 0 && x % 16 == 0 && x_sr % 4 == 0 && w % 8 == 0 && out % 8 == 0 && out_sr % 4 == 0;
-  (regs ? rms_rows_kernel<true> : rms_rows_kernel<false>)<<<(unsigned)rows, 256, 0, r->stream>>>(
+  (regs ? rms_rows_kernel<true> : rms_rows_kernel<false>)<<<(unsigned)rows, RMS_THREADS, 0, r->stream>>>(
       (const float *)(uintptr_t)x, k, x_sr, (const uint16_t *)(uintptr_t)w, eps, (uint16_t *)(uintptr_t)out, out_sr);
   BT_LAUNCHED("rms_rows");
   return BT_OK;

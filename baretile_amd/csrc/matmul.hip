@@ -14,7 +14,7 @@
 //     with v_cvt_scalef32_pk_bf16_fp8 (7 instructions for 8 values: a mask, a rotate and a mask, 4 conversions).
 //   B-side scaling (more rows): each weight gets its power of two with v_ldexp_f32, reading the biased exponent byte
 //     straight from the tile.
-#include "program.h"
+#include "rows.h"
 #include <cstdlib>
 
 namespace bt {
@@ -2327,14 +2327,18 @@ static void launch_stream_m(const MatmulArgs &args, int epi, int dt, int splits,
   else if (dt == BT_FP32) skinny_stream_kernel<FMT, MT, 1, BT_FP32><<<blocks, threads, 0, s>>>(args, groups, stages, part);
   else skinny_stream_kernel<FMT, MT, 1, BT_BF16><<<blocks, threads, 0, s>>>(args, groups, stages, part);
 }
-static bool launch_stream(Runtime *r, const MatmulArgs &args, int fmt, bool swi) {
+// The streaming kernels' plan for a product: whether they take it, and its split of K.
+struct StreamPlan {
+  int mt, splits, stages;
+};
+static bool stream_plan(const MatmulArgs &args, StreamPlan *p) {
   const bt_operand &a = args.a;
   if (args.batch != 1 || args.m < 5 || args.m > 32 || args.k % 256 || args.chunks <= 12 || a.sc != 1 || a.ptr % 16 ||
       a.sr % 8 ||
       ((int64_t)(args.m - 1) * a.sr + args.k) * 2 >= (1ll << 32) ||
       (int64_t)args.chunks * Tile<BT_BF16>::bytes >= (1ll << 32))
     return false;
-  const int mt = args.m > 16 ? 2 : 1, total = args.chunks / 4;
+  const int total = args.chunks / 4;
   // the splits follow from groups of 4 runs whatever the kernel's block, so every format of B sums K alike; SiLU x up
   // takes those of the plain product of its shape (one split: each gate run beside its up run in a block; more:
   // partial sums per run)
@@ -2342,25 +2346,37 @@ static bool launch_stream(Runtime *r, const MatmulArgs &args, int fmt, bool swi)
   int splits = 1;  // the divisor of the stages that brings the grid nearest 512 blocks
   for (int d = 1; d <= total; d++)
     if (total % d == 0 && std::abs(groups * d - 512) < std::abs(groups * splits - 512)) splits = d;
+  p->mt = args.m > 16 ? 2 : 1;
+  p->splits = splits;
+  p->stages = total / splits;
+  return true;
+}
+static void launch_stream_plan(const MatmulArgs &args, int fmt, int epi, int dt, const StreamPlan &p, float *part,
+                               hipStream_t s) {
+  if (fmt == BT_BF16 && p.mt == 2) launch_stream_m<BT_BF16, 2>(args, epi, dt, p.splits, p.stages, part, s);
+  else if (fmt == BT_BF16) launch_stream_m<BT_BF16, 1>(args, epi, dt, p.splits, p.stages, part, s);
+  else if (fmt == BT_BFP8 && p.mt == 2) launch_stream_m<BT_BFP8, 2>(args, epi, dt, p.splits, p.stages, part, s);
+  else if (fmt == BT_BFP8) launch_stream_m<BT_BFP8, 1>(args, epi, dt, p.splits, p.stages, part, s);
+  else if (p.mt == 2) launch_stream_m<BT_BFP4, 2>(args, epi, dt, p.splits, p.stages, part, s);
+  else launch_stream_m<BT_BFP4, 1>(args, epi, dt, p.splits, p.stages, part, s);
+}
+static bool launch_stream(Runtime *r, const MatmulArgs &args, int fmt, bool swi) {
+  StreamPlan p;
+  if (!stream_plan(args, &p)) return false;
   float *part = nullptr;
-  if (splits > 1) {
-    part = (float *)runtime_scratch(r, (size_t)splits * 16 * mt * args.n * 4);
+  if (p.splits > 1) {
+    part = (float *)runtime_scratch(r, (size_t)p.splits * 16 * p.mt * args.n * 4);
     if (!part) return false;
   }
-  const int epi = splits > 1 ? 0 : swi ? 2 : 1, dt = args.prog.dtype == BT_FP32 ? BT_FP32 : BT_BF16;
-  const int stages = total / splits;
-  if (fmt == BT_BF16 && mt == 2) launch_stream_m<BT_BF16, 2>(args, epi, dt, splits, stages, part, r->stream);
-  else if (fmt == BT_BF16) launch_stream_m<BT_BF16, 1>(args, epi, dt, splits, stages, part, r->stream);
-  else if (fmt == BT_BFP8 && mt == 2) launch_stream_m<BT_BFP8, 2>(args, epi, dt, splits, stages, part, r->stream);
-  else if (fmt == BT_BFP8) launch_stream_m<BT_BFP8, 1>(args, epi, dt, splits, stages, part, r->stream);
-  else if (mt == 2) launch_stream_m<BT_BFP4, 2>(args, epi, dt, splits, stages, part, r->stream);
-  else launch_stream_m<BT_BFP4, 1>(args, epi, dt, splits, stages, part, r->stream);
-  if (splits > 1) {
+  const int epi = p.splits > 1 ? 0 : swi ? 2 : 1, dt = args.prog.dtype == BT_FP32 ? BT_FP32 : BT_BF16;
+  launch_stream_plan(args, fmt, epi, dt, p, part, r->stream);
+  if (p.splits > 1) {
     const int64_t outs = (int64_t)args.m * (swi ? args.n / 2 : args.n);
     const unsigned rb = (unsigned)((outs + 255) / 256);
-    if (swi) parts_reduce_kernel<BT_BF16, true><<<rb, 256, 0, r->stream>>>(args, splits, 16 * mt, part);
-    else if (dt == BT_FP32) parts_reduce_kernel<BT_FP32, false><<<rb, 256, 0, r->stream>>>(args, splits, 16 * mt, part);
-    else parts_reduce_kernel<BT_BF16, false><<<rb, 256, 0, r->stream>>>(args, splits, 16 * mt, part);
+    const int splits = p.splits, rows = 16 * p.mt;
+    if (swi) parts_reduce_kernel<BT_BF16, true><<<rb, 256, 0, r->stream>>>(args, splits, rows, part);
+    else if (dt == BT_FP32) parts_reduce_kernel<BT_FP32, false><<<rb, 256, 0, r->stream>>>(args, splits, rows, part);
+    else parts_reduce_kernel<BT_BF16, false><<<rb, 256, 0, r->stream>>>(args, splits, rows, part);
   }
   return true;
 }
@@ -2755,5 +2771,184 @@ extern "C" int bt_matmul_swiglu(bt_runtime *rt, const bt_operand *a, int b_fmt, 
       gemm3_kernel<BT_BF16, BT_BF16, 4, GEMM_SWIGLU, 128><<<tb, 512, 0, r->stream>>>(args, mb128, tail, bt_operand{}, nb - tail);
     BT_LAUNCHED("matmul_swiglu");
   }
+  return BT_OK;
+}
+
+// ---- the batched decode step's products with their neighbours fused: their split-K partial sums are summed by the
+// kernel that consumes the product, so neither the product nor its reduction is stored or launched on its own ----
+
+namespace bt {
+
+// 8 neighbouring values of a product row as bf16 bits, two to a word: each the sum of its split-K partials in split
+// order (p, p + stride, ...), rounded half up, as parts_reduce_kernel's bf16 store gives them.
+__device__ __forceinline__ uint4 sum8_bf16(const float *p, int splits, int64_t stride) {
+  float4 lo = *(const float4 *)p, hi = *(const float4 *)(p + 4);
+#pragma unroll 4
+  for (int s = 1; s < splits; s++) {
+    const float4 a = *(const float4 *)(p + s * stride), b = *(const float4 *)(p + s * stride + 4);
+    lo.x += a.x, lo.y += a.y, lo.z += a.z, lo.w += a.w;
+    hi.x += b.x, hi.y += b.y, hi.z += b.z, hi.w += b.w;
+  }
+  return make_uint4(bf16_packed(lo.x) | bf16_packed(lo.y) << 16, bf16_packed(lo.z) | bf16_packed(lo.w) << 16,
+                    bf16_packed(hi.x) | bf16_packed(hi.y) << 16, bf16_packed(hi.z) | bf16_packed(hi.w) << 16);
+}
+
+// bt_rope_put's 8-pair kernel on a product held as split-K partials (row i at part + i * n, split s stride apart).
+__global__ void __launch_bounds__(256) rope_parts_kernel(const bt_rope_args a, const FastDiv hq, const FastDiv nh,
+                                                         uint32_t threads, const float *part, int splits,
+                                                         int64_t stride, int n) {
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  if (t >= threads) return;
+  const int half = a.head_dim / 2;
+  const uint32_t th = fdiv(t, hq), ti = fdiv(th, nh);
+  const int j = 8 * (int)(t - th * hq.d), hh = (int)(th - ti * nh.d), i = (int)ti;
+  const float *x = part + (int64_t)i * n + (int64_t)hh * a.head_dim;
+  const uint16_t *cs = (const uint16_t *)(uintptr_t)a.cos + (int64_t)i * a.cs_sr + (int64_t)hh * a.head_dim;
+  const uint16_t *sn = (const uint16_t *)(uintptr_t)a.sin + (int64_t)i * a.cs_sr + (int64_t)hh * a.head_dim;
+  const uint4 ca = *(const uint4 *)(cs + j), cb = *(const uint4 *)(cs + j + half);
+  const uint4 sa = *(const uint4 *)(sn + j), sb = *(const uint4 *)(sn + j + half);
+  const uint4 xa = sum8_bf16(x + j, splits, stride), xb = sum8_bf16(x + j + half, splits, stride);
+  uint4 oa, ob;
+  rope8(xa, xb, ca, cb, sa, sb, oa, ob);
+  uint16_t *dst = rope_dst(a, i, hh);
+  if (!dst) return;
+  *(uint4 *)(dst + j) = oa;
+  *(uint4 *)(dst + j + half) = ob;
+}
+
+// One row a block: x = residual + the product (its split-K partials summed in split order, then the residual added in
+// fp32, as bt_matmul's residual epilogue does), written out, then bt_rms_rows' RMSNorm of x into h. Every load (the
+// residual, each split's partials, the norm's weights) is issued before the first sum.
+__global__ void __launch_bounds__(RMS_THREADS) residual_rms_kernel(const float *part, int splits, int64_t stride,
+                                                                   int n, const float *res, int64_t res_sr, float *x,
+                                                                   int64_t x_sr, const uint16_t *w, float eps,
+                                                                   uint16_t *h, int64_t h_sr) {
+  __shared__ float lds[RMS_THREADS / 64];
+  constexpr int MAXS = 8;  // splits summed from registers; more are added in a second pass
+  const int tid = threadIdx.x, m = blockIdx.x;
+  const float *p = part + (int64_t)m * n;
+  const float *rr = res + (int64_t)m * res_sr;
+  float *xr = x + (int64_t)m * x_sr;
+  float4 v[RMS_NV], s[RMS_NV];
+  uint2 wv[RMS_NV];
+#pragma unroll
+  for (int i = 0; i < RMS_NV; i++) {
+    const int c = (i * RMS_THREADS + tid) * 4;
+    const bool in = c < n;
+    v[i] = in ? *(const float4 *)(rr + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    wv[i] = in ? *(const uint2 *)(w + c) : make_uint2(0u, 0u);
+    float4 q[MAXS];
+#pragma unroll
+    for (int k = 0; k < MAXS; k++)
+      q[k] = in && k < splits ? *(const float4 *)(p + k * stride + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    s[i] = q[0];
+#pragma unroll
+    for (int k = 1; k < MAXS; k++)
+      if (k < splits) s[i].x += q[k].x, s[i].y += q[k].y, s[i].z += q[k].z, s[i].w += q[k].w;
+    for (int k = MAXS; k < splits; k++) {
+      const float4 t = in ? *(const float4 *)(p + k * stride + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      s[i].x += t.x, s[i].y += t.y, s[i].z += t.z, s[i].w += t.w;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RMS_NV; i++) {
+    const int c = (i * RMS_THREADS + tid) * 4;
+    v[i] = make_float4(v[i].x + s[i].x, v[i].y + s[i].y, v[i].z + s[i].z, v[i].w + s[i].w);
+    if (c < n) *(float4 *)(xr + c) = v[i];
+  }
+#pragma unroll
+  for (int i = 0; i < RMS_NV; i++) {
+    v[i].x = round_packed(v[i].x), v[i].y = round_packed(v[i].y);
+    v[i].z = round_packed(v[i].z), v[i].w = round_packed(v[i].w);
+  }
+  const float r = rms_scale(v, n, eps, lds);
+  uint16_t *hr = h + (int64_t)m * h_sr;
+#pragma unroll
+  for (int i = 0; i < RMS_NV; i++) {
+    const int c = (i * RMS_THREADS + tid) * 4;
+    if (c < n) *(uint2 *)(hr + c) = rms_out(v[i], r, wv[i]);
+  }
+}
+
+// The product's split-K partial sums in the runtime's scratch, by the streaming kernels (partials written even for
+// one split), for a kernel that consumes them. Fails for a product those kernels don't take.
+static int stream_partials(Runtime *r, const bt_operand *a, int b_fmt, uint64_t b, int64_t m, int64_t k, int64_t n,
+                           const char *what, StreamPlan *p, float **part) {
+  if (!a || !a->ptr || !b) return fail(BT_EINVAL, "%s needs A and B", what);
+  if (a->dtype != BT_BF16 || a->rep != 1 || a->cyc != 0) return fail(BT_EINVAL, "%s: A is plain bf16 rows", what);
+  if (b_fmt != BT_BF16 && b_fmt != BT_BFP8 && b_fmt != BT_BFP4) return fail(BT_EINVAL, "B format %d", b_fmt);
+  if (b % 16) return fail(BT_EINVAL, "B's tiles must be 16-byte aligned");
+  if (m < 1 || k < 1 || n < 1 || k > (1 << 30) || n > (1 << 30)) return fail(BT_EINVAL, "%s: shape", what);
+  MatmulArgs args{};
+  args.a = *a;
+  args.b = (const uint8_t *)(uintptr_t)b;
+  args.batch = 1, args.m = (int32_t)m, args.k = (int32_t)k, args.n = (int32_t)n;
+  args.chunks = (int32_t)((k + 63) / 64);
+  args.nruns = (int32_t)((n + 15) / 16);
+  args.mtiles = (int32_t)((m + 15) / 16);
+  args.b_matrix_bytes = 0;
+  args.prog = bt_program{};
+  args.prog.dtype = BT_FP32;
+  args.n_inst = 0;
+  args.out = bt_operand{};
+  if (!stream_plan(args, p))
+    return fail(BT_EINVAL, "%s takes 5 to 32 rows of A (contiguous, 16-byte aligned rows) and K a multiple of 256 "
+                "over 768, not %lld x %lld", what, (long long)m, (long long)k);
+  *part = (float *)runtime_scratch(r, (size_t)p->splits * 16 * p->mt * n * 4);
+  if (!*part)
+    return fail(BT_ESTATE, "%s: no room for the partial sums (inside a graph capture, make the call once before "
+                "capturing so the runtime's scratch has grown)", what);
+  launch_stream_plan(args, b_fmt, 0, BT_FP32, *p, *part, r->stream);
+  BT_LAUNCHED(what);
+  return BT_OK;
+}
+
+}  // namespace bt
+
+extern "C" int bt_matmul_rope_put(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_t b, int64_t m, int64_t k,
+                                  int64_t n, const bt_rope_args *rope) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (!rope) return fail(BT_EINVAL, "matmul_rope_put needs the RoPE arguments");
+  const bt_rope_args &ra = *rope;
+  if (!ra.cos || !ra.sin || !ra.q || !ra.cache || !ra.places) return fail(BT_EINVAL, "matmul_rope_put needs every buffer");
+  if (ra.rows != m || ra.heads < 1 || ra.kv < 1 || ra.head_dim < 16 || ra.head_dim % 16 || ra.cache_rows < 1 ||
+      (int64_t)(ra.heads + 2 * ra.kv) * ra.head_dim != n)
+    return fail(BT_EINVAL, "matmul_rope_put: %lld rows of %lld columns for %d rows of %d heads and %d key heads of %d "
+                "(a multiple of 16)", (long long)m, (long long)n, ra.rows, ra.heads, ra.kv, ra.head_dim);
+  if ((ra.cos | ra.sin | ra.q | ra.cache | ra.vcache) % 16 || (ra.cs_sr | ra.q_sr | ra.cache_sh | ra.cache_sr |
+                                                               ra.cache_tsh) % 8)
+    return fail(BT_EINVAL, "matmul_rope_put writes 16 bytes at a time: tables, q and caches 16-byte aligned, their "
+                "strides multiples of 8");
+  StreamPlan p;
+  float *part;
+  if (int s = stream_partials(r, a, b_fmt, b, m, k, n, "matmul_rope_put", &p, &part)) return s;
+  const uint32_t t8 = (uint32_t)(m * (n / 2) / 8);
+  rope_parts_kernel<<<(t8 + 255) / 256, 256, 0, r->stream>>>(ra, make_fastdiv((uint32_t)(ra.head_dim / 16)),
+                                                             make_fastdiv((uint32_t)(ra.heads + 2 * ra.kv)), t8, part,
+                                                             p.splits, (int64_t)16 * p.mt * n, (int)n);
+  BT_LAUNCHED("matmul_rope_put");
+  return BT_OK;
+}
+
+extern "C" int bt_matmul_residual_rms(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_t b, int64_t m,
+                                      int64_t k, int64_t n, uint64_t residual, int64_t res_sr, uint64_t x, int64_t x_sr,
+                                      uint64_t norm, float eps, uint64_t h, int64_t h_sr) {
+  Runtime *r;
+  if (int s = enter(rt, &r)) return s;
+  if (!residual || !x || !norm || !h) return fail(BT_EINVAL, "matmul_residual_rms needs the residual, x, norm and h");
+  if (n > 4 * RMS_THREADS * RMS_NV || n % 4)
+    return fail(BT_EINVAL, "matmul_residual_rms: rows of at most %d columns, a multiple of 4, not %lld",
+                4 * RMS_THREADS * RMS_NV, (long long)n);
+  if ((residual | x) % 16 || (res_sr | x_sr) % 4 || (norm | h) % 8 || h_sr % 4)
+    return fail(BT_EINVAL, "matmul_residual_rms: fp32 rows 16-byte aligned, bf16 rows 8-byte aligned");
+  StreamPlan p;
+  float *part;
+  if (int s = stream_partials(r, a, b_fmt, b, m, k, n, "matmul_residual_rms", &p, &part)) return s;
+  residual_rms_kernel<<<(unsigned)m, RMS_THREADS, 0, r->stream>>>(part, p.splits, (int64_t)16 * p.mt * n, (int)n,
+                                                          (const float *)(uintptr_t)residual, res_sr,
+                                                          (float *)(uintptr_t)x, x_sr, (const uint16_t *)(uintptr_t)norm,
+                                                          eps, (uint16_t *)(uintptr_t)h, h_sr);
+  BT_LAUNCHED("matmul_residual_rms");
   return BT_OK;
 }

@@ -340,15 +340,22 @@ def slots_layer(x, p, c, rot, keys, values, place):
   of llama.forward(slots=...) (llama.py:293-354). x is (1, S, dim), the stream of the S slots; keys and values are
   (S * kv, size, head) bf16, slot s's key heads at s * kv .. s * kv + kv - 1; rot holds the tables at the place for
   each slot's row; place is a (1, 1) int32 row. The slots' query heads become S * heads attention heads of one row.
-  RoPE and the cache puts run as one kernel (bt_rope_put), in fp32 with one rounding."""
+  RoPE and the cache puts run as one kernel (bt_rope_put), in fp32 with one rounding. The qkv product feeds that kernel
+  its split-K partial sums, and the o product feeds the residual add and the MLP's norm likewise (matmul_rope_put,
+  matmul_residual_rms), with the same results as the separate steps."""
   S, hd, rep = x.rows, head(c), c.heads // c.kv
   if keys.dtype != "bf16": raise ValueError("slots_layer takes bf16 caches")
   h = rms(x, p["input_layernorm"], c)
-  q = h.matmul(p["qkv_proj"]).rope_put(rot[0], rot[1], keys, place, c.heads, c.kv, values=values)
+  q = h.matmul_rope_put(p["qkv_proj"], rot[0], rot[1], keys, place, c.heads, c.kv, values=values)
   o = q.reshape(S * c.heads, 1, hd).attend(keys.repeat_interleave(rep), values.repeat_interleave(rep),
-                                           place.reshape(1, 1, 1))
-  x = (x + o.reshape(1, S, c.heads * hd).matmul(p["o_proj"], "fp32")).realize()
-  return (x + mlp(rms(x, p["post_attention_layernorm"], c), p)).realize()
+                                           place.reshape(1, 1, 1)).reshape(1, S, c.heads * hd)
+  norm = p["post_attention_layernorm"]
+  if x.dtype == "fp32" and x.batch == 1 and norm.dtype == "bf16":
+    x, h = o.matmul_residual_rms(p["o_proj"], x, norm, c.eps)
+  else:
+    x = (x + o.matmul(p["o_proj"], "fp32")).realize()
+    h = rms(x, norm, c)
+  return (x + mlp(h, p)).realize()
 
 
 def starts(w, n, slots, part):

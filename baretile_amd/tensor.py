@@ -805,30 +805,47 @@ class Tensor:
     are separate key and value caches of rows * kv heads, row i's at i * kv .. i * kv + kv - 1 (the slots of
     llama.py:293-354, each with a cache of its own). cos and sin are bf16 rows laid out as self; the tables turn x
     into x cos + (-x2, x1) sin, which leaves the value heads (cos 1, sin 0) as they are."""
-    x, c, sn, cc, pl = self.realize(), cos.realize(), sin.realize(), cache.realize(), places.realize()
-    vc = values.realize() if values is not None else None
-    nh = heads + 2 * kv
-    if not (x.dtype == c.dtype == sn.dtype == cc.dtype == "bf16" and x.batch == 1 and x.cols % nh == 0 and x.sc == 1):
-      raise ValueError(f"rope_put needs bf16 rows of {nh} heads and bf16 tables: {x.shape} {x.dtype}")
-    d = x.cols // nh
-    if not (c.shape[-2:] == sn.shape[-2:] == (x.rows, x.cols) and c.sc == 1 and sn.sc == 1 and c.sr == sn.sr):
-      raise ValueError(f"rope_put needs cos and sin laid out as the rows: {c.shape} {sn.shape} for {x.shape}")
-    plain = lambda t: t.cols == d and t.sc == 1 and t.rep == 1 and not t.cyc and t.layout == "plain"
-    if vc is None and not (cc.batch == 2 * kv and plain(cc)):
-      raise ValueError(f"rope_put needs a plain ({2 * kv}, size, {d}) cache: {cc.shape}")
-    if vc is not None and not (cc.batch == vc.batch == x.rows * kv and vc.dtype == "bf16" and plain(cc) and plain(vc)
-                               and cc.rows == vc.rows and cc.sb == vc.sb and cc.sr == vc.sr):
-      raise ValueError(f"rope_put needs plain ({x.rows * kv}, size, {d}) key and value caches: {cc.shape}")
-    if not (pl.dtype == "int32" and pl.batch * pl.rows == 1 and pl.cols in (1, x.rows) and pl.sc == 1):
-      raise ValueError("rope_put needs places as an int32 row, one for each row or one for all")
-    q = Tensor(self.rt, x.rows, heads * d)
-    _written(cc.storage)
-    if vc is not None: _written(vc.storage)
-    args = _lib.RopeArgs(x.addr, c.addr, sn.addr, q.addr, cc.addr, pl.addr, x.sr, c.sr, q.sr, cc.sb, cc.sr, cc.rows,
-                         x.rows, heads, kv, d, vc.addr if vc is not None else 0, kv * cc.sb if vc is not None else 0,
-                         int(pl.cols == 1 and x.rows > 1), 0)
-    self.rt.run("rope_put", "rope_put", ctypes.byref(args), reads=_bytes(x, c, sn))
+    x = self.realize()
+    if not (x.dtype == "bf16" and x.batch == 1 and x.sc == 1):
+      raise ValueError(f"rope_put needs bf16 rows of one matrix: {x.shape} {x.dtype}")
+    q, args, tables = _rope_args(self.rt, x.rows, x.cols, cos, sin, cache, places, heads, kv, values)
+    args.qkv, args.qkv_sr = x.addr, x.sr
+    self.rt.run("rope_put", "rope_put", ctypes.byref(args), reads=_bytes(x, *tables))
     return q
+
+  def matmul_rope_put(self, w, cos, sin, cache, places, heads, kv, values=None):
+    """(self @ w).rope_put(cos, sin, cache, places, heads, kv, values): for 5 to 32 rows of bf16 against w by columns
+    with a long K (a batched decode step's qkv), the product's split-K partial sums go straight to the RoPE kernel
+    (bt_matmul_rope_put), two launches instead of four, bit for bit the same; other shapes take the two calls."""
+    a = self.realize()
+    if not _stream_fits(a, w): return self.matmul(w).rope_put(cos, sin, cache, places, heads, kv, values)
+    q, args, tables = _rope_args(self.rt, a.rows, w.cols, cos, sin, cache, places, heads, kv, values)
+    self.rt.run("matmul_rope_put", "matmul_rope_put", ctypes.byref(_lib.operand(a.addr, "bf16", 0, a.sr)),
+                _lib.DTYPES[w.dtype], w.storage.addr, a.rows, a.cols, w.cols, ctypes.byref(args),
+                reads=_bytes(a, w, *tables))
+    return q
+
+  def matmul_residual_rms(self, w, residual, norm, eps=1e-5):
+    """(x, h) with x = residual + self @ w in fp32 and h = x.rms_rows(norm, eps): for 5 to 32 rows of bf16 against w by
+    columns with a long K (a batched decode step's o product and the MLP's norm), the product's split-K partial sums
+    are summed in the norm's kernel (bt_matmul_residual_rms), two launches instead of four, bit for bit the same;
+    other shapes take the unfused calls."""
+    a, res, nw = self.realize(), residual.realize(), norm.realize()
+    if not (res.dtype == "fp32" and res.batch == 1 and res.sc == 1 and res.rep == 1 and not res.cyc and
+            res.shape[-2:] == (a.rows, w.cols) and res.layout == "plain"):
+      raise ValueError(f"matmul_residual_rms needs fp32 residual rows of one matrix, {a.rows} x {w.cols}: {res.shape}")
+    if not (nw.dtype == "bf16" and nw._contiguous() and nw.batch * nw.rows * nw.cols == w.cols):
+      raise ValueError(f"matmul_residual_rms needs bf16 norm weights, one for each column: {nw.shape}")
+    if not (_stream_fits(a, w) and w.cols <= 8192 and w.cols % 4 == 0 and res.addr % 16 == 0 and res.sr % 4 == 0):
+      x = (res + self.matmul(w, "fp32")).realize()
+      return x, x.rms_rows(nw, eps)
+    x = Tensor(self.rt, a.rows, w.cols, dtype="fp32")
+    h = Tensor(self.rt, a.rows, w.cols)
+    x.lead = h.lead = res.lead
+    self.rt.run("matmul_residual_rms", "matmul_residual_rms", ctypes.byref(_lib.operand(a.addr, "bf16", 0, a.sr)),
+                _lib.DTYPES[w.dtype], w.storage.addr, a.rows, a.cols, w.cols, res.addr, res.sr, x.addr, x.sr, nw.addr,
+                eps, h.addr, h.sr, reads=_bytes(a, w, res, nw))
+    return x, h
 
   # ---- attention, rows in and out
   def attend(self, k, v, places, window=0, fidelity=None, parts=None, firsts=None, merged=False):
@@ -1195,6 +1212,43 @@ def _realize_reduce(t, into):
   out = _dest(t, into)
   t.rt.run("reduce", "reduce", ctypes.byref(prog), kind, k, src.batch, src.rows, src.cols, sweep, step,
            ctypes.byref(out._operand()), reads=_bytes(*low.keep))
+
+
+def _stream_fits(a, w):
+  """Whether a product of a (realized) against w is one the fused decode-step products take: 5 to 32 bf16 rows of one
+  matrix, contiguous and 16-byte aligned, against w by columns with K a multiple of 256 over 768."""
+  return (isinstance(w, Tensor) and w.rt is a.rt and w.op is None and w.layout == "columns" and w.batch == 1 and
+          a.dtype == "bf16" and a.batch == 1 and a.sc == 1 and a.rep == 1 and not a.cyc and a.layout == "plain" and
+          5 <= a.rows <= 32 and a.cols == w.rows and w.rows % 256 == 0 and w.rows > 768 and a.addr % 16 == 0 and
+          a.sr % 8 == 0)
+
+
+def _rope_args(rt, rows, cols, cos, sin, cache, places, heads, kv, values):
+  """The query tensor and bt_rope_args (qkv left 0) of RoPE and the cache put over `rows` rows of `cols` columns
+  (heads + 2 kv heads), after the checks of rope_put; and the tables it reads."""
+  c, sn, cc, pl = cos.realize(), sin.realize(), cache.realize(), places.realize()
+  vc = values.realize() if values is not None else None
+  nh = heads + 2 * kv
+  if not (c.dtype == sn.dtype == cc.dtype == "bf16" and cols % nh == 0):
+    raise ValueError(f"rope_put needs rows of {nh} heads and bf16 tables and caches: {rows} x {cols}")
+  d = cols // nh
+  if not (c.shape[-2:] == sn.shape[-2:] == (rows, cols) and c.sc == 1 and sn.sc == 1 and c.sr == sn.sr):
+    raise ValueError(f"rope_put needs cos and sin laid out as the rows: {c.shape} {sn.shape} for {rows} x {cols}")
+  plain = lambda t: t.cols == d and t.sc == 1 and t.rep == 1 and not t.cyc and t.layout == "plain"
+  if vc is None and not (cc.batch == 2 * kv and plain(cc)):
+    raise ValueError(f"rope_put needs a plain ({2 * kv}, size, {d}) cache: {cc.shape}")
+  if vc is not None and not (cc.batch == vc.batch == rows * kv and vc.dtype == "bf16" and plain(cc) and plain(vc)
+                             and cc.rows == vc.rows and cc.sb == vc.sb and cc.sr == vc.sr):
+    raise ValueError(f"rope_put needs plain ({rows * kv}, size, {d}) key and value caches: {cc.shape}")
+  if not (pl.dtype == "int32" and pl.batch * pl.rows == 1 and pl.cols in (1, rows) and pl.sc == 1):
+    raise ValueError("rope_put needs places as an int32 row, one for each row or one for all")
+  q = Tensor(rt, rows, heads * d)
+  _written(cc.storage)
+  if vc is not None: _written(vc.storage)
+  args = _lib.RopeArgs(0, c.addr, sn.addr, q.addr, cc.addr, pl.addr, 0, c.sr, q.sr, cc.sb, cc.sr, cc.rows, rows,
+                       heads, kv, d, vc.addr if vc is not None else 0, kv * cc.sb if vc is not None else 0,
+                       int(pl.cols == 1 and rows > 1), 0)
+  return q, args, (c, sn)
 
 
 def _check_range(x):

@@ -3,12 +3,14 @@
 The headline is the decode GEMV on block-float weights: one launch of the fused matmul kernel for
 x [B, 576] @ W [576, 49152] with W packed as bfp4 (B = 1) or bfp8, fp32 accumulation and a bf16 result. Inputs are
 resident in HBM before timing starts. Each step reads a different copy of W from a pool larger than the 256 MB
-Infinity Cache, so every step streams its weights from HBM. Steps are captured into one HIP graph and replayed, and
-HIP events on the runtime's stream bracket the timed replay. The pool holds 1 GiB of copies, four times the Infinity
-Cache, and every launch takes the next copy in a cursor that runs on across the warmup and timed graphs, so a timed
-launch reads a copy last touched more than 600 MB of traffic earlier, whatever --steps is. `value` is the achieved HBM bandwidth of the headline
-configuration: the algorithmic bytes of one step (packed W, x and the output) over the measured time per step. The
-other five GEMV configurations (bfp4 and bfp8 at B = 1, 4, 16) are in "configs".
+Infinity Cache, so every step streams its weights from HBM. The steps are launched back to back on the runtime's
+stream between two HIP events, queued behind a device-side wait that lasts until the host has queued them all, so the
+events bracket the launches' device time and not the host's time to queue them. The pool holds 1 GiB of copies, four
+times the Infinity Cache, and every launch takes the next copy in a cursor that runs on across the warmup and timed
+launches, so a timed launch reads a copy last touched more than 600 MB of traffic earlier, whatever --steps is.
+`value` is the achieved HBM bandwidth of the headline configuration: the algorithmic bytes of one step (packed W, x
+and the output) over the measured time per step. The other five GEMV configurations (bfp4 and bfp8 at B = 1, 4, 16)
+are in "configs". The other legs time HIP graph replays of their steps the same way.
 
 The other BASELINE configurations are reported beside it, each against its own roofline:
   "c1"        config 1, relu(x @ W) with x [128, 576] and W [576, 1536] in bfp8, in one launch;
@@ -49,7 +51,7 @@ def log(*a):
 
 def gpu_leg(fmt, rows, steps, warmup):
   """Times `steps` GEMV launches on one GPU, then a plain streaming read of the same weight bytes, then a launch that
-  does almost nothing, each in a graph of `steps` launches. Returns (us per GEMV, its result, x, w, us per streaming
+  does almost nothing, each as `steps` launches back to back. Returns (us per GEMV, its result, x, w, us per streaming
   read, us per near-empty launch)."""
   from baretile_amd import _lib
   from baretile_amd.runtime import Runtime
@@ -88,32 +90,22 @@ def gpu_leg(fmt, rows, steps, warmup):
       cursor[0] += 1
 
     def timed(fn, warm):
-      """us per launch of fn(i) for i < steps, captured into one graph and replayed between two events."""
+      """us per launch of fn(i) for i < steps: the launches queued back to back on the runtime's stream, behind a
+      device-side hold long enough for the host to queue them all, between two events."""
       for i in range(3): fn(i)  # the first launches load the code object
       rt.wait()
-      def capture(n):
-        graph = c_void_p()
-        _lib.call("graph_begin", rt.handle)
-        for i in range(n): fn(i)
-        _lib.call("graph_end", rt.handle, byref(graph))
-        return graph
-      if warm:  # the untimed steps, in a graph of their own
-        wg = capture(min(warm, steps))
-        for _ in range(max(1, warm // min(warm, steps))): _lib.call("graph_launch", rt.handle, wg)
-        rt.wait()
-        _lib.call("graph_destroy", wg)
-      graph = capture(steps)
+      for i in range(warm): fn(i)  # the untimed steps
+      rt.wait()
       start, end = c_void_p(), c_void_p()
       _lib.call("event_create", rt.handle, byref(start))
       _lib.call("event_create", rt.handle, byref(end))
-      hold(rt)
+      hold(rt, steps)
       _lib.call("event_record", rt.handle, start)
-      _lib.call("graph_launch", rt.handle, graph)
+      for i in range(steps): fn(i)
       _lib.call("event_record", rt.handle, end)
       ms = c_float()
-      _lib.call("event_elapsed", start, end, byref(ms))
       rt.wait()
-      _lib.call("graph_destroy", graph)
+      _lib.call("event_elapsed", start, end, byref(ms))
       _lib.call("event_destroy", start)
       _lib.call("event_destroy", end)
       return ms.value * 1000 / steps
@@ -258,12 +250,16 @@ def decode_leg(tokens=128, prompt_len=32, check=True, replay=True):
 HOLD_S = 0.001  # the device-side wait queued before a timed replay's first event
 
 
-def hold(rt):
-  """Queues a kernel that keeps the device busy for HOLD_S, so that the host has queued the whole replay by the time
-  the device reaches the timed region's first event: the region then holds the replay's device time alone, not the
-  host's time to submit it (which a serving loop overlaps with earlier work)."""
+HOLD_PER_LAUNCH_S = 25e-6  # more than the host takes to queue one launch
+
+
+def hold(rt, launches=0):
+  """Queues a kernel that keeps the device busy for HOLD_S, or HOLD_PER_LAUNCH_S for each of `launches` launches if
+  longer, so that the host has queued the whole timed region by the time the device reaches its first event: the
+  region then holds the launches' device time alone, not the host's time to queue them (which a serving loop overlaps
+  with earlier work)."""
   from baretile_amd import _lib
-  _lib.call("sleep", rt.handle, HOLD_S)
+  _lib.call("sleep", rt.handle, max(HOLD_S, HOLD_PER_LAUNCH_S * launches))
 
 
 def graph_us(rt, fn, n):

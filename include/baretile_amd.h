@@ -252,6 +252,25 @@ int bt_rope_put(bt_runtime *rt, const bt_rope_args *args);
  * in rope->q and the key and value heads in the cache, bit for bit what the two calls write. */
 int bt_matmul_row_rope(bt_runtime *rt, const bt_row_args *args, const bt_rope_args *rope);
 
+/* The batched decode step's products with their neighbours (llama.py:106-160 with slots, llama.py:293-354): where
+ * fused_kernel would run RoPE and the residual add as a matmul's epilogue (kernels.py:41-727), here the product of 5 to
+ * 32 rows of A (bf16, contiguous 16-byte aligned rows) against a long K (a multiple of 256, over 768) is left as
+ * split-K partial sums in the runtime's scratch and the kernel that consumes it sums them, in split order as
+ * bt_matmul's reduction does, so the product and its reduction are neither stored nor launched on their own. Each is
+ * bit for bit the unfused calls. Inside a graph capture the runtime's scratch can't grow: make the call once before
+ * capturing. BT_EINVAL for a product outside those shapes.
+ *
+ * bt_matmul_rope_put: bt_matmul (bf16 product, no epilogue) then bt_rope_put on its product. rope->qkv and qkv_sr
+ * are not used; rope->rows is m, n is (heads + 2 kv) head_dim with head_dim a multiple of 16, and the tables, q and
+ * caches 16-byte aligned with strides a multiple of 8.
+ * bt_matmul_residual_rms: x = residual + a @ b (fp32, bt_matmul's residual epilogue; x may be the residual itself),
+ * then h = bt_rms_rows(x, norm, eps) (bf16); n <= 8192 and a multiple of 4. */
+int bt_matmul_rope_put(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_t b, int64_t m, int64_t k, int64_t n,
+                       const bt_rope_args *rope);
+int bt_matmul_residual_rms(bt_runtime *rt, const bt_operand *a, int b_fmt, uint64_t b, int64_t m, int64_t k, int64_t n,
+                           uint64_t residual, int64_t res_sr, uint64_t x, int64_t x_sr, uint64_t norm, float eps,
+                           uint64_t h, int64_t h_sr);
+
 
 /* ---- attention: replaces attention_kernel and its division/combine launches (kernels.py:794-1005,
  * tensor.py:797-841) -------------------------------------------------------------------------------------------

@@ -382,6 +382,52 @@ def test_matmul_row_rope_equals_two_calls(rt, fmt, k, hd, heads, kv):
   assert np.any(value(c1).reshape(2 * kv, size, hd)[:, place])
 
 
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bfp4"])
+@pytest.mark.parametrize("rows,k,hd,heads,kv", [(32, 4096, 128, 4, 2), (5, 1024, 64, 3, 1), (17, 2048, 128, 8, 4)])
+def test_matmul_rope_put_equals_two_calls(rt, fmt, rows, k, hd, heads, kv):
+  # a batched decode step's qkv product with RoPE and the puts into each slot's caches (bt_matmul_rope_put: the
+  # product's split-K partial sums summed in the RoPE kernel) writes, bit for bit, what bt_matmul to bf16 then
+  # bt_rope_put write: q, each slot's new key and value rows, and nothing else in the caches
+  from baretile_amd.models import llama
+  nh, size, place = heads + 2 * kv, 40, 37
+  c = llama.model(dim=heads * hd, heads=heads, kv=kv, layers=1, eps=1e-5, theta=10000.0, head_dim=hd)
+  cos, sin, _ = llama.rotary(c, size)
+  rng = np.random.default_rng(rows + k)
+  wt, _ = _weights(rt, k, nh * hd, fmt, k + nh)
+  h = Tensor.of(rt, B.bf16(rng.normal(0, 1, (rows, k)).astype(np.float32)))
+  cs, sn = Tensor.of(rt, np.repeat(cos[[place]], rows, 0)), Tensor.of(rt, np.repeat(sin[[place]], rows, 0))
+  pl = Tensor.of(rt, [[place]], "int32")
+  caches = [[Tensor.zeros(rt, size, hd, batch=rows * kv) for _ in range(2)] for _ in range(2)]
+  q1 = h.matmul_rope_put(wt, cs, sn, caches[0][0], pl, heads, kv, values=caches[0][1])
+  q2 = h.matmul(wt).rope_put(cs, sn, caches[1][0], pl, heads, kv, values=caches[1][1])
+  assert q1.tobytes() == q2.tobytes()
+  assert caches[0][0].tobytes() == caches[1][0].tobytes() and caches[0][1].tobytes() == caches[1][1].tobytes()
+  got = value(caches[0][0]).reshape(rows * kv, size, hd)
+  assert np.any(got[:, place]) and not np.any(np.delete(got, place, axis=1))
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bfp4"])
+@pytest.mark.parametrize("rows,k,n", [(32, 4096, 4096), (5, 1024, 576), (20, 14336, 1024)])
+def test_matmul_residual_rms_equals_unfused(rt, fmt, rows, k, n):
+  # a batched decode step's o product with the residual add and the MLP's RMSNorm (bt_matmul_residual_rms: the split-K
+  # partial sums summed in the norm's kernel) gives, bit for bit, x = residual + product (bt_matmul's residual
+  # epilogue) and rms_rows(x); and x within the reference's bound of the oracle's residual + a @ w
+  rng = np.random.default_rng(rows + n)
+  wt, wv = _weights(rt, k, n, fmt, k + n)
+  a = B.bf16(rng.normal(0, 1, (rows, k)).astype(np.float32))
+  res = rng.normal(0, 4, (rows, n)).astype(np.float32)
+  norm = Tensor.of(rt, B.bf16(rng.normal(1, 0.1, (1, n)).astype(np.float32)))
+  ta, tr = Tensor.of(rt, a), Tensor.of(rt, res[None], "fp32")
+  x1, h1 = ta.matmul_residual_rms(wt, tr, norm, 1e-5)
+  x2 = (tr + ta.matmul(wt, "fp32")).realize()
+  h2 = x2.rms_rows(norm, 1e-5)
+  assert x1.tobytes() == x2.tobytes() and h1.tobytes() == h2.tobytes()
+  got = np.frombuffer(x1.tobytes(), np.float32).reshape(rows, n)
+  want = res + a.astype(np.float64) @ wv
+  assert np.all(np.abs(got - want) <= 2.0 ** -8 * (np.abs(a) @ np.abs(wv)) + 1e-3 * np.abs(res) + 1e-6)
+  assert np.frombuffer(tr.tobytes(), np.float32).reshape(rows, n).tolist() == res.tolist()  # the residual kept
+
+
 @pytest.mark.parametrize("fmt", ["bfp8", "bfp4"])
 def test_block_float_cache(rt, fmt):
   # test_kernels.py:2106-2132: put writes bf16 rows into a block-float cache, each run of 16 rounded as cast rounds it,
