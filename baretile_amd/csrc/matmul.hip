@@ -441,6 +441,111 @@ __global__ void __launch_bounds__(SL ? 512 : 256) gemv_kernel(const MatmulArgs a
   }
 }
 
+// The plain decode GEMV of 1 to 4 rows of one matrix against block-float B with at most 12 chunks of K (the lm head's
+// 576 rows: 9), A-side scaled as gemv_kernel and summing in its order, with fewer and wider loads: the block's waves
+// stage the rows of A once in LDS (16-byte words), and a run's exponent bytes come 4 chunks to a dword load (lanes
+// 16c .. 16c + 15 the 64 bytes of chunk 4 t + c, the loads past the last chunk reading zeros through the buffer's
+// range). The lane whose dword holds exponent bytes 4q .. 4q + 3 (K-rows exp_row(4q) + 0 .. 3, consecutive) scales
+// those 4 rows of A for every row of the matrix and writes them to the chunk's slot, so each round of 4 chunks is a
+// wave barrier, then each chunk's fragments, B's decode and 2 matrix instructions as in gemv_kernel. Per wave 9 loads
+// of B's values and 3 of its exponents at K = 576, against gemv_kernel's 9 + 9 + 9 x ROWS: 4.67 against 5.1 us a
+// launch for the lm head in bfp4. G: chunks the kernel holds (4, 8, 9 or 12), at least the product's. Each buffer
+// resource is uniform across the wave (one made per lane would have the compiler loop over the lanes' resources), and
+// the rows of A are staged before B's loads are issued (other orders measured slower).
+struct XArgs {  // what the kernel reads of a MatmulArgs: 56 bytes instead of the kilobyte that carries a program
+  const uint8_t *b;
+  uint64_t a, out;
+  int64_t a_sr, out_sr;
+  int32_t m, k, n, chunks, nruns, out_bf16;
+};
+template <int FMT, int DT, int ROWS, int G>
+__global__ void __launch_bounds__(256) gemv_x_kernel(const XArgs h) {
+  constexpr int TB = Tile<FMT>::bytes, R = (G + 3) / 4, GC = 4 * R;  // rounds of 4 chunks, and their chunks
+  __shared__ __attribute__((aligned(16))) uint16_t slots_all[4 * GC * ROWS * 64];
+  __shared__ __attribute__((aligned(16))) uint16_t xs[ROWS * GC * 64];
+  const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
+  const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rows = min(ROWS, h.m);
+  uint16_t *slots = slots_all + wib * GC * ROWS * 64;
+#pragma unroll
+  for (int m = 0; m < ROWS; m++) {  // A's rows into LDS, zeros past K and past the last row
+    const __amdgpu_buffer_rsrc_t xr = buffer((const uint16_t *)(uintptr_t)h.a + (int64_t)min(m, rows - 1) * h.a_sr,
+                                             m < rows ? (uint32_t)h.k * 2 : 0u);
+    for (int u = threadIdx.x; u < GC * 8; u += 256) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(xr, 16 * u, 0, 0);
+      *(uint4 *)(xs + m * GC * 64 + 8 * u) = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+  }
+  uint32_t bq[G][4], ew[R];
+  const int run = blockIdx.x * 4 + wib;
+  const bool in = run < h.nruns;
+  const __amdgpu_buffer_rsrc_t tr = buffer(h.b + (int64_t)(in ? run : 0) * h.chunks * TB, in ? (uint32_t)h.chunks * TB : 0u);
+#pragma unroll
+  for (int i = 0; i < G; i++) {
+    if (FMT == BT_BFP8) {
+      const auto q = __builtin_amdgcn_raw_buffer_load_b128(tr, i * TB + 64 + 16 * lane, 0, STREAM);
+      bq[i][0] = q[0], bq[i][1] = q[1], bq[i][2] = q[2], bq[i][3] = q[3];
+    } else {
+      const auto q = __builtin_amdgcn_raw_buffer_load_b64(tr, i * TB + 64 + 8 * lane, 0, STREAM);
+      bq[i][0] = q[0], bq[i][1] = q[1];
+    }
+    if (i % 4 == 0) ew[i / 4] = __builtin_amdgcn_raw_buffer_load_b32(tr, (i + g) * TB + 4 * col, 0, STREAM);
+  }
+  __syncthreads();
+  const int r0 = exp_row(4 * col);  // the 4 consecutive K-rows of the lane's exponent dword
+  const int frag = (ROWS == 1 ? 0 : min(col, rows - 1) * 64) + 8 * g;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int rd = 0; rd < R; rd++) {
+    const int c = 4 * rd + g;  // the lane's chunk in the round
+    const uint32_t e = ew[rd];
+#pragma unroll
+    for (int m = 0; m < ROWS; m++) {
+      if (ROWS > 1 && m >= rows) break;
+      const uint2 xw = *(const uint2 *)(xs + m * GC * 64 + c * 64 + r0);
+      uint32_t sv[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t xb = (j < 2 ? xw.x : xw.y) >> (16 * (j & 1)) & 0xFFFFu;
+        sv[j] = __float_as_uint(ldexpf(__uint_as_float(xb << 16), (int)(int8_t)(e >> (8 * j))));
+      }
+      *(uint2 *)(slots + (c * ROWS + m) * 64 + r0) = make_uint2(__builtin_amdgcn_perm(sv[1], sv[0], 0x07060302u),
+                                                                 __builtin_amdgcn_perm(sv[3], sv[2], 0x07060302u));
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 4 * rd; i < 4 * rd + 4 && i < G; i++) {
+      bf16x8 av[2], bv[2];
+      av[0] = *(const bf16x8 *)(slots + i * ROWS * 64 + frag);
+      av[1] = *(const bf16x8 *)(slots + i * ROWS * 64 + frag + 32);
+      if (FMT == BT_BFP8) {
+        bv[0] = q8_to_bf16<false>(make_uint2(bq[i][0], bq[i][1]), make_uint2(0, 0));
+        bv[1] = q8_to_bf16<false>(make_uint2(bq[i][2], bq[i][3]), make_uint2(0, 0));
+      } else {
+        bv[0] = q4_to_bf16(bq[i][0]);
+        bv[1] = q4_to_bf16(bq[i][1]);
+      }
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0], bv[0], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[1], bv[1], acc, 0, 0, 0);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  // lanes of rows 4g + i < rows store them, one buffer store a value
+  const int n = run * 16 + col;
+  if (!in || n >= h.n) return;
+  const __amdgpu_buffer_rsrc_t orr =
+      buffer((const void *)(uintptr_t)h.out, (uint32_t)(((int64_t)(rows - 1) * h.out_sr + h.n) * (h.out_bf16 ? 2 : 4)));
+#pragma unroll
+  for (int i = 0; i < (ROWS == 1 ? 1 : 4); i++) {
+    const int mm = 4 * g + i;
+    if (mm >= rows) continue;
+    const uint32_t at = (uint32_t)(mm * (int)h.out_sr + n);
+    if (h.out_bf16) __builtin_amdgcn_raw_buffer_store_b16((uint16_t)bf16_packed(acc[i]), orr, at * 2, 0, 0);
+    else __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(DT == BT_BF16 ? round_packed(acc[i]) : acc[i]), orr,
+                                               at * 4, 0, 0);
+  }
+}
+
 // B-side scaling with row-major, 16-byte aligned A: each lane turns its 16 B values into bf16 q * 2^d with
 // v_ldexp_f32 and reads its A fragments straight from memory. A wave takes MT 16-row tiles of A against one run, so
 // each B value is loaded and converted once for MT tiles; the waves that share a run (more tiles than MT) are
@@ -2185,6 +2290,27 @@ static void launch_lds(const MatmulArgs &args, unsigned blocks, size_t lds, hipS
   else launch_lds_n<FMT, DT, 1, 1>(args, blocks, lds, s);
 }
 
+template <int FMT, int DT, int ROWS>
+static void launch_x_rows(const MatmulArgs &args, hipStream_t s) {
+  const unsigned blocks = (unsigned)((args.nruns + 3) / 4);
+  XArgs x;
+  x.b = args.b;
+  x.a = args.a.ptr, x.a_sr = args.a.sr, x.out = args.out.ptr, x.out_sr = args.out.sr;
+  x.m = args.m, x.k = args.k, x.n = args.n, x.chunks = args.chunks, x.nruns = args.nruns;
+  x.out_bf16 = args.out.dtype == BT_BF16;
+  if (args.chunks <= 4) gemv_x_kernel<FMT, DT, ROWS, 4><<<blocks, 256, 0, s>>>(x);
+  else if (args.chunks <= 8) gemv_x_kernel<FMT, DT, ROWS, 8><<<blocks, 256, 0, s>>>(x);
+  else if (args.chunks <= 9) gemv_x_kernel<FMT, DT, ROWS, 9><<<blocks, 256, 0, s>>>(x);
+  else gemv_x_kernel<FMT, DT, ROWS, 12><<<blocks, 256, 0, s>>>(x);
+}
+template <int FMT, int DT>
+static void launch_x(const MatmulArgs &args, hipStream_t s) {
+  if constexpr (FMT != BT_BF16) {
+    if (args.m == 1) launch_x_rows<FMT, DT, 1>(args, s);
+    else launch_x_rows<FMT, DT, 4>(args, s);
+  }
+}
+
 template <int FMT, int DT>
 static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bool vec) {
   const bool rows_contiguous = args.a.sc == 1 && (int64_t)args.k * 2 < (1ll << 31);
@@ -2198,6 +2324,10 @@ static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bo
     // an epilogue program, slices): one kernel with all of them, groups of 8
     // (and a plain output)
     const bool lean = args.batch == 1 && !args.n_inst && sl == 1 && plain_out(args);
+    if (FMT != BT_BF16 && lean && args.chunks <= 12 && args.k % 8 == 0 && args.a.ptr % 16 == 0 && args.a.sr % 8 == 0) {
+      launch_x<FMT, DT>(args, s);
+      return;
+    }
     if (args.m == 1) {
       constexpr int SB = 64 * 2;  // slot bytes a chunk
       if (!lean && sl > 1) {
