@@ -563,8 +563,10 @@ __global__ void __launch_bounds__(256) gemv_x_kernel(const XArgs h) {
 // rows (their A and exponent loads keep the texture units busy while HBM idles). Exponents as in skinny2_kernel.
 template <int FMT, int DT, int MT, int NRW, int G, bool PROG>
 __global__ void __launch_bounds__(256) skinny_lds_kernel(const MatmulArgs args) {
-  constexpr int TB = Tile<FMT>::bytes;
+  constexpr int TB = Tile<FMT>::bytes, R = (G + 3) / 4;  // R: rounds of 4 chunks (bfp4)
   extern __shared__ __attribute__((aligned(16))) uint16_t la[];  // A: 16 MT rows, kp halfwords apart
+  // bfp4: each chunk's exponents as gaps placed in the bf16 exponent field (place_gaps), 128 bytes a chunk a run
+  __shared__ __attribute__((aligned(16))) uint8_t gaps_all[FMT == BT_BFP4 ? 4 * NRW * 4 * R * 128 : 16];
   const Head h = early_head(args);
   const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
   const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -572,19 +574,22 @@ __global__ void __launch_bounds__(256) skinny_lds_kernel(const MatmulArgs args) 
   const int run0 = ((int)blockIdx.x * 4 + wib) * NRW;
   // 1. A's pieces for this thread (16 bytes each; rows past the last and columns past K are zeros), loaded before
   // the weights so that staging them waits for these alone
-  const uint16_t *abase = (const uint16_t *)h.a.ptr;
+  // (buffer loads: the wait for them then counts them alone, where a flat load's wait would be for every load issued)
   const int pieces = chunks * 8, kw = h.k / 8, total = 16 * MT * pieces;
   constexpr int AP = (16 * MT * 96 + 255) / 256;  // at most 12 chunks: 96 pieces a row
+  const __amdgpu_buffer_rsrc_t ar = buffer((const void *)(uintptr_t)h.a.ptr,
+                                           (uint32_t)(((int64_t)(h.m - 1) * h.a.sr + h.k) * 2));
   uint4 av[AP];
 #pragma unroll
   for (int j = 0; j < AP; j++) {
     const int q = (int)threadIdx.x + 256 * j, row = q / pieces, c8 = q % pieces;
-    av[j] = make_uint4(0, 0, 0, 0);
-    if (q < total && row < h.m && c8 < kw) av[j] = *(const uint4 *)(abase + (int64_t)row * h.a.sr + c8 * 8);
+    const uint32_t off = q < total && row < h.m && c8 < kw ? (uint32_t)(row * (int)h.a.sr + c8 * 8) * 2 : 0x80000000u;
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(ar, off, 0, 0);
+    av[j] = make_uint4(v[0], v[1], v[2], v[3]);
   }
   // 2. the wave's weights, in flight while A is staged and while earlier runs are multiplied
   uint4 bq[NRW][G];
-  uint32_t ew[NRW][G];
+  uint32_t ew[NRW][FMT == BT_BFP4 ? R : G];  // bfp8: dword col of each chunk's exponents; bfp4: of chunk 4 t + g
 #pragma unroll
   for (int r = 0; r < NRW; r++) {
     const bool in = run0 + r < h.nruns;
@@ -599,7 +604,8 @@ __global__ void __launch_bounds__(256) skinny_lds_kernel(const MatmulArgs args) 
         const auto q = __builtin_amdgcn_raw_buffer_load_b64(tr, at + 64 + 8 * lane, 0, 0);
         bq[r][i] = make_uint4(q[0], q[1], 0, 0);
       }
-      ew[r][i] = __builtin_amdgcn_raw_buffer_load_b32(tr, at + 4 * col, 0, 0);
+      if (FMT == BT_BFP8) ew[r][i] = __builtin_amdgcn_raw_buffer_load_b32(tr, at + 4 * col, 0, 0);
+      else if (i % 4 == 0) ew[r][i / 4] = __builtin_amdgcn_raw_buffer_load_b32(tr, (i + g) * TB + 4 * col, 0, 0);
     }
   }
   // 3. A into LDS
@@ -615,19 +621,26 @@ __global__ void __launch_bounds__(256) skinny_lds_kernel(const MatmulArgs args) 
     f32x4 acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; t++) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    uint8_t *gp = gaps_all + (wib * NRW + r) * 4 * R * 128;
 #pragma unroll
     for (int i = 0; i < G; i++) {
       if (i >= chunks) continue;
-      uint32_t ex[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) ex[k] = (uint32_t)__shfl((int)ew[r][i], 4 * g + k, 64);
       bf16x8 bv[2];
       if (FMT == BT_BFP8) {
+        uint32_t ex[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) ex[k] = (uint32_t)__shfl((int)ew[r][i], 4 * g + k, 64);
         bv[0] = q8_to_bf16<true>(make_uint2(bq[r][i].x, bq[r][i].y), make_uint2(ex[0], ex[1]));
         bv[1] = q8_to_bf16<true>(make_uint2(bq[r][i].z, bq[r][i].w), make_uint2(ex[2], ex[3]));
       } else {
-        bv[0] = q4_to_bf16_scaled(bq[r][i].x, make_uint2(ex[0], ex[1]));
-        bv[1] = q4_to_bf16_scaled(bq[r][i].y, make_uint2(ex[2], ex[3]));
+        if (i % 4 == 0) {  // the round's 4 chunks: lane (g, col) places dword col of chunk i + g, once for the wave
+          *(uint2 *)(gp + (i + g) * 128 + 8 * col) = place_gaps(ew[r][i / 4]);
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        bv[0] = q4_to_bf16_placed(bq[r][i].x, *(const uint4 *)(gp + i * 128 + 32 * g));
+        bv[1] = q4_to_bf16_placed(bq[r][i].y, *(const uint4 *)(gp + i * 128 + 32 * g + 16));
       }
 #pragma unroll
       for (int t = 0; t < MT; t++) {
