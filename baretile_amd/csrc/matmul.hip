@@ -446,12 +446,16 @@ __global__ void __launch_bounds__(SL ? 512 : 256) gemv_kernel(const MatmulArgs a
 // stage the rows of A once in LDS (16-byte words), and a run's exponent bytes come 4 chunks to a dword load (lanes
 // 16c .. 16c + 15 the 64 bytes of chunk 4 t + c, the loads past the last chunk reading zeros through the buffer's
 // range). The lane whose dword holds exponent bytes 4q .. 4q + 3 (K-rows exp_row(4q) + 0 .. 3, consecutive) scales
-// those 4 rows of A for every row of the matrix and writes them to the chunk's slot, so each round of 4 chunks is a
-// wave barrier, then each chunk's fragments, B's decode and 2 matrix instructions as in gemv_kernel. Per wave 9 loads
-// of B's values and 3 of its exponents at K = 576, against gemv_kernel's 9 + 9 + 9 x ROWS: 4.67 against 5.1 us a
-// launch for the lm head in bfp4. G: chunks the kernel holds (4, 8, 9 or 12), at least the product's. Each buffer
-// resource is uniform across the wave (one made per lane would have the compiler loop over the lanes' resources), and
-// the rows of A are staged before B's loads are issued (other orders measured slower).
+// those 4 rows of A for every row of the matrix and writes them to the chunk's slot; then each chunk's fragments, B's
+// decode and 2 matrix instructions as in gemv_kernel. Per wave 9 loads of B's values and 3 of its exponents at
+// K = 576, against gemv_kernel's 9 + 9 + 9 x ROWS. The order of the loads is the order the data is needed: A's rows
+// (into registers), the exponent dwords, B's values; then A goes to LDS and is scaled for all rounds while the values
+// are still in flight, so after the last value arrives only its decode and products remain (scheduling barriers keep
+// the compiler from sinking the exponent loads among the value loads, or the reads of A behind the writes of slots).
+// For the lm head in bfp4: 4.62 us a launch at 1 row and 5.44 at 4, against 4.81 and 6.00 with A staged before B's
+// loads were issued and each round scaled after its values. G: chunks the kernel holds (4, 8, 9 or 12), at least the
+// product's. Each buffer resource is uniform across the wave (one made per lane would have the compiler loop over the
+// lanes' resources).
 struct XArgs {  // what the kernel reads of a MatmulArgs: 56 bytes instead of the kilobyte that carries a program
   const uint8_t *b;
   uint64_t a, out;
@@ -467,19 +471,24 @@ __global__ void __launch_bounds__(256) gemv_x_kernel(const XArgs h) {
   const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rows = min(ROWS, h.m);
   uint16_t *slots = slots_all + wib * GC * ROWS * 64;
+  static_assert(GC * 8 <= 256, "a thread stages at most one 16-byte piece of each row of A");
+  uint4 xv[ROWS];
 #pragma unroll
-  for (int m = 0; m < ROWS; m++) {  // A's rows into LDS, zeros past K and past the last row
+  for (int m = 0; m < ROWS; m++) {  // A's rows, zeros past K and past the last row
     const __amdgpu_buffer_rsrc_t xr = buffer((const uint16_t *)(uintptr_t)h.a + (int64_t)min(m, rows - 1) * h.a_sr,
                                              m < rows ? (uint32_t)h.k * 2 : 0u);
-    for (int u = threadIdx.x; u < GC * 8; u += 256) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(xr, 16 * u, 0, 0);
-      *(uint4 *)(xs + m * GC * 64 + 8 * u) = make_uint4(v[0], v[1], v[2], v[3]);
-    }
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(xr, 16 * threadIdx.x, 0, 0);
+    xv[m] = make_uint4(v[0], v[1], v[2], v[3]);
   }
+  __builtin_amdgcn_sched_barrier(0);
   uint32_t bq[G][4], ew[R];
   const int run = blockIdx.x * 4 + wib;
   const bool in = run < h.nruns;
   const __amdgpu_buffer_rsrc_t tr = buffer(h.b + (int64_t)(in ? run : 0) * h.chunks * TB, in ? (uint32_t)h.chunks * TB : 0u);
+#pragma unroll
+  for (int rd = 0; rd < R; rd++)  // exponents first: A is scaled while the values are in flight
+    ew[rd] = __builtin_amdgcn_raw_buffer_load_b32(tr, (4 * rd + g) * TB + 4 * col, 0, STREAM);
+  __builtin_amdgcn_sched_barrier(0);  // (the scheduler would otherwise sink them among the value loads)
 #pragma unroll
   for (int i = 0; i < G; i++) {
     if (FMT == BT_BFP8) {
@@ -489,12 +498,21 @@ __global__ void __launch_bounds__(256) gemv_x_kernel(const XArgs h) {
       const auto q = __builtin_amdgcn_raw_buffer_load_b64(tr, i * TB + 64 + 8 * lane, 0, STREAM);
       bq[i][0] = q[0], bq[i][1] = q[1];
     }
-    if (i % 4 == 0) ew[i / 4] = __builtin_amdgcn_raw_buffer_load_b32(tr, (i + g) * TB + 4 * col, 0, STREAM);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  if (threadIdx.x < GC * 8)
+#pragma unroll
+    for (int m = 0; m < ROWS; m++) *(uint4 *)(xs + m * GC * 64 + 8 * threadIdx.x) = xv[m];
   __syncthreads();
   const int r0 = exp_row(4 * col);  // the 4 consecutive K-rows of the lane's exponent dword
   const int frag = (ROWS == 1 ? 0 : min(col, rows - 1) * 64) + 8 * g;
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  uint2 xw[R][ROWS];  // every piece of A the lane scales, read before the first is used
+#pragma unroll
+  for (int rd = 0; rd < R; rd++)
+#pragma unroll
+    for (int m = 0; m < ROWS; m++) xw[rd][m] = *(const uint2 *)(xs + m * GC * 64 + (4 * rd + g) * 64 + r0);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int rd = 0; rd < R; rd++) {
     const int c = 4 * rd + g;  // the lane's chunk in the round
@@ -502,33 +520,32 @@ __global__ void __launch_bounds__(256) gemv_x_kernel(const XArgs h) {
 #pragma unroll
     for (int m = 0; m < ROWS; m++) {
       if (ROWS > 1 && m >= rows) break;
-      const uint2 xw = *(const uint2 *)(xs + m * GC * 64 + c * 64 + r0);
       uint32_t sv[4];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const uint32_t xb = (j < 2 ? xw.x : xw.y) >> (16 * (j & 1)) & 0xFFFFu;
+        const uint32_t xb = (j < 2 ? xw[rd][m].x : xw[rd][m].y) >> (16 * (j & 1)) & 0xFFFFu;
         sv[j] = __float_as_uint(ldexpf(__uint_as_float(xb << 16), (int)(int8_t)(e >> (8 * j))));
       }
       *(uint2 *)(slots + (c * ROWS + m) * 64 + r0) = make_uint2(__builtin_amdgcn_perm(sv[1], sv[0], 0x07060302u),
                                                                  __builtin_amdgcn_perm(sv[3], sv[2], 0x07060302u));
     }
-    __builtin_amdgcn_wave_barrier();
+  }
+  __builtin_amdgcn_sched_barrier(0);  // all of A scaled before the first product waits for its values
+  __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int i = 4 * rd; i < 4 * rd + 4 && i < G; i++) {
-      bf16x8 av[2], bv[2];
-      av[0] = *(const bf16x8 *)(slots + i * ROWS * 64 + frag);
-      av[1] = *(const bf16x8 *)(slots + i * ROWS * 64 + frag + 32);
-      if (FMT == BT_BFP8) {
-        bv[0] = q8_to_bf16<false>(make_uint2(bq[i][0], bq[i][1]), make_uint2(0, 0));
-        bv[1] = q8_to_bf16<false>(make_uint2(bq[i][2], bq[i][3]), make_uint2(0, 0));
-      } else {
-        bv[0] = q4_to_bf16(bq[i][0]);
-        bv[1] = q4_to_bf16(bq[i][1]);
-      }
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0], bv[0], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[1], bv[1], acc, 0, 0, 0);
+  for (int i = 0; i < G; i++) {
+    bf16x8 av[2], bv[2];
+    av[0] = *(const bf16x8 *)(slots + i * ROWS * 64 + frag);
+    av[1] = *(const bf16x8 *)(slots + i * ROWS * 64 + frag + 32);
+    if (FMT == BT_BFP8) {
+      bv[0] = q8_to_bf16<false>(make_uint2(bq[i][0], bq[i][1]), make_uint2(0, 0));
+      bv[1] = q8_to_bf16<false>(make_uint2(bq[i][2], bq[i][3]), make_uint2(0, 0));
+    } else {
+      bv[0] = q4_to_bf16(bq[i][0]);
+      bv[1] = q4_to_bf16(bq[i][1]);
     }
-    __builtin_amdgcn_wave_barrier();
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0], bv[0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[1], bv[1], acc, 0, 0, 0);
   }
   // lanes of rows 4g + i < rows store them, one buffer store a value
   const int n = run * 16 + col;
