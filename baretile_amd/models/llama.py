@@ -335,27 +335,37 @@ def row_layer(x, p, c, rot, places, cache, rows):
   return gate_up.matmul_row(p["down_proj"], "fp32", swiglu=True, residual=x)
 
 
-def slots_layer(x, p, c, rot, keys, values, place):
+def slots_layer(x, p, c, rot, keys, values, place, h=None, then=None):
   """One block for a batch of slots, each with its own cache and one new token, all at one place: the batched decode
   of llama.forward(slots=...) (llama.py:293-354). x is (1, S, dim), the stream of the S slots; keys and values are
   (S * kv, size, head) bf16, slot s's key heads at s * kv .. s * kv + kv - 1; rot holds the tables at the place for
   each slot's row; place is a (1, 1) int32 row. The slots' query heads become S * heads attention heads of one row.
   RoPE and the cache puts run as one kernel (bt_rope_put), in fp32 with one rounding. The qkv product feeds that kernel
   its split-K partial sums, and the o product feeds the residual add and the MLP's norm likewise (matmul_rope_put,
-  matmul_residual_rms), with the same results as the separate steps."""
+  matmul_residual_rms), with the same results as the separate steps.
+
+  h: x's input norm when it is already made (by the block before, with `then`). then: the norm weights that the next
+  step applies to the new x (the next block's input norm, or the model's final norm); with them the down product
+  feeds the residual add and that norm as the o product does, and (x, the next step's h) comes back."""
   S, hd, rep = x.rows, head(c), c.heads // c.kv
   if keys.dtype != "bf16": raise ValueError("slots_layer takes bf16 caches")
-  h = rms(x, p["input_layernorm"], c)
+  if h is None: h = rms(x, p["input_layernorm"], c)
   q = h.matmul_rope_put(p["qkv_proj"], rot[0], rot[1], keys, place, c.heads, c.kv, values=values)
   o = q.reshape(S * c.heads, 1, hd).attend(keys.repeat_interleave(rep), values.repeat_interleave(rep),
                                            place.reshape(1, 1, 1)).reshape(1, S, c.heads * hd)
   norm = p["post_attention_layernorm"]
-  if x.dtype == "fp32" and x.batch == 1 and norm.dtype == "bf16":
+  fused = x.dtype == "fp32" and x.batch == 1
+  if fused and norm.dtype == "bf16":
     x, h = o.matmul_residual_rms(p["o_proj"], x, norm, c.eps)
   else:
     x = (x + o.matmul(p["o_proj"], "fp32")).realize()
     h = rms(x, norm, c)
-  return (x + mlp(h, p)).realize()
+  if then is None: return (x + mlp(h, p)).realize()
+  m = p["down_proj"].rows
+  if fused and then.dtype == "bf16" and h.batch == 1 and m % 16 == 0 and h.cols % 32 == 0:
+    return h.matmul_swiglu(p["gate_up_proj"]).matmul_residual_rms(p["down_proj"], x, then, c.eps)
+  x = (x + mlp(h, p)).realize()
+  return x, rms(x, then, c)
 
 
 def starts(w, n, slots, part):

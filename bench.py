@@ -530,7 +530,10 @@ def _layer_decode(rt, llama, L, B, Tensor, c, rc, p, w, ref, wbytes, cos, sin, t
   at = Tensor.of(rt, [[size - 1] * slots], "int32")
   rot = (w["cos"].gather(at), w["sin"].gather(at), w["turn"])
   place = Tensor.of(rt, [[size - 1]], "int32")
-  step = lambda: llama.slots_layer(xs, p, c, rot, keys, values, place).realize()
+  # a block of a stack: its input norm made by the block before (h), its down product ending in the norm of the block
+  # after (then; this one block stands for it), so that a step holds the block's two norms, as each block of a model
+  hs = llama.rms(xs, p["input_layernorm"], c).realize()
+  step = lambda: llama.slots_layer(xs, p, c, rot, keys, values, place, h=hs, then=p["input_layernorm"])[0].realize()
   step()
   rt.wait()
   reps, t0 = 20, time.perf_counter()

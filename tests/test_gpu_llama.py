@@ -165,6 +165,48 @@ def test_slots_layer_matches_each_slot_in_numpy(rt):
       assert np.abs(got_r - want_r).max() <= 0.03 * np.abs(want_r).max(), (s, np.abs(got_r - want_r).max())
 
 
+def test_slots_layer_then_fuses_the_next_norm(rt):
+  # slots_layer(h=, then=): the block's input norm given, and the down product's partial sums, the residual add and
+  # the next norm in one kernel (bt_matmul_residual_rms) -- bit for bit the block's x and rms_rows of it, in two
+  # launches fewer than the block with both norms run on their own. 8 slots and K = ffn = 1024 (16 chunks), the
+  # shapes the streaming product takes
+  rng = np.random.default_rng(17)
+  S, size, place, dim, heads, kv, hd, ffn = 8, 64, 21, 256, 4, 2, 64, 1024
+  bf = lambda a: B.bf16(np.asarray(a, np.float32))
+  w = {"layers.0.input_layernorm": bf(rng.normal(1, 0.1, (1, dim))),
+       "layers.0.post_attention_layernorm": bf(rng.normal(1, 0.1, (1, dim))),
+       "layers.0.qkv_proj": bf(rng.normal(0, 0.02, (dim, (heads + 2 * kv) * hd))),
+       "layers.0.o_proj": bf(rng.normal(0, 0.02, (heads * hd, dim))),
+       "layers.0.gate_up_proj": bf(rng.normal(0, 0.02, (dim, 2 * ffn))),
+       "layers.0.down_proj": bf(rng.normal(0, 0.02, (ffn, dim))),
+       "norm": bf(rng.normal(1, 0.1, (1, dim))), "embed": bf(rng.normal(0, 1, (64, dim)))}
+  dc = llama.model(dim=dim, heads=heads, kv=kv, layers=1, eps=1e-5, theta=10000.0, ffn=ffn, head_dim=hd,
+                   precision=llama.precision(llama.model(layers=1, dim=dim), "bfp4"))
+  dw = llama.upload(rt, w, dc, places=size)
+  p = llama.block(dw, 0)
+  K, V = (bf(rng.normal(0, 1, (S * kv, size, hd))) for _ in range(2))
+  keys, values = Tensor.of(rt, K), Tensor.of(rt, V)
+  rows = Tensor.of(rt, [[place] * S], "int32")
+  rot = (dw["cos"].gather(rows), dw["sin"].gather(rows), dw["turn"])
+  at = Tensor.of(rt, [[place]], "int32")
+  x = Tensor.of(rt, rng.normal(0, 1, (1, S, dim)).astype(np.float32), "fp32")
+  then = dw["norm"]
+  n0 = rt.launches
+  h0 = llama.rms(x, p["input_layernorm"], dc)
+  x1 = llama.slots_layer(x, p, dc, rot, keys, values, at, h=h0)
+  h1 = llama.rms(x1, then, dc)
+  want_x, want_h = x1.tobytes(), h1.tobytes()
+  n1 = rt.launches
+  x2, h2 = llama.slots_layer(x, p, dc, rot, keys, values, at, h=h0, then=then)
+  got_x, got_h = x2.tobytes(), h2.tobytes()
+  n2 = rt.launches
+  assert got_x == want_x and got_h == want_h
+  assert n2 - n1 == (n1 - n0) - 2, (n1 - n0, n2 - n1)
+  # without h the block makes its input norm itself, the same one
+  x3, h3 = llama.slots_layer(x, p, dc, rot, keys, values, at, then=then)
+  assert x3.tobytes() == want_x and h3.tobytes() == want_h
+
+
 @pytest.mark.parametrize("kv", ["bfp8", "bfp4"])
 def test_block_float_kv_cache_matches_numpy(rt, kv):
   # the KV cache in bfp8 or bfp4 (precision's kv entry, tt_transformers' cache format, llama.py:74-83): a prompt's
