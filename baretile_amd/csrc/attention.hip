@@ -31,6 +31,10 @@ typedef short bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int KB = 64;  // keys per block
+// Cache policy of the decode kernels' K and V loads: sc1 | nt, streamed (each byte is read once a step, and a
+// cache-allocating read of hundreds of MB only evicts): 537 MB of bf16 K and V in 84 us against 97 with the default
+// policy. Prefill keeps the default: its blocks read each key block once per query tile.
+constexpr int DEC_POL = 18;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t attn_rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
@@ -94,13 +98,13 @@ __device__ __forceinline__ uint4 kv_decode8(uint32_t lo, uint32_t hi, uint32_t x
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 // The value bytes of 8 values from value e on (e a multiple of 8): bfp8 two words, bfp4 one.
-template <int KF>
+template <int KF, int POL = 0>
 __device__ __forceinline__ uint2 kv_raw8(const KvSrc &s, uint32_t e) {
   if (KF == BT_BFP8) {
-    const auto q = __builtin_amdgcn_raw_buffer_load_b64(s.val, e, 0, 0);
+    const auto q = __builtin_amdgcn_raw_buffer_load_b64(s.val, e, 0, POL);
     return make_uint2(q[0], q[1]);
   }
-  return make_uint2(__builtin_amdgcn_raw_buffer_load_b32(s.val, e / 2, 0, 0), 0u);
+  return make_uint2(__builtin_amdgcn_raw_buffer_load_b32(s.val, e / 2, 0, POL), 0u);
 }
 // 8 values from value e on (e a multiple of 8), as bf16 pairs; a block float's exponent byte read at e / 16.
 template <int KF>
@@ -114,11 +118,11 @@ __device__ __forceinline__ uint4 kv_load8(const KvSrc &s, uint32_t e) {
   return kv_decode8<KF>(q.x, q.y, x);
 }
 // A row's HD / 16 exponent bytes (row start e, a multiple of 16), for decoding its pieces one by one.
-template <int KF, int HD>
+template <int KF, int HD, int POL = 0>
 __device__ __forceinline__ uint2 kv_row_exps(const KvSrc &s, uint32_t e) {
   if (KF == BT_BF16) return make_uint2(0, 0);
-  if (HD == 64) return make_uint2(__builtin_amdgcn_raw_buffer_load_b32(s.exp, e / 16, 0, 0), 0u);
-  const auto v = __builtin_amdgcn_raw_buffer_load_b64(s.exp, e / 16, 0, 0);
+  if (HD == 64) return make_uint2(__builtin_amdgcn_raw_buffer_load_b32(s.exp, e / 16, 0, POL), 0u);
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(s.exp, e / 16, 0, POL);
   return make_uint2(v[0], v[1]);
 }
 
@@ -126,15 +130,15 @@ __device__ __forceinline__ uint2 kv_row_exps(const KvSrc &s, uint32_t e) {
 template <int KF> struct Raw8 {
   uint32_t w[KF == BT_BF16 ? 4 : KF == BT_BFP8 ? 2 : 1];
 };
-template <int KF>
+template <int KF, int POL = 0>
 __device__ __forceinline__ Raw8<KF> kv_fetch8(const KvSrc &s, uint32_t e) {
   Raw8<KF> r;
   if constexpr (KF == BT_BF16) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(s.val, e * 2, 0, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(s.val, e * 2, 0, POL);
 #pragma unroll
     for (int i = 0; i < 4; i++) r.w[i] = v[i];
   } else {
-    const uint2 q = kv_raw8<KF>(s, e);
+    const uint2 q = kv_raw8<KF, POL>(s, e);
     r.w[0] = q.x;
     if constexpr (KF == BT_BFP8) r.w[1] = q.y;
   }
@@ -147,10 +151,10 @@ __device__ __forceinline__ uint4 kv_value8(const Raw8<KF> &r, uint32_t x) {
   else return kv_decode8<KF>(r.w[0], 0u, x);
 }
 // A block-float value's exponent byte (value e); 0 for bf16, which has none.
-template <int KF>
+template <int KF, int POL = 0>
 __device__ __forceinline__ uint32_t kv_exp8(const KvSrc &s, uint32_t e) {
   if constexpr (KF == BT_BF16) return 0u;
-  else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(s.exp, e / 16, 0, 0);
+  else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(s.exp, e / 16, 0, POL);
 }
 
 // A lane's pair: which query row it is, which keys it sees, where its q and output rows are.
@@ -347,14 +351,14 @@ __device__ __forceinline__ void fetch_keys(KeyBytes<HD, KF, WIDE> &kb_, const Kv
   for (int kt = 0; kt < 4; kt++) {
     const uint32_t row = (uint32_t)((int64_t)(kb + 16 * kt + n) * k_sr);
     if constexpr (KF != BT_BF16 && WIDE) {
-      const uint2 xs = kv_row_exps<KF, HD>(kr, row);
+      const uint2 xs = kv_row_exps<KF, HD, DEC_POL>(kr, row);
       kb_.x[kt][0] = xs.x;
       if constexpr (HD != 64) kb_.x[kt][1] = xs.y;
     }
 #pragma unroll
     for (int kk = 0; kk < HD / 32; kk++) {
-      kb_.q[kt][kk] = kv_fetch8<KF>(kr, row + 32 * kk + 8 * g);
-      if constexpr (KF != BT_BF16 && !WIDE) kb_.x[kt][kk] = kv_exp8<KF>(kr, row + 32 * kk + 8 * g);
+      kb_.q[kt][kk] = kv_fetch8<KF, DEC_POL>(kr, row + 32 * kk + 8 * g);
+      if constexpr (KF != BT_BF16 && !WIDE) kb_.x[kt][kk] = kv_exp8<KF, DEC_POL>(kr, row + 32 * kk + 8 * g);
     }
   }
 }
@@ -412,8 +416,8 @@ attention_decode_kernel(const bt_attention_args a, int tiles, int parts, float *
 #pragma unroll
     for (int i = 0; i < VI; i++) {
       const uint32_t e = (uint32_t)((int64_t)(kb + vrow + RPI * i) * a.v_sr + vcol);
-      vq[i] = kv_fetch8<KF>(vr, e);
-      vx[i] = kv_exp8<KF>(vr, e);
+      vq[i] = kv_fetch8<KF, DEC_POL>(vr, e);
+      vx[i] = kv_exp8<KF, DEC_POL>(vr, e);
     }
   };
   int kb = first + KB * wib;
