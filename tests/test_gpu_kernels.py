@@ -452,9 +452,12 @@ def attend(rt, q, k, v, places, window=0, parts=0):
 # (heads, rows, head width, keys, heads per key head, window, parts): decode tiles (rep * rows <= 16) in one part and
 # split into parts, prefill tiles, windows, and BASELINE config 4's decode shape; in one part, 256 keys give each of
 # a decode block's 4 waves one 64-key block (only its last step) and 320 give the first wave two (a step that fetches
-# the next block, then the last)
+# the next block, then the last); 5 to 8 key blocks with the parts left to the library split into parts of two
+# blocks and their combine (320, 384, 450, 500 and 512 keys: an odd block, two tiles, a window, one query head a key
+# head)
 ATTENTION_CASES = [(4, 8, 64, 96, 2, 0, 0), (2, 40, 128, 200, 1, 50, 0), (8, 1, 128, 512, 4, 0, 0),
-                   (8, 1, 64, 256, 4, 0, 1), (8, 1, 128, 320, 4, 0, 1),
+                   (8, 1, 64, 256, 4, 0, 1), (8, 1, 128, 320, 4, 0, 1), (8, 1, 64, 320, 4, 0, 0),
+                   (16, 3, 64, 384, 8, 0, 0), (8, 2, 128, 450, 4, 60, 0), (4, 1, 128, 500, 1, 0, 0),
                    (32, 1, 128, 4096, 4, 0, 0), (9, 32, 64, 160, 3, 0, 0), (9, 1, 64, 160, 3, 0, 0),
                    (8, 1, 128, 1000, 4, 0, 7), (8, 2, 64, 700, 4, 100, 0), (8, 256, 128, 300, 4, 0, 0),
                    (6, 130, 64, 130, 3, 17, 0), (32, 1, 128, 16384, 4, 0, 0), (16, 600, 128, 600, 4, 0, 0),

@@ -466,6 +466,22 @@ def test_block_float_cache_long_decode(rt):
   assert got.tobytes() == want.tobytes()
 
 
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4"])
+def test_block_float_cache_split_decode(rt, fmt):
+  # 480 cached rows (8 blocks of 64 keys: parts of two blocks, then their combine), 128-wide heads, two query rows:
+  # the cache read in place gives bit for bit what its values give in bf16
+  rng = np.random.default_rng(22)
+  x = B.bf16(rng.normal(0, 1, (4, 480, 128)))
+  cache = Tensor.of(rt, np.zeros((4, 480, 128), np.float32)).cast(fmt).realize()
+  cache.put(Tensor.of(rt, [list(range(480))], "int32"), Tensor.of(rt, x.astype(np.float32)))
+  same = Tensor.of(rt, value(cache).reshape(4, 480, 128).astype(np.float32))
+  q = Tensor.of(rt, B.bf16(rng.normal(0, 1, (8, 2, 128)) / 11).astype(np.float32))
+  pl = Tensor.of(rt, [[[470], [479]]], "int32")
+  got = q.attend(cache[0:2, :, :].repeat_interleave(4), cache[2:4, :, :].repeat_interleave(4), pl)
+  want = q.attend(same[0:2, :, :].repeat_interleave(4), same[2:4, :, :].repeat_interleave(4), pl)
+  assert got.tobytes() == want.tobytes()
+
+
 def test_rope_put_slots(rt):
   # the slots' layout: separate key and value caches of rows * kv heads, row i's heads at i * kv, one place for all
   # rows (llama.slots_layer); against the same float64 RoPE, and nothing else written
