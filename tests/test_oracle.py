@@ -5,6 +5,8 @@ transposed operand) fails it: known answers from the reference's own tests, clos
 (exact rationals, float arithmetic instead of bit manipulation), and independent libraries (torch, transformers).
 """
 from fractions import Fraction
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -106,6 +108,17 @@ def test_decode_bits_against_float_arithmetic():
   b4 = B.decode_bits(np.full(16, 130), n, "bfp4")
   assert np.array_equal(B.bf16_floats(b4)[1:8], (np.arange(1, 8) * 2.0).astype(np.float32))
   assert np.array_equal(B.bf16_floats(b4)[9:16], (-np.arange(1, 8) * 2.0).astype(np.float32))
+
+
+def test_decode_bits_against_the_reference_unpacker():
+  # the whole domain, edge rules included (a zero magnitude with its sign set reads -inf, exponents wrap mod 256),
+  # against the reference unpacker's own output (tests/golden/make_unpacker_vectors.py ran tensor.py's `_bf16s`):
+  # every bfp8 byte and every bfp4 nibble at every exponent byte
+  g = np.load(os.path.join(os.path.dirname(__file__), "golden", "unpacker_bf16s.npz"))
+  e, x = np.meshgrid(np.arange(256), np.arange(256), indexing="ij")
+  assert np.array_equal(B.decode_bits(e, x, "bfp8"), g["bits8"])
+  e, n = np.meshgrid(np.arange(256), np.arange(16), indexing="ij")
+  assert np.array_equal(B.decode_bits(e, n, "bfp4"), g["bits4"])
 
 
 # ---- matmul and elementwise -------------------------------------------------------------------------------------
