@@ -581,6 +581,8 @@ __global__ void __launch_bounds__(256) gemv_x_kernel(const XArgs h) {
 // loaded ahead of the values and made ready (bfp4's gaps placed, bfp8's handed out) while the values are in flight:
 // 6.25 us for the lm head at 16 rows in bfp4 and 8.83 in bfp8, against 6.72 and 9.87 with each round's exponents
 // waited for behind the values. The weights are read with the streaming cache policy (read once): 6.18 and 8.61.
+// A's rows in LDS are G chunks long, so mapping a thread's pieces of A to rows divides by a constant (about 75
+// fewer VALU instructions a wave than a division by the product's K): 5.92 and 8.35.
 template <int FMT, int DT, int MT, int NRW, int G, bool PROG>
 __global__ void __launch_bounds__(256) skinny_lds_kernel(const MatmulArgs args) {
   constexpr int TB = Tile<FMT>::bytes, R = (G + 3) / 4;  // R: rounds of 4 chunks (bfp4)
@@ -590,13 +592,17 @@ __global__ void __launch_bounds__(256) skinny_lds_kernel(const MatmulArgs args) 
   const Head h = early_head(args);
   const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
   const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int chunks = h.chunks, kp = chunks * 64 + 8;  // padded rows: a fragment read's 16 rows hit distinct banks
+  // A's rows in LDS are G chunks long whatever the product's K (padded: a fragment read's 16 rows hit distinct
+  // banks), so that a piece's row and place are a division by a constant
+  const int chunks = h.chunks;
+  constexpr int kp = G * 64 + 8;
   const int run0 = ((int)blockIdx.x * 4 + wib) * NRW;
   // 1. A's pieces for this thread (16 bytes each; rows past the last and columns past K are zeros), loaded before
   // the weights so that staging them waits for these alone
   // (buffer loads: the wait for them then counts them alone, where a flat load's wait would be for every load issued)
-  const int pieces = chunks * 8, kw = h.k / 8, total = 16 * MT * pieces;
-  constexpr int AP = (16 * MT * 96 + 255) / 256;  // at most 12 chunks: 96 pieces a row
+  const int kw = h.k / 8;
+  constexpr int pieces = G * 8, total = 16 * MT * pieces;
+  constexpr int AP = (total + 255) / 256;
   const __amdgpu_buffer_rsrc_t ar = buffer((const void *)(uintptr_t)h.a.ptr,
                                            (uint32_t)(((int64_t)(h.m - 1) * h.a.sr + h.k) * 2));
   uint4 av[AP];
@@ -2328,20 +2334,21 @@ static bool plain_out(const MatmulArgs &args) {
 }
 
 template <int FMT, int DT, int MT, int NRW, int G>
-static void launch_lds_g(const MatmulArgs &args, unsigned blocks, size_t lds, hipStream_t s) {
+static void launch_lds_g(const MatmulArgs &args, unsigned blocks, hipStream_t s) {
+  const size_t lds = (size_t)16 * MT * (G * 64 + 8) * 2;  // A, G chunks a row
   if (args.n_inst) skinny_lds_kernel<FMT, DT, MT, NRW, G, true><<<blocks, 256, lds, s>>>(args);
   else skinny_lds_kernel<FMT, DT, MT, NRW, G, false><<<blocks, 256, lds, s>>>(args);
 }
 template <int FMT, int DT, int MT, int NRW>
-static void launch_lds_n(const MatmulArgs &args, unsigned blocks, size_t lds, hipStream_t s) {
-  if (args.chunks <= 6) launch_lds_g<FMT, DT, MT, NRW, 6>(args, blocks, lds, s);
-  else if (args.chunks <= 9) launch_lds_g<FMT, DT, MT, NRW, 9>(args, blocks, lds, s);
-  else launch_lds_g<FMT, DT, MT, NRW, 12>(args, blocks, lds, s);
+static void launch_lds_n(const MatmulArgs &args, unsigned blocks, hipStream_t s) {
+  if (args.chunks <= 6) launch_lds_g<FMT, DT, MT, NRW, 6>(args, blocks, s);
+  else if (args.chunks <= 9) launch_lds_g<FMT, DT, MT, NRW, 9>(args, blocks, s);
+  else launch_lds_g<FMT, DT, MT, NRW, 12>(args, blocks, s);
 }
 template <int FMT, int DT>
-static void launch_lds(const MatmulArgs &args, unsigned blocks, size_t lds, hipStream_t s) {
-  if (args.m > 16) launch_lds_n<FMT, DT, 2, 1>(args, blocks, lds, s);
-  else launch_lds_n<FMT, DT, 1, 1>(args, blocks, lds, s);
+static void launch_lds(const MatmulArgs &args, unsigned blocks, hipStream_t s) {
+  if (args.m > 16) launch_lds_n<FMT, DT, 2, 1>(args, blocks, s);
+  else launch_lds_n<FMT, DT, 1, 1>(args, blocks, s);
 }
 
 template <int FMT, int DT, int ROWS>
@@ -2409,8 +2416,7 @@ static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bo
              ((int64_t)(args.m - 1) * args.a.sr + args.k) * 2 < (1ll << 31) && (args.n_inst || plain_out(args))) {
     // A staged whole in LDS once a block, a run a wave (more runs a wave measured slower: fewer waves in flight)
     const unsigned blocks = (unsigned)((args.nruns + 3) / 4);
-    const size_t lds = (size_t)(args.m > 16 ? 32 : 16) * (args.chunks * 64 + 8) * 2;
-    launch_lds<FMT, DT>(args, blocks, lds, s);
+    launch_lds<FMT, DT>(args, blocks, s);
   } else if (vec && fits && ((int64_t)31 * args.a.sr + 2 * (int64_t)args.k + 1024) * 2 < (1ll << 32)) {
     // two 16-row tiles a wave from 17 rows up; the waves of a run side by side. A short K (3-12 chunks) with many
     // rows: one tile a wave and all of K in one group of loads, so each wave makes one trip to memory.
