@@ -510,9 +510,9 @@ __global__ void __launch_bounds__(256) attention_combine_kernel(const bt_attenti
 
 // Prefill. A block is 4 waves and 128 consecutive pairs of one key head; wave w takes pairs 32w .. 32w + 31 of them as
 // two groups of 16 (the 16-pair tile of the scheme above), so every K and V fragment it reads from LDS feeds two
-// matrix instructions. The block's keys come through LDS 64 at a time, double-buffered, one barrier a step: K as it is
-// stored (row-major), V transposed (V^T[dim][key]) so that P V's value operand, 8 keys of one column, is two 8-byte
-// reads. The row sums come from the matrix cores too: P times a column of ones, accumulated and rescaled like O.
+// matrix instructions. The block's keys come through LDS 64 at a time, double-buffered, one barrier a step: K and V
+// as they are stored (row-major); P V's value operand, 8 keys of one column, is two transposing 8-byte reads
+// (ds_read_b64_tr_b16), so V is never transposed by VALU work. The row sums come from the matrix cores too: P times a column of ones, accumulated and rescaled like O.
 // Masks are applied only on blocks of keys that some pair of the wave sees in part, and the running output is
 // rescaled only when some pair's maximum moved. p is rounded to bf16 to nearest even (v_cvt_pk_bf16_f32).
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -540,9 +540,9 @@ template <int HD, typename Mid>
 __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf)[2][HD / 32], const uint16_t *kl,
                                            const uint16_t *vt, int kb, const int (&lo)[2], const int (&hi)[2],
                                            int lane, bool mask, Mid mid) {
-  // V^T rows of KB + 4 halfwords (34 dwords): the 16 rows one 8-byte read pass covers start 2 banks apart, so it
-  // hits 32 distinct banks (at KB + 8 rows n and n + 8 shared them)
-  constexpr int KS = HD + 8, VT = KB + 4;
+  // K rows of HD + 8 halfwords: the 16 rows of a fragment read start 4 banks apart. V rows of HD + 16 halfwords (8
+  // dwords apart, mod 64): a transposed read's 4 rows of 32 bytes fall in distinct banks.
+  constexpr int KS = HD + 8, VRS = HD + 16;
   constexpr float L2E = 1.4426950408889634f;
   const int g = lane >> 4, n = lane & 15;
   f32x4 s[2][4];
@@ -642,11 +642,16 @@ __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf
 #pragma unroll
     for (int q = 0; q < 2; q++)
       pa[q] = as_bf16x8(pb[q][2 * ks][0], pb[q][2 * ks][1], pb[q][2 * ks + 1][0], pb[q][2 * ks + 1][1]);
-    const uint16_t *col = vt + n * VT + 32 * ks + 4 * g;
+    // transposed reads of row-major V: lane n of a 16-lane group addresses key 4g + n / 4 of the step (and 16
+    // further), dims 16c + 4 (n % 4) .. + 3; the read hands lane n the group's 4 keys of dim 16c + n
+    const uint16_t *row = vt + (32 * ks + 4 * g + n / 4) * VRS + 4 * (n % 4);
 #pragma unroll
     for (int c = 0; c < HD / 16; c++) {
-      const uint2 a0 = *(const uint2 *)(col + 16 * c * VT);       // keys 4g .. 4g + 3 of the step
-      const uint2 a1 = *(const uint2 *)(col + 16 * c * VT + 16);  // keys 16 + 4g .. 16 + 4g + 3
+      typedef short s16x4 __attribute__((ext_vector_type(4)));
+      typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+      const s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(row + 16 * c));
+      const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(row + 16 * VRS + 16 * c));
+      const uint2 a0 = __builtin_bit_cast(uint2, r0), a1 = __builtin_bit_cast(uint2, r1);
       const bf16x8 vf = as_bf16x8(a0.x, a0.y, a1.x, a1.y);
       gr[0].o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], vf, gr[0].o[c], 0, 0, 0);
       gr[1].o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[1], vf, gr[1].o[c], 0, 0, 0);
@@ -663,8 +668,10 @@ __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf
 // Prefill. A block is 8 waves and 128 consecutive pairs of one key head. Waves w and w + 4 take the same 32 pairs,
 // as two groups of 16 (the tile of the scheme above), so every K and V fragment a wave reads from LDS feeds two matrix
 // instructions; the two halves of the block (waves 0-3, 4-7) split the keys, half h folding blocks 2t + h of 64 keys,
-// each half with its own double-buffered LDS stage, one barrier a step. K is staged as stored (row-major), V transposed
-// (V^T[dim][key]) so that P V's value operand, 8 keys of one column, is two 8-byte reads. The row sums come from the
+// each half with its own double-buffered LDS stage, one barrier a step. K and V are staged as stored (row-major); P V's
+// value operand, 8 keys of one column, is two transposing 8-byte reads of V (ds_read_b64_tr_b16: within each 16 lanes,
+// slot k of lane i is halfword i % 4 of what lane 4k + i / 4 addressed), which replaced staging V transposed by VALU
+// permutes (2048-row prefill 65.2-67.6 -> 61.4-63.2 us). The row sums come from the
 // matrix cores too: P times a column of ones, accumulated and rescaled like O. At the end half 1 hands its state to
 // half 0 through LDS, which joins the two (rescaling both to the larger maximum) and stores the output.
 //
@@ -672,11 +679,9 @@ __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf
 // and row block rblocks - 1 - u / kvhs.
 template <int HD, int KF>
 __global__ void __launch_bounds__(512, 1) attention_prefill_kernel(const bt_attention_args a, int rblocks, int kvhs) {
-  constexpr int KS = HD + 8, VT = KB + 4, KBUF = KB * KS, STG = KBUF + HD * VT;  // halfwords of one stage (VT as in
-                                                                                 // fold_pairs)
-  constexpr int KW = KB * HD / 8 / 256;  // 16-byte words of K each thread of a half moves per block
-  constexpr int KPT = HD / 32;           // keys of V each thread of a half moves per block (8 columns of each)
-  constexpr int NKG = KB / KPT;          // threads along the keys of V
+  constexpr int KS = HD + 8, VRS = HD + 16, KBUF = KB * KS, STG = KBUF + KB * VRS;  // halfwords of one stage (V
+                                                                                    // row-major, as fold_pairs reads it)
+  constexpr int KW = KB * HD / 8 / 256;  // 16-byte words of K (and of V) each thread of a half moves per block
   constexpr int XF = 2 * (HD / 4 + 8);   // floats per lane a wave hands over: O, l and the maxima of both groups
   static_assert(4 * XF * 64 * 4 <= 4 * STG * 2, "the hand-over fits in the stages");
   __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][STG];  // [half][stage]
@@ -727,37 +732,26 @@ __global__ void __launch_bounds__(512, 1) attention_prefill_kernel(const bt_atte
   // buffers end there
   const KvSrc kr = kv_src<KF>(a.k, a.k_exps, (int64_t)kvh * a.k_sh, bhi < 0 ? 0 : (int64_t)bhi * a.k_sr + HD);
   const KvSrc vr = kv_src<KF>(a.v, a.v_exps, (int64_t)kvh * a.v_sh, bhi < 0 ? 0 : (int64_t)bhi * a.v_sr + HD);
-  // K: thread's words at row kr0 + (256 / (HD / 8)) i, column kc; V: keys KPT kg .. + KPT - 1, columns 8 dg .. + 7.
+  // K and V: the thread's words at row kr0 + (256 / (HD / 8)) i, column kc (both staged row-major)
   const int kr0 = th / (HD / 8), kc = th % (HD / 8) * 8;
   constexpr int KSTEP = 256 / (HD / 8);
-  const int kg = th % NKG, dg = th / NKG;
   // value offsets from a block's first row: the thread's first word, then uniform steps
-  const uint32_t koff = (uint32_t)((int64_t)kr0 * a.k_sr + kc), voff = (uint32_t)((int64_t)KPT * kg * a.v_sr + 8 * dg);
-  const uint32_t kstep = (uint32_t)(KSTEP * a.k_sr), vstep = (uint32_t)a.v_sr;
-  uint4 kreg[KW], vreg[KPT];
+  const uint32_t koff = (uint32_t)((int64_t)kr0 * a.k_sr + kc), voff = (uint32_t)((int64_t)kr0 * a.v_sr + kc);
+  const uint32_t kstep = (uint32_t)(KSTEP * a.k_sr), vstep = (uint32_t)(KSTEP * a.v_sr);
+  uint4 kreg[KW], vreg[KW];
   auto fetch = [&](int kb) {
     const uint32_t kbo = (uint32_t)((int64_t)kb * a.k_sr), vbo = (uint32_t)((int64_t)kb * a.v_sr);
 #pragma unroll
     for (int i = 0; i < KW; i++) kreg[i] = kv_load8<KF>(kr, koff + (kbo + i * kstep));
 #pragma unroll
-    for (int i = 0; i < KPT; i++) vreg[i] = kv_load8<KF>(vr, voff + (vbo + i * vstep));
+    for (int i = 0; i < KW; i++) vreg[i] = kv_load8<KF>(vr, voff + (vbo + i * vstep));
   };
   auto stash = [&](uint16_t *stage) {
     uint16_t *kl = stage, *vt = stage + KBUF;
 #pragma unroll
     for (int i = 0; i < KW; i++) *(uint4 *)(kl + (kr0 + KSTEP * i) * KS + kc) = kreg[i];
 #pragma unroll
-    for (int d = 0; d < 8; d++) {
-      uint32_t w[KPT / 2];
-#pragma unroll
-      for (int i = 0; i < KPT; i += 2) {
-        const uint32_t x = ((const uint32_t *)&vreg[i])[d / 2], y = ((const uint32_t *)&vreg[i + 1])[d / 2];
-        w[i / 2] = d & 1 ? (x >> 16) | (y & 0xFFFF0000u) : (x & 0xFFFFu) | (y << 16);
-      }
-      uint16_t *at = vt + (8 * dg + d) * VT + KPT * kg;
-      if constexpr (KPT == 4) *(uint2 *)at = make_uint2(w[0], w[1]);
-      else *(uint32_t *)at = w[0];
-    }
+    for (int i = 0; i < KW; i++) *(uint4 *)(vt + (kr0 + KSTEP * i) * VRS + kc) = vreg[i];
   };
   // half hf folds blocks first + 64 (2t + hf), t < steps, the same count for both halves (a block past the last
   // visible key reads as zeros and is masked whole)
