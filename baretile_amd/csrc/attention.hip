@@ -21,6 +21,7 @@
 // visible keys, written as fp32 partial sums to scratch and combined by a second kernel. Prefill: the block's waves take 4 consecutive tiles and share each block
 // of 64 keys and values through LDS, double-buffered.
 #include "common.h"
+#include "lds_load.h"
 #include <mutex>
 #include <algorithm>
 #include <type_traits>
@@ -533,6 +534,12 @@ template <int HD> struct Group {
 // p stays below 256 and most blocks need no rescale; O / l is the same for any reference.
 constexpr float LAZY = 8.0f;
 
+// The prefill stages K and V row-major, HD halfwords a row, the 16-byte units of row r permuted: logical unit u sits
+// at u ^ swz(r), swz a permutation of 0..7. A K fragment read (8 rows a pass, one unit each) and a transposed V read
+// (4 rows a pass, two neighbouring units each) then fall in distinct banks, with no padding between rows, so that
+// rows can be loaded straight into LDS 1 KB a wave instruction.
+__device__ __forceinline__ int swz(int r) { return 2 * (r & 3) + ((r >> 2) & 1); }
+
 // mask: some pair of the wave sees only part of the block (wave-uniform). A block no pair sees leaves the state as
 // it was (every p is 0). mid() runs once the scores are made: the caller's loads of a later block, issued where fewer
 // registers are live.
@@ -540,11 +547,11 @@ template <int HD, typename Mid>
 __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf)[2][HD / 32], const uint16_t *kl,
                                            const uint16_t *vt, int kb, const int (&lo)[2], const int (&hi)[2],
                                            int lane, bool mask, Mid mid) {
-  // K rows of HD + 8 halfwords: the 16 rows of a fragment read start 4 banks apart. V rows of HD + 16 halfwords (8
-  // dwords apart, mod 64): a transposed read's 4 rows of 32 bytes fall in distinct banks.
-  constexpr int KS = HD + 8, VRS = HD + 16;
   constexpr float L2E = 1.4426950408889634f;
   const int g = lane >> 4, n = lane & 15;
+  int kcol[HD / 32];  // the lane's K fragment units (rows 16 kt + n: the same swizzle for every kt)
+#pragma unroll
+  for (int kk = 0; kk < HD / 32; kk++) kcol[kk] = ((4 * kk + g) ^ swz(n)) * 8;
   f32x4 s[2][4];
   uint32_t pb[2][4][2];  // [group][key tile][pair of keys]: packed p
   // p = 2^(s log2(e) - m) against the reference m before this block; if the block moves some pair's reference, those
@@ -569,13 +576,13 @@ __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf
   };
   bf16x8 kf[2][HD / 32];  // two key tiles' K fragments, the next read while the current one is multiplied
 #pragma unroll
-  for (int kk = 0; kk < HD / 32; kk++) kf[0][kk] = *(const bf16x8 *)(kl + n * KS + 32 * kk + 8 * g);
+  for (int kk = 0; kk < HD / 32; kk++) kf[0][kk] = *(const bf16x8 *)(kl + n * HD + kcol[kk]);
 #pragma unroll
   for (int kt = 0; kt < 4; kt++) {
     if (kt < 3) {
 #pragma unroll
       for (int kk = 0; kk < HD / 32; kk++)
-        kf[(kt + 1) & 1][kk] = *(const bf16x8 *)(kl + (16 * (kt + 1) + n) * KS + 32 * kk + 8 * g);
+        kf[(kt + 1) & 1][kk] = *(const bf16x8 *)(kl + (16 * (kt + 1) + n) * HD + kcol[kk]);
     }
     s[0][kt] = s[1][kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -643,14 +650,17 @@ __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf
     for (int q = 0; q < 2; q++)
       pa[q] = as_bf16x8(pb[q][2 * ks][0], pb[q][2 * ks][1], pb[q][2 * ks + 1][0], pb[q][2 * ks + 1][1]);
     // transposed reads of row-major V: lane n of a 16-lane group addresses key 4g + n / 4 of the step (and 16
-    // further), dims 16c + 4 (n % 4) .. + 3; the read hands lane n the group's 4 keys of dim 16c + n
-    const uint16_t *row = vt + (32 * ks + 4 * g + n / 4) * VRS + 4 * (n % 4);
+    // further), dims 16c + 4 (n % 4) .. + 3 (logical unit 2c + (n % 4) / 2); the read hands lane n the group's 4 keys
+    // of dim 16c + n
+    const uint16_t *row = vt + (32 * ks + 4 * g + n / 4) * HD + 4 * (n & 1);
+    const int fv = swz(4 * (g & 1) + n / 4), nu = (n & 3) >> 1;  // rows 32ks + 4g + n/4 (+ 16): that row mod 8
 #pragma unroll
     for (int c = 0; c < HD / 16; c++) {
       typedef short s16x4 __attribute__((ext_vector_type(4)));
       typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-      const s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(row + 16 * c));
-      const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(row + 16 * VRS + 16 * c));
+      const int at = ((2 * c + nu) ^ fv) * 8;
+      const s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(row + at));
+      const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(row + 16 * HD + at));
       const uint2 a0 = __builtin_bit_cast(uint2, r0), a1 = __builtin_bit_cast(uint2, r1);
       const bf16x8 vf = as_bf16x8(a0.x, a0.y, a1.x, a1.y);
       gr[0].o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[0], vf, gr[0].o[c], 0, 0, 0);
@@ -679,8 +689,7 @@ __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf
 // and row block rblocks - 1 - u / kvhs.
 template <int HD, int KF>
 __global__ void __launch_bounds__(512, 1) attention_prefill_kernel(const bt_attention_args a, int rblocks, int kvhs) {
-  constexpr int KS = HD + 8, VRS = HD + 16, KBUF = KB * KS, STG = KBUF + KB * VRS;  // halfwords of one stage (V
-                                                                                    // row-major, as fold_pairs reads it)
+  constexpr int KBUF = KB * HD, STG = 2 * KBUF;  // halfwords of one stage: K, then V, row-major, units swizzled (swz)
   constexpr int KW = KB * HD / 8 / 256;  // 16-byte words of K (and of V) each thread of a half moves per block
   constexpr int XF = 2 * (HD / 4 + 8);   // floats per lane a wave hands over: O, l and the maxima of both groups
   static_assert(4 * XF * 64 * 4 <= 4 * STG * 2, "the hand-over fits in the stages");
@@ -732,47 +741,90 @@ __global__ void __launch_bounds__(512, 1) attention_prefill_kernel(const bt_atte
   // buffers end there
   const KvSrc kr = kv_src<KF>(a.k, a.k_exps, (int64_t)kvh * a.k_sh, bhi < 0 ? 0 : (int64_t)bhi * a.k_sr + HD);
   const KvSrc vr = kv_src<KF>(a.v, a.v_exps, (int64_t)kvh * a.v_sh, bhi < 0 ? 0 : (int64_t)bhi * a.v_sr + HD);
-  // K and V: the thread's words at row kr0 + (256 / (HD / 8)) i, column kc (both staged row-major)
-  const int kr0 = th / (HD / 8), kc = th % (HD / 8) * 8;
-  constexpr int KSTEP = 256 / (HD / 8);
-  // value offsets from a block's first row: the thread's first word, then uniform steps
-  const uint32_t koff = (uint32_t)((int64_t)kr0 * a.k_sr + kc), voff = (uint32_t)((int64_t)kr0 * a.v_sr + kc);
-  const uint32_t kstep = (uint32_t)(KSTEP * a.k_sr), vstep = (uint32_t)(KSTEP * a.v_sr);
-  uint4 kreg[KW], vreg[KW];
-  auto fetch = [&](int kb) {
-    const uint32_t kbo = (uint32_t)((int64_t)kb * a.k_sr), vbo = (uint32_t)((int64_t)kb * a.v_sr);
-#pragma unroll
-    for (int i = 0; i < KW; i++) kreg[i] = kv_load8<KF>(kr, koff + (kbo + i * kstep));
-#pragma unroll
-    for (int i = 0; i < KW; i++) vreg[i] = kv_load8<KF>(vr, voff + (vbo + i * vstep));
-  };
-  auto stash = [&](uint16_t *stage) {
-    uint16_t *kl = stage, *vt = stage + KBUF;
-#pragma unroll
-    for (int i = 0; i < KW; i++) *(uint4 *)(kl + (kr0 + KSTEP * i) * KS + kc) = kreg[i];
-#pragma unroll
-    for (int i = 0; i < KW; i++) *(uint4 *)(vt + (kr0 + KSTEP * i) * VRS + kc) = vreg[i];
-  };
   // half hf folds blocks first + 64 (2t + hf), t < steps, the same count for both halves (a block past the last
   // visible key reads as zeros and is masked whole)
   const int first = blo & ~(KB - 1);
   const int nblk = bhi >= first ? (bhi - first) / KB + 1 : 0, steps = (nblk + 1) / 2;
   uint16_t *const st0 = lds[hf][0], *const st1 = lds[hf][1];
-  if (steps > 0) {
-    fetch(first + KB * hf);
-    stash(st0);
-  }
-  __syncthreads();
-  auto step = [&](int t, uint16_t *cur, uint16_t *nxt) {
-    const int kb = first + KB * (2 * t + hf);
-    const bool more = t + 1 < steps, mask = kb < alo || kb + KB - 1 > ahi;
-    fold_pairs<HD>(gr, qf, cur, cur + KBUF, kb, lo, hi, lane, mask, [&] {
-      if (more) fetch(kb + 2 * KB);
-    });
-    if (more) stash(nxt);
+  if constexpr (KF == BT_BF16) {
+    // bf16: each stage straight from memory into LDS, 1 KB a wave instruction, a block's stage requested at the start
+    // of the step before it (into the buffer that step's barrier freed), so it has a whole step to land and holds no
+    // registers. Wave wq's instruction i fills rows (wq + 4 i) RPI .. + RPI - 1: lane l row (l / UPR), unit l % UPR,
+    // which holds logical unit (l % UPR) ^ swz(row). (2048-row prefill 61.0-62.1 -> 60.4-60.8 us against loads into
+    // registers issued after the scores and stashed at the end of the step.)
+    constexpr int UPR = HD / 8, RPI = 64 / UPR, NI = KB / RPI / 4;
+    const i32x4 kw4 = buffer_words((const uint16_t *)(uintptr_t)a.k + (int64_t)kvh * a.k_sh,
+                                   bhi < 0 ? 0u : (uint32_t)(((int64_t)bhi * a.k_sr + HD) * 2));
+    const i32x4 vw4 = buffer_words((const uint16_t *)(uintptr_t)a.v + (int64_t)kvh * a.v_sh,
+                                   bhi < 0 ? 0u : (uint32_t)(((int64_t)bhi * a.v_sr + HD) * 2));
+    uint32_t kof[NI], vof[NI];  // byte offsets from a block's first row
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      const int r = (wq + 4 * i) * RPI + lane / UPR, uu = (lane % UPR) ^ swz(r);
+      kof[i] = (uint32_t)(((int64_t)r * a.k_sr + 8 * uu) * 2);
+      vof[i] = (uint32_t)(((int64_t)r * a.v_sr + 8 * uu) * 2);
+    }
+    auto load_stage = [&](int kb, uint16_t *stage) {
+      const uint32_t kbo = (uint32_t)((int64_t)kb * a.k_sr * 2), vbo = (uint32_t)((int64_t)kb * a.v_sr * 2);
+#pragma unroll
+      for (int i = 0; i < NI; i++) lds_load16(kw4, kbo + kof[i], stage + (wq + 4 * i) * RPI * HD);
+#pragma unroll
+      for (int i = 0; i < NI; i++) lds_load16(vw4, vbo + vof[i], stage + KBUF + (wq + 4 * i) * RPI * HD);
+    };
+    if (steps > 0) load_stage(first + KB * hf, st0);
+    wait_vm<0>();
     __syncthreads();
-  };
-  for (int t = 0; t < steps; t++) step(t, t & 1 ? st1 : st0, t & 1 ? st0 : st1);
+    auto step = [&](int t, uint16_t *cur, uint16_t *nxt) {
+      const int kb = first + KB * (2 * t + hf);
+      const bool more = t + 1 < steps, mask = kb < alo || kb + KB - 1 > ahi;
+      if (more) load_stage(kb + 2 * KB, nxt);
+      fold_pairs<HD>(gr, qf, cur, cur + KBUF, kb, lo, hi, lane, mask, [] {});
+      wait_vm<0>();
+      __syncthreads();
+    };
+    for (int t = 0; t < steps; t++) step(t, t & 1 ? st1 : st0, t & 1 ? st0 : st1);
+  } else {
+    // block floats: loaded into registers, decoded there, and written to LDS in the same layout. The thread's words
+    // at row kr0 + (256 / (HD / 8)) i, logical unit kc / 8.
+    const KvSrc kr = kv_src<KF>(a.k, a.k_exps, (int64_t)kvh * a.k_sh, bhi < 0 ? 0 : (int64_t)bhi * a.k_sr + HD);
+    const KvSrc vr = kv_src<KF>(a.v, a.v_exps, (int64_t)kvh * a.v_sh, bhi < 0 ? 0 : (int64_t)bhi * a.v_sr + HD);
+    const int kr0 = th / (HD / 8), kc = th % (HD / 8) * 8;
+    constexpr int KSTEP = 256 / (HD / 8);
+    // value offsets from a block's first row: the thread's first word, then uniform steps
+    const uint32_t koff = (uint32_t)((int64_t)kr0 * a.k_sr + kc), voff = (uint32_t)((int64_t)kr0 * a.v_sr + kc);
+    const uint32_t kstep = (uint32_t)(KSTEP * a.k_sr), vstep = (uint32_t)(KSTEP * a.v_sr);
+    uint4 kreg[KW], vreg[KW];
+    auto fetch = [&](int kb) {
+      const uint32_t kbo = (uint32_t)((int64_t)kb * a.k_sr), vbo = (uint32_t)((int64_t)kb * a.v_sr);
+#pragma unroll
+      for (int i = 0; i < KW; i++) kreg[i] = kv_load8<KF>(kr, koff + (kbo + i * kstep));
+#pragma unroll
+      for (int i = 0; i < KW; i++) vreg[i] = kv_load8<KF>(vr, voff + (vbo + i * vstep));
+    };
+    auto stash = [&](uint16_t *stage) {
+#pragma unroll
+      for (int i = 0; i < KW; i++) {
+        const int r = kr0 + KSTEP * i, at = r * HD + (((kc >> 3) ^ swz(r)) << 3);
+        *(uint4 *)(stage + at) = kreg[i];
+        *(uint4 *)(stage + KBUF + at) = vreg[i];
+      }
+    };
+    if (steps > 0) {
+      fetch(first + KB * hf);
+      stash(st0);
+    }
+    __syncthreads();
+    auto step = [&](int t, uint16_t *cur, uint16_t *nxt) {
+      const int kb = first + KB * (2 * t + hf);
+      const bool more = t + 1 < steps, mask = kb < alo || kb + KB - 1 > ahi;
+      fold_pairs<HD>(gr, qf, cur, cur + KBUF, kb, lo, hi, lane, mask, [&] {
+        if (more) fetch(kb + 2 * KB);
+      });
+      if (more) stash(nxt);
+      __syncthreads();
+    };
+    for (int t = 0; t < steps; t++) step(t, t & 1 ? st1 : st0, t & 1 ? st0 : st1);
+  }
   // half 1 hands over O, l and its maxima (row i's, for the rows this lane holds); half 0 joins and stores
   float *xs = (float *)&lds[0][0][0] + wq * XF * 64 + lane;
   float md[2][4];
