@@ -158,6 +158,23 @@ __device__ __forceinline__ uint32_t kv_exp8(const KvSrc &s, uint32_t e) {
   else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(s.exp, e / 16, 0, POL);
 }
 
+// x of lane l combined with lanes l ^ 16 and l ^ 32 (hence l ^ 48): the matrix-core layout's 4 lane groups that hold
+// one column. VALU lane swaps (v_permlane16_swap / v_permlane32_swap with both operands x: the pair comes back as
+// x[l] and x[l ^ 16], in one order or the other), where a shuffle would take a trip through LDS; max and the sum are
+// commutative, so the result is the shuffles' to the bit.
+__device__ __forceinline__ float max_groups(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_groups(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // A lane's pair: which query row it is, which keys it sees, where its q and output rows are.
 struct Pair {
   int lo, hi;  // visible keys lo..hi (empty when lo > hi)
@@ -212,8 +229,7 @@ __device__ __forceinline__ void fold_scores(State<HD> &st, f32x4 (&s)[4], const 
       if (j < pr.lo || j > pr.hi) s[kt][i] = -__builtin_inff();
       mx = fmaxf(mx, s[kt][i]);
     }
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  mx = max_groups(mx);
   const float mn = fmaxf(st.m, mx);
   const bool none = mn == -__builtin_inff();  // no key of the pair seen yet
   const float scale = none ? 1.0f : __expf(st.m - mn);
@@ -227,8 +243,7 @@ __device__ __forceinline__ void fold_scores(State<HD> &st, f32x4 (&s)[4], const 
       pb[kt][i] = bf16_packed(p);
       sum += bf16_value(pb[kt][i]);
     }
-  sum += __shfl_xor(sum, 16, 64);
-  sum += __shfl_xor(sum, 32, 64);
+  sum = sum_groups(sum);
   st.l = st.l * scale + sum;
   st.m = mn;
   float sc[4];
@@ -535,10 +550,16 @@ template <int HD> struct Group {
 constexpr float LAZY = 8.0f;
 
 // The prefill stages K and V row-major, HD halfwords a row, the 16-byte units of row r permuted: logical unit u sits
-// at u ^ swz(r), swz a permutation of 0..7. A K fragment read (8 rows a pass, one unit each) and a transposed V read
-// (4 rows a pass, two neighbouring units each) then fall in distinct banks, with no padding between rows, so that
-// rows can be loaded straight into LDS 1 KB a wave instruction.
-__device__ __forceinline__ int swz(int r) { return 2 * (r & 3) + ((r >> 2) & 1); }
+// at u ^ swz<HD>(r). LDS has 64 banks of 4 bytes, 256 bytes a bank line. A K fragment read takes 16 rows a pass, one
+// unit each; a transposed V read 8 rows a pass (4 keys of two lane groups), two neighbouring units each. At HD 128 (a
+// row a bank line, 16 units) swz is a permutation of 0..15 whose halves (rows 0-7, 8-15) differ in their top three
+// bits; at HD 64 (two rows a line, 8 units each) rows of one parity get distinct permutations of 0..7. Either way both
+// reads fall in distinct banks with no padding between rows, so rows can be loaded straight into LDS, 1 KB a wave
+// instruction.
+template <int HD> __device__ __forceinline__ int swz(int r) {
+  if constexpr (HD == 128) return 2 * (r & 7) + ((r >> 3) & 1);
+  else return 2 * ((r >> 1) & 3) + ((r >> 3) & 1);
+}
 
 // mask: some pair of the wave sees only part of the block (wave-uniform). A block no pair sees leaves the state as
 // it was (every p is 0). mid() runs once the scores are made: the caller's loads of a later block, issued where fewer
@@ -551,7 +572,7 @@ __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf
   const int g = lane >> 4, n = lane & 15;
   int kcol[HD / 32];  // the lane's K fragment units (rows 16 kt + n: the same swizzle for every kt)
 #pragma unroll
-  for (int kk = 0; kk < HD / 32; kk++) kcol[kk] = ((4 * kk + g) ^ swz(n)) * 8;
+  for (int kk = 0; kk < HD / 32; kk++) kcol[kk] = ((4 * kk + g) ^ swz<HD>(n)) * 8;
   f32x4 s[2][4];
   uint32_t pb[2][4][2];  // [group][key tile][pair of keys]: packed p
   // p = 2^(s log2(e) - m) against the reference m before this block; if the block moves some pair's reference, those
@@ -611,8 +632,7 @@ __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf
     float mx = s[q][0][0];
 #pragma unroll
     for (int e = 1; e < 16; e += 2) mx = fmaxf(fmaxf(mx, s[q][e / 4][e % 4]), s[q][(e + 1) / 4 % 4][(e + 1) % 4]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = max_groups(mx);
     const float m2 = mx * L2E;
     const bool up = m2 > gr[q].m + LAZY;  // false for a pair with no visible key in the block
     need |= up;
@@ -653,7 +673,7 @@ __device__ __forceinline__ void fold_pairs(Group<HD> (&gr)[2], const bf16x8 (&qf
     // further), dims 16c + 4 (n % 4) .. + 3 (logical unit 2c + (n % 4) / 2); the read hands lane n the group's 4 keys
     // of dim 16c + n
     const uint16_t *row = vt + (32 * ks + 4 * g + n / 4) * HD + 4 * (n & 1);
-    const int fv = swz(4 * (g & 1) + n / 4), nu = (n & 3) >> 1;  // rows 32ks + 4g + n/4 (+ 16): that row mod 8
+    const int fv = swz<HD>(4 * g + n / 4), nu = (n & 3) >> 1;  // rows 32ks + 4g + n/4 (+ 16) swizzle as row 4g + n/4
 #pragma unroll
     for (int c = 0; c < HD / 16; c++) {
       typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -750,7 +770,7 @@ __global__ void __launch_bounds__(512, 1) attention_prefill_kernel(const bt_atte
     // bf16: each stage straight from memory into LDS, 1 KB a wave instruction, a block's stage requested at the start
     // of the step before it (into the buffer that step's barrier freed), so it has a whole step to land and holds no
     // registers. Wave wq's instruction i fills rows (wq + 4 i) RPI .. + RPI - 1: lane l row (l / UPR), unit l % UPR,
-    // which holds logical unit (l % UPR) ^ swz(row). (2048-row prefill 61.0-62.1 -> 60.4-60.8 us against loads into
+    // which holds logical unit (l % UPR) ^ swz<HD>(row). (2048-row prefill 61.0-62.1 -> 60.4-60.8 us against loads into
     // registers issued after the scores and stashed at the end of the step.)
     constexpr int UPR = HD / 8, RPI = 64 / UPR, NI = KB / RPI / 4;
     const i32x4 kw4 = buffer_words((const uint16_t *)(uintptr_t)a.k + (int64_t)kvh * a.k_sh,
@@ -760,7 +780,7 @@ __global__ void __launch_bounds__(512, 1) attention_prefill_kernel(const bt_atte
     uint32_t kof[NI], vof[NI];  // byte offsets from a block's first row
 #pragma unroll
     for (int i = 0; i < NI; i++) {
-      const int r = (wq + 4 * i) * RPI + lane / UPR, uu = (lane % UPR) ^ swz(r);
+      const int r = (wq + 4 * i) * RPI + lane / UPR, uu = (lane % UPR) ^ swz<HD>(r);
       kof[i] = (uint32_t)(((int64_t)r * a.k_sr + 8 * uu) * 2);
       vof[i] = (uint32_t)(((int64_t)r * a.v_sr + 8 * uu) * 2);
     }
@@ -804,7 +824,7 @@ __global__ void __launch_bounds__(512, 1) attention_prefill_kernel(const bt_atte
     auto stash = [&](uint16_t *stage) {
 #pragma unroll
       for (int i = 0; i < KW; i++) {
-        const int r = kr0 + KSTEP * i, at = r * HD + (((kc >> 3) ^ swz(r)) << 3);
+        const int r = kr0 + KSTEP * i, at = r * HD + (((kc >> 3) ^ swz<HD>(r)) << 3);
         *(uint4 *)(stage + at) = kreg[i];
         *(uint4 *)(stage + KBUF + at) = vreg[i];
       }
