@@ -575,9 +575,9 @@ __global__ void __launch_bounds__(256) gemv_x_kernel(const XArgs h) {
 // with A's 16-byte reads while HBM idles). A run's 64 exponent bytes come in one 4-byte load a lane and are handed
 // to the lanes that use them with ds_bpermute. Otherwise as skinny_vec_kernel: groups of G chunks issued together
 // and unconditionally, B scaled by its exponents into bf16, K split into slices summed in order in LDS.
-// Up to 32 rows of A (one matrix) with a short K (at most G chunks, G <= 12): the block stages all of A (at most
-// 48 KB) in LDS once while its waves' weights are in flight, and each of its 4 waves multiplies NRW runs of B from
-// there. A is read from memory once a block instead of once a run, which is what limits the one-run kernels at 16
+// Up to 256 rows of A (one matrix) with a short K (at most G chunks, G <= 12), 16 MT of them a block (blockIdx.y):
+// the block stages its rows of A (at most 48 KB) in LDS once while its waves' weights are in flight, and each of its 4
+// waves multiplies NRW runs of B from there. A is read from memory once a block instead of once a run, which is what limits the one-run kernels at 16
 // rows (their A and exponent loads keep the texture units busy while HBM idles). Exponents as in skinny2_kernel,
 // loaded ahead of the values and made ready (bfp4's gaps placed, bfp8's handed out) while the values are in flight:
 // 6.25 us for the lm head at 16 rows in bfp4 and 8.83 in bfp8, against 6.72 and 9.87 with each round's exponents
@@ -598,6 +598,7 @@ __global__ void __launch_bounds__(256) skinny_lds_kernel(const MatmulArgs args) 
   const int chunks = h.chunks;
   constexpr int kp = G * 64 + 8;
   const int run0 = ((int)blockIdx.x * 4 + wib) * NRW;
+  const int row0 = 16 * MT * (int)blockIdx.y;  // the block's rows of A (and of the output): row0 .. row0 + 16 MT - 1
   // 1. A's pieces for this thread (16 bytes each; rows past the last and columns past K are zeros), loaded before
   // the weights so that staging them waits for these alone
   // (buffer loads: the wait for them then counts them alone, where a flat load's wait would be for every load issued)
@@ -610,7 +611,8 @@ __global__ void __launch_bounds__(256) skinny_lds_kernel(const MatmulArgs args) 
 #pragma unroll
   for (int j = 0; j < AP; j++) {
     const int q = (int)threadIdx.x + 256 * j, row = q / pieces, c8 = q % pieces;
-    const uint32_t off = q < total && row < h.m && c8 < kw ? (uint32_t)(row * (int)h.a.sr + c8 * 8) * 2 : 0x80000000u;
+    const uint32_t off =
+        q < total && row0 + row < h.m && c8 < kw ? (uint32_t)((row0 + row) * (int)h.a.sr + c8 * 8) * 2 : 0x80000000u;
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(ar, off, 0, 0);
     av[j] = make_uint4(v[0], v[1], v[2], v[3]);
   }
@@ -700,7 +702,8 @@ __global__ void __launch_bounds__(256) skinny_lds_kernel(const MatmulArgs args) 
     if (run0 + r >= h.nruns) continue;
     if constexpr (PROG) {
 #pragma unroll
-      for (int t = 0; t < MT; t++) store_tile<DT, false, true, 1>(args, h, acc[t], 0, t, run0 + r, g, col);
+      for (int t = 0; t < MT; t++)
+        store_tile<DT, false, true, 1>(args, h, acc[t], 0, (int)blockIdx.y * MT + t, run0 + r, g, col);
     } else {
       // without a program the output is plain (bf16 or fp32, contiguous rows, byte offsets within 32 bits: the host
       // checks): a buffer store a value, as the lean GEMV stores
@@ -712,7 +715,7 @@ __global__ void __launch_bounds__(256) skinny_lds_kernel(const MatmulArgs args) 
       for (int t = 0; t < MT; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const int mm = 16 * t + 4 * g + i;
+          const int mm = row0 + 16 * t + 4 * g + i;
           if (mm >= h.m || n >= h.n) continue;
           const uint32_t at = (uint32_t)(mm * (int)h.out.sr + n);
           if (bf) __builtin_amdgcn_raw_buffer_store_b16((uint16_t)bf16_packed(acc[t][i]), orr, at * 2, 0, 0);
@@ -2295,8 +2298,9 @@ static bool plain_out(const MatmulArgs &args) {
 template <int FMT, int DT, int MT, int NRW, int G>
 static void launch_lds_g(const MatmulArgs &args, unsigned blocks, hipStream_t s) {
   const size_t lds = (size_t)16 * MT * (G * 64 + 8) * 2;  // A, G chunks a row
-  if (args.n_inst) skinny_lds_kernel<FMT, DT, MT, NRW, G, true><<<blocks, 256, lds, s>>>(args);
-  else skinny_lds_kernel<FMT, DT, MT, NRW, G, false><<<blocks, 256, lds, s>>>(args);
+  const dim3 grid(blocks, (unsigned)((args.m + 16 * MT - 1) / (16 * MT)));  // y: blocks of 16 MT rows
+  if (args.n_inst) skinny_lds_kernel<FMT, DT, MT, NRW, G, true><<<grid, 256, lds, s>>>(args);
+  else skinny_lds_kernel<FMT, DT, MT, NRW, G, false><<<grid, 256, lds, s>>>(args);
 }
 template <int FMT, int DT, int MT, int NRW>
 static void launch_lds_n(const MatmulArgs &args, unsigned blocks, hipStream_t s) {
@@ -2371,9 +2375,11 @@ static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bo
       else if (group == 8) launch_sliced(gemv_kernel<FMT, DT, 4, 8, true, false, false>, args, units, 1, 8 * SB, 0, s);
       else launch_sliced(gemv_kernel<FMT, DT, 4, 12, true, false, false>, args, units, 1, 12 * SB, 0, s);
     }
-  } else if (FMT != BT_BF16 && vec && fits && args.batch == 1 && args.m <= 32 && args.chunks <= 12 &&
+  } else if (FMT != BT_BF16 && vec && fits && args.batch == 1 && args.m <= 256 && args.chunks <= 12 &&
              ((int64_t)(args.m - 1) * args.a.sr + args.k) * 2 < (1ll << 31) && (args.n_inst || plain_out(args))) {
-    // A staged whole in LDS once a block, a run a wave (more runs a wave measured slower: fewer waves in flight)
+    // A staged in LDS once a block (32 rows a block, the blocks of a run side by side in y), a run a wave (more runs
+    // a wave measured slower: fewer waves in flight). From 33 rows up each run's weights are decoded once for every
+    // 2 row tiles, where the one-tile skinny kernel decodes them once a tile: C1's 128 rows 10.1 -> 9.85 us.
     const unsigned blocks = (unsigned)((args.nruns + 3) / 4);
     launch_lds<FMT, DT>(args, blocks, s);
   } else if (vec && fits && ((int64_t)31 * args.a.sr + 2 * (int64_t)args.k + 1024) * 2 < (1ll << 32)) {
