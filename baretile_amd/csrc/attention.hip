@@ -272,29 +272,55 @@ __device__ __forceinline__ void fold_scores(State<HD> &st, f32x4 (&s)[4], const 
   }
 }
 
-// The Q^T operand fragments of the lane's pair: dims 32kk + 8(l/16) .. +8, zeros for a pair past the last.
+// pair_of with the Q^T operand fragments of the lane's pair (dims 32kk + 8(l/16) .. +8, zeros for a pair past the
+// last), every load issued before any is used: the place, the first key, the q row, as global loads from addresses
+// that are always valid (a pair past the last reads pair 0's and is then marked empty, a call without firsts reads the
+// place twice). So a kernel's prologue is one trip to memory rather than a chain of three.
 template <int HD>
-__device__ __forceinline__ void load_q(const bt_attention_args &a, const Pair &pr, int lane, bf16x8 (&qf)[HD / 32]) {
-  const uint16_t *q = (const uint16_t *)a.q + pr.q;
+__device__ __forceinline__ Pair pair_q(const bt_attention_args &a, int kvh, int p, int lane, bf16x8 (&qf)[HD / 32]) {
+  Pair x;
+  const int np = a.rep * a.rows;
+  x.valid = p < np;
+  const int pp = x.valid ? p : 0, h = pp % a.rep, r = pp / a.rep, e = kvh * a.rep + h;
+  x.q = (int64_t)e * a.q_sh + (int64_t)r * a.q_sr;
+  x.o = (int64_t)e * a.o_sh + (int64_t)r * a.o_sr;
+  const int32_t *pl = (const int32_t *)a.places + (int64_t)e * a.places_sh + r;
+  const int32_t *fp = a.firsts ? (const int32_t *)a.firsts + (int64_t)e * a.firsts_sh + r : pl;
+  const uint16_t *q = (const uint16_t *)a.q + x.q + 8 * (lane >> 4);
+  const int place = gload(pl), first = gload(fp);
+  uint4 v[HD / 32];
+#pragma unroll
+  for (int kk = 0; kk < HD / 32; kk++) v[kk] = gload((const uint4 *)(q + 32 * kk));
+  x.lo = a.window > 0 ? max(0, place - a.window + 1) : 0;
+  x.lo = max(x.lo, a.firsts ? first : 0);
+  x.hi = min(place, a.keys - 1);
+  if (!x.valid) x.lo = 1, x.hi = 0;
 #pragma unroll
   for (int kk = 0; kk < HD / 32; kk++) {
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (pr.valid) v = *(const uint4 *)(q + 32 * kk + 8 * (lane >> 4));
-    qf[kk] = *(const bf16x8 *)&v;
+    const uint4 w = x.valid ? v[kk] : make_uint4(0, 0, 0, 0);
+    qf[kk] = *(const bf16x8 *)&w;
   }
+  return x;
 }
 
-// The smallest first key and largest last key over the 16 pairs of the wave's tile (lanes 0..15 hold them all).
+// The smallest first key and largest last key over the 16 pairs of the wave's tile (each 16-lane row holds them
+// all): min and max over a row by DPP lane moves (swaps within quads, then the half-row and row mirrors), which take
+// no trip through LDS; min and max are exact, so the order doesn't matter.
+__device__ __forceinline__ int row_min(int x) {
+  x = min(x, __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false));   // quad_perm [1, 0, 3, 2]
+  x = min(x, __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false));   // quad_perm [2, 3, 0, 1]
+  x = min(x, __builtin_amdgcn_update_dpp(x, x, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  return min(x, __builtin_amdgcn_update_dpp(x, x, 0x140, 0xF, 0xF, false));  // row_mirror
+}
+__device__ __forceinline__ int row_max(int x) {
+  x = max(x, __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x141, 0xF, 0xF, false));
+  return max(x, __builtin_amdgcn_update_dpp(x, x, 0x140, 0xF, 0xF, false));
+}
 __device__ __forceinline__ void tile_range(const Pair &pr, int &lo, int &hi) {
-  lo = pr.lo <= pr.hi ? pr.lo : 0x7FFFFFFF;
-  hi = pr.lo <= pr.hi ? pr.hi : -1;
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) {
-    lo = min(lo, __shfl_xor(lo, o, 64));
-    hi = max(hi, __shfl_xor(hi, o, 64));
-  }
-  lo = __builtin_amdgcn_readfirstlane(lo);
-  hi = __builtin_amdgcn_readfirstlane(hi);
+  lo = __builtin_amdgcn_readfirstlane(row_min(pr.lo <= pr.hi ? pr.lo : 0x7FFFFFFF));
+  hi = __builtin_amdgcn_readfirstlane(row_max(pr.lo <= pr.hi ? pr.hi : -1));
 }
 
 // Floats of one tile's partial result: m[16], l[16], then O[16][HD].
@@ -409,9 +435,8 @@ attention_decode_kernel(const bt_attention_args a, int tiles, int parts, float *
   const int part = bid % parts;
   bid /= parts;
   const int t = bid % tiles, kvh = bid / tiles;
-  const Pair pr = pair_of(a, kvh, 16 * t + n);
   bf16x8 qf[HD / 32];
-  load_q<HD>(a, pr, lane, qf);
+  const Pair pr = pair_q<HD>(a, kvh, 16 * t + n, lane, qf);
   int lo, hi;
   tile_range(pr, lo, hi);
   const int start = lo & ~(KB - 1), nblk = hi >= lo ? (hi - start) / KB + 1 : 0, per = (nblk + parts - 1) / parts;
@@ -725,8 +750,7 @@ __global__ void __launch_bounds__(512, 1) attention_prefill_kernel(const bt_atte
   int lo[2], hi[2];
 #pragma unroll
   for (int q = 0; q < 2; q++) {
-    pr[q] = pair_of(a, kvh, base + 16 * q + n);
-    load_q<HD>(a, pr[q], lane, qf[q]);
+    pr[q] = pair_q<HD>(a, kvh, base + 16 * q + n, lane, qf[q]);
     lo[q] = pr[q].lo, hi[q] = pr[q].hi;
   }
   // the wave's range (union over its pairs) and the keys every valid pair sees (intersection)
@@ -736,11 +760,7 @@ __global__ void __launch_bounds__(512, 1) attention_prefill_kernel(const bt_atte
     if (pr[q].lo <= pr[q].hi) wlo = min(wlo, pr[q].lo), whi = max(whi, pr[q].hi);
     if (pr[q].valid) alo = max(alo, pr[q].lo), ahi = min(ahi, pr[q].hi);
   }
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) {
-    wlo = min(wlo, __shfl_xor(wlo, o, 64)), whi = max(whi, __shfl_xor(whi, o, 64));
-    alo = max(alo, __shfl_xor(alo, o, 64)), ahi = min(ahi, __shfl_xor(ahi, o, 64));
-  }
+  wlo = row_min(wlo), whi = row_max(whi), alo = row_max(alo), ahi = row_min(ahi);
   wlo = __builtin_amdgcn_readfirstlane(wlo), whi = __builtin_amdgcn_readfirstlane(whi);
   alo = __builtin_amdgcn_readfirstlane(alo), ahi = __builtin_amdgcn_readfirstlane(ahi);
   if (lane == 0 && hf == 0) range[wq][0] = wlo, range[wq][1] = whi;

@@ -10,6 +10,16 @@
 
 namespace bt {
 
+// Loads through the global address space, so the compiler emits global_load (vector memory only) rather than flat,
+// whose wait also waits for LDS. (The host pass of hipcc also parses device functions, and has no such address space.)
+template <class T> __device__ __forceinline__ T gload(const T *p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return *(const __attribute__((address_space(1))) T *)p;
+#else
+  return *p;
+#endif
+}
+
 // The last error's text, per host thread. Set by fail(), read through bt_last_error().
 void set_error(const char *fmt, ...);
 // fail(BT_EINVAL, "...") records the message and returns the code, so entry points can `return fail(...)`.

@@ -62,15 +62,6 @@ template <> struct Tile<BT_BF16> { static constexpr int bytes = 2048; };
 template <> struct Tile<BT_BFP8> { static constexpr int bytes = 1088; };
 template <> struct Tile<BT_BFP4> { static constexpr int bytes = 576; };
 
-// Loads through the global address space, so the compiler emits global_load (vector memory only) rather than flat.
-// (The host pass of hipcc also parses device functions, and has no such address space.)
-template <class T> __device__ __forceinline__ T gload(const T *p) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  return *(const __attribute__((address_space(1))) T *)p;
-#else
-  return *p;
-#endif
-}
 
 __device__ __forceinline__ uint32_t pack_hi(float lo, float hi) {  // two exact fp32 values -> a bf16 pair
   return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
