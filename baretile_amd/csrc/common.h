@@ -20,6 +20,21 @@ template <class T> __device__ __forceinline__ T gload(const T *p) {
 #endif
 }
 
+// The sum of x over the wave's 64 lanes, in every lane, with no trip through LDS: lanes l and l ^ 32, then l ^ 16
+// (VALU lane swaps, v_permlane32_swap / v_permlane16_swap with both operands x), then within 16-lane rows by DPP
+// moves: l ^ 8 (row_ror 8), l and 7 - l of each half-row (row_half_mirror), then l ^ 2 and l ^ 1 (quad_perm). Each
+// step pairs lanes symmetrically and adds the pair, so every lane ends with the same bits.
+__device__ __forceinline__ float wave_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+  x += __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0x128, 0xF, 0xF, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0x141, 0xF, 0xF, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0x4E, 0xF, 0xF, false));
+  return x + __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), 0xB1, 0xF, 0xF, false));
+}
+
 // The last error's text, per host thread. Set by fail(), read through bt_last_error().
 void set_error(const char *fmt, ...);
 // fail(BT_EINVAL, "...") records the message and returns the code, so entry points can `return fail(...)`.

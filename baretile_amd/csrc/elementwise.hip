@@ -59,11 +59,6 @@ __global__ void __launch_bounds__(256) elementwise_wide_kernel(const bt_program 
   }
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
 __device__ __forceinline__ float nan_max(float a, float b) {
   return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b);
 }
@@ -551,8 +546,7 @@ __global__ void __launch_bounds__(RMS_THREADS) rms_rows_kernel(const float *x, i
       const float e = round_packed(xr[c]);
       ss += e * e;
     }
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) ss += __shfl_xor(ss, s, 64);
+    ss = wave_sum(ss);
     if (lane == 0) part[wib] = ss;
     __syncthreads();
     float total = part[0];

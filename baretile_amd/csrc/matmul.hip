@@ -2151,8 +2151,7 @@ __global__ void __launch_bounds__(256) gemv_row_kernel(const RowArgs args, const
       const float v = round_packed(x[k]);
       ss += v * v;
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    ss = wave_sum(ss);
     if (lane == 0) red[wib] = ss;
     __syncthreads();
     const float total = ((red[0] + red[1]) + red[2]) + red[3];

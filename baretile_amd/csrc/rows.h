@@ -49,15 +49,14 @@ __device__ __forceinline__ uint16_t *rope_dst(const bt_rope_args &a, int i, int 
 // RMSNorm of one row by a block of RMS_THREADS threads, the row held in registers: thread t holds columns
 // (RMS_THREADS i + t) * 4 .. + 3 of group i < RMS_NV (zeros past k), already rounded to bf16 (half up), so every load
 // of the row is issued before the first is used. Returns 1 / sqrt(mean of x^2 + eps); the sum is each thread's groups
-// in order, then the wave's lanes by xor shuffles, then the waves in order. part: RMS_THREADS / 64 floats of LDS.
+// in order, then the wave's lanes (wave_sum), then the waves in order. part: RMS_THREADS / 64 floats of LDS.
 constexpr int RMS_THREADS = 1024, RMS_NV = 2;  // 2 x 4 x 1024 = 8192 columns
 __device__ __forceinline__ float rms_scale(const float4 (&v)[RMS_NV], int64_t k, float eps, float *part) {
   const int tid = threadIdx.x, lane = tid & 63, wib = tid >> 6;
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < RMS_NV; i++) ss += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
-#pragma unroll
-  for (int s = 32; s > 0; s >>= 1) ss += __shfl_xor(ss, s, 64);
+  ss = wave_sum(ss);
   if (lane == 0) part[wib] = ss;
   __syncthreads();
   float total = part[0];
