@@ -257,17 +257,18 @@ __device__ __forceinline__ void fold_scores(State<HD> &st, f32x4 (&s)[4], const 
   for (int ks = 0; ks < 2; ks++) {
     const bf16x8 pa = as_bf16x8(pb[2 * ks][0] | pb[2 * ks][1] << 16, pb[2 * ks][2] | pb[2 * ks][3] << 16,
                                 pb[2 * ks + 1][0] | pb[2 * ks + 1][1] << 16, pb[2 * ks + 1][2] | pb[2 * ks + 1][3] << 16);
-    const uint16_t *rows = vl + (32 * ks + 4 * g) * VS + n;
+    // transposing reads (ds_read_b64_tr_b16) of the row-major values: lane n of a 16-lane group addresses key
+    // 32ks + 4g + n / 4 (and 16 further), dims 16c + 4 (n % 4) .. + 3, and is handed the group's 4 keys of dim
+    // 16c + n, the operand's keys 4g .. 4g + 3 (then 16 + 4g ..) in order: two reads where 16-bit gathers took eight
+    const uint16_t *rows = vl + (32 * ks + 4 * g + n / 4) * VS + 4 * (n & 3);
 #pragma unroll
     for (int c = 0; c < HD / 16; c++) {
-      const uint16_t *at = rows + 16 * c;
-      uint32_t w[4];
-#pragma unroll
-      for (int j = 0; j < 4; j += 2) {
-        w[j / 2] = (uint32_t)at[j * VS] | (uint32_t)at[(j + 1) * VS] << 16;            // keys 4g + j, 4g + j + 1
-        w[2 + j / 2] = (uint32_t)at[(16 + j) * VS] | (uint32_t)at[(17 + j) * VS] << 16;  // keys 16 + 4g + j, +1
-      }
-      st.o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, as_bf16x8(w[0], w[1], w[2], w[3]), st.o[c], 0, 0, 0);
+      typedef short s16x4 __attribute__((ext_vector_type(4)));
+      typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+      const s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(rows + 16 * c));
+      const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(rows + 16 * VS + 16 * c));
+      const uint2 a0 = __builtin_bit_cast(uint2, r0), a1 = __builtin_bit_cast(uint2, r1);
+      st.o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, as_bf16x8(a0.x, a0.y, a1.x, a1.y), st.o[c], 0, 0, 0);
     }
   }
 }
@@ -425,7 +426,9 @@ __device__ __forceinline__ void decode_keys(bf16x8 (&kf)[4][HD / 32], const KeyB
 template <int HD, int KF, bool WIDE>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 attention_decode_kernel(const bt_attention_args a, int tiles, int parts, float *scratch) {
-  constexpr int VS = HD + 8, VR = KB * VS;  // halfwords of one wave's value block
+  // halfwords of one wave's value block: rows of HD + 16, so that the 8 rows a transposing read's pass of 32 lanes
+  // addresses (8 dwords each) start 8 banks apart
+  constexpr int VS = HD + 16, VR = KB * VS;
   constexpr int PF = partial_floats<HD>();
   static_assert(4 * PF * 4 <= 4 * VR * 2, "the wave partials fit in the value blocks' LDS");
   __shared__ __attribute__((aligned(16))) uint16_t lds[4 * VR];
