@@ -216,9 +216,10 @@ __device__ __forceinline__ void block_scores(f32x4 (&s)[4], const bf16x8 (&kf)[4
     for (int kk = 0; kk < HD / 32; kk++) s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kt][kk], qf[kk], s[kt], 0, 0, 0);
   }
 }
+// fresh (wave-uniform): st is still the initial state, whose zero O needs no rescale (skipping it gives the same bits)
 template <int HD, int VS>
 __device__ __forceinline__ void fold_scores(State<HD> &st, f32x4 (&s)[4], const uint16_t *vl, int kb, const Pair &pr,
-                                            int lane) {
+                                            int lane, bool fresh) {
   const int g = lane >> 4, n = lane & 15;
   float mx = -__builtin_inff();
 #pragma unroll
@@ -246,13 +247,15 @@ __device__ __forceinline__ void fold_scores(State<HD> &st, f32x4 (&s)[4], const 
   sum = sum_groups(sum);
   st.l = st.l * scale + sum;
   st.m = mn;
-  float sc[4];
+  if (!fresh) {
+    float sc[4];
 #pragma unroll
-  for (int i = 0; i < 4; i++) sc[i] = __shfl(scale, 4 * g + i, 64);
+    for (int i = 0; i < 4; i++) sc[i] = __shfl(scale, 4 * g + i, 64);
 #pragma unroll
-  for (int c = 0; c < HD / 16; c++)
+    for (int c = 0; c < HD / 16; c++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) st.o[c][i] *= sc[i];
+      for (int i = 0; i < 4; i++) st.o[c][i] *= sc[i];
+  }
 #pragma unroll
   for (int ks = 0; ks < 2; ks++) {
     const bf16x8 pa = as_bf16x8(pb[2 * ks][0] | pb[2 * ks][1] << 16, pb[2 * ks][2] | pb[2 * ks][3] << 16,
@@ -472,6 +475,7 @@ attention_decode_kernel(const bt_attention_args a, int tiles, int parts, float *
   // a block's values go out as soon as the previous block's are in LDS (B = 8 at 1024 keys 13.1 -> 10.9 us, B = 32 at
   // 4096 keys 95.5 -> 90-93 us), its keys once the previous scores are made; the last block's step is its own copy,
   // so the loop's fetches carry no condition.
+  bool fresh = true;  // the wave's first block
   auto step = [&](int kb, auto more) {
     constexpr bool MORE = decltype(more)::value;
     wave_lds_sync();  // the previous block's reads of vl are done
@@ -486,7 +490,8 @@ attention_decode_kernel(const bt_attention_args a, int tiles, int parts, float *
       block_scores<HD>(s, kf, qf);
     }
     if constexpr (MORE) fetch_keys<HD, KF, WIDE>(kbytes, kr, kb + 4 * KB, a.k_sr, lane);
-    fold_scores<HD, VS>(st, s, vl, kb, pr, lane);
+    fold_scores<HD, VS>(st, s, vl, kb, pr, lane, fresh);
+    fresh = false;
   };
   for (; kb + 4 * KB <= last; kb += 4 * KB) step(kb, std::true_type{});
   if (kb <= last) step(kb, std::false_type{});
