@@ -228,6 +228,27 @@ __device__ __forceinline__ void store_tile(const MatmulArgs &args, const Head &h
     return;
   }
   if constexpr (PROG != 0) {
+  // a program of one operation on the product and no inputs (relu(x), silu(x), x * x, ...): the operation straight on
+  // the lane's 4 values, without the evaluator's register file (its other registers read as 0 until written); the
+  // same arithmetic, so the same bits
+  const bt_inst in0 = args.prog.inst[0];
+  if (h.n_inst == 1 && args.prog.n_inputs == 0 && args.prog.result == in0.dst && in0.op != BT_OP_LOAD &&
+      in0.op != BT_OP_CONST && in0.op != BT_OP_MOV && in0.op != BT_OP_WHERE) {
+    Vals<4> va, vb;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t x = __float_as_uint(DT == BT_BF16 ? round_packed(acc[i]) : acc[i]);
+      va.x[i] = in0.a == 0 ? x : 0u;
+      vb.x[i] = in0.b == 0 ? x : 0u;
+    }
+    const Vals<4> o = apply_op<DT, 4, INL>(in0.op, va, vb);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int mm = mt * 16 + 4 * g + i;
+      if (mm < m) store_value<DT>(out, obase + (int64_t)mm * out.sr, o.x[i]);
+    }
+    return;
+  }
 #pragma unroll 1
   for (int i = 0; i < 4; i++) {
     const int mm = mt * 16 + 4 * g + i;
