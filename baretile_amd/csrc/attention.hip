@@ -18,7 +18,8 @@
 //
 // Decode (at most 4 tiles, 64 pairs, per key head): the block's 4 waves split the keys of one tile, 64 at a time, and
 // combine their running sums in LDS at the end. Long caches are split further into parts, each a run of the tile's
-// visible keys, written as fp32 partial sums to scratch and combined by a second kernel. Prefill: the block's waves take 4 consecutive tiles and share each block
+// visible keys, written as fp32 partial sums to scratch and combined by a second kernel; from 5 to 16 blocks of keys a
+// part is one block, folded by a block of one wave whose state is the part's partial sum. Prefill: the block's waves take 4 consecutive tiles and share each block
 // of 64 keys and values through LDS, double-buffered.
 #include "common.h"
 #include "lds_load.h"
@@ -502,6 +503,66 @@ attention_decode_kernel(const bt_attention_args a, int tiles, int parts, float *
   finish_tile<HD>(a, ws, 4, kvh, t, part, parts, tiles, scratch);
 }
 
+// Decode in parts of one 64-key block each, a block of one wave: the wave folds its block and writes its state as the
+// part's partial result, from its registers, with no join through LDS (which a 4-wave block of one or two blocks of
+// keys spends most of its time on). The combine kernel joins the parts.
+template <int HD, int KF, bool WIDE>
+__global__ void __launch_bounds__(64) attention_decode1_kernel(const bt_attention_args a, int tiles, int parts,
+                                                               float *scratch) {
+  constexpr int VS = HD + 16, VR = KB * VS, PF = partial_floats<HD>();
+  __shared__ __attribute__((aligned(16))) uint16_t vl[VR];
+  const int lane = threadIdx.x, g = lane >> 4, n = lane & 15;
+  int bid = blockIdx.x;
+  const int part = bid % parts;
+  bid /= parts;
+  const int t = bid % tiles, kvh = bid / tiles;
+  bf16x8 qf[HD / 32];
+  const Pair pr = pair_q<HD>(a, kvh, 16 * t + n, lane, qf);
+  int lo, hi;
+  tile_range(pr, lo, hi);
+  const int start = lo & ~(KB - 1), nblk = hi >= lo ? (hi - start) / KB + 1 : 0, per = (nblk + parts - 1) / parts;
+  const int first = start + part * per * KB, last = min(first + per * KB - 1, hi);
+  State<HD> st;
+  st.m = -__builtin_inff(), st.l = 0.0f;
+#pragma unroll
+  for (int c = 0; c < HD / 16; c++) st.o[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const KvSrc kr = kv_src<KF>(a.k, a.k_exps, (int64_t)kvh * a.k_sh, (int64_t)(a.keys - 1) * a.k_sr + HD);
+  const KvSrc vr = kv_src<KF>(a.v, a.v_exps, (int64_t)kvh * a.v_sh, (int64_t)(a.keys - 1) * a.v_sr + HD);
+  constexpr int RPI = 64 * 8 / HD, VI = KB / RPI;
+  const int vrow = lane / (HD / 8), vcol = lane % (HD / 8) * 8;
+  bool fresh = true;
+  for (int kb = first; kb <= last; kb += KB) {
+    Raw8<KF> vq[VI];
+    uint32_t vx[VI];
+#pragma unroll
+    for (int i = 0; i < VI; i++) {
+      const uint32_t e = (uint32_t)((int64_t)(kb + vrow + RPI * i) * a.v_sr + vcol);
+      vq[i] = kv_fetch8<KF, DEC_POL>(vr, e);
+      vx[i] = kv_exp8<KF, DEC_POL>(vr, e);
+    }
+    KeyBytes<HD, KF, WIDE> kbytes;
+    fetch_keys<HD, KF, WIDE>(kbytes, kr, kb, a.k_sr, lane);
+    wave_lds_sync();  // the previous block's reads of vl are done
+#pragma unroll
+    for (int i = 0; i < VI; i++) *(uint4 *)(vl + (vrow + RPI * i) * VS + vcol) = kv_value8<KF>(vq[i], vx[i]);
+    wave_lds_sync();
+    f32x4 sc[4];
+    {
+      bf16x8 kf[4][HD / 32];
+      decode_keys<HD, KF, WIDE>(kf, kbytes, lane);
+      block_scores<HD>(sc, kf, qf);
+    }
+    fold_scores<HD, VS>(st, sc, vl, kb, pr, lane, fresh);
+    fresh = false;
+  }
+  float *dst = scratch + ((int64_t)(kvh * tiles + t) * parts + part) * PF;
+  if (lane < 16) dst[n] = st.m, dst[16 + n] = st.l;
+#pragma unroll
+  for (int c = 0; c < HD / 16; c++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) dst[32 + (4 * g + i) * HD + 16 * c + n] = st.o[c][i];
+}
+
 // Joins the parts of each tile: M = max m_p, L = sum e^(m_p - M) l_p, out = sum e^(m_p - M) O_p / L. The block
 // first finds every pair's M, weights and L with its 16 groups of 16 threads splitting the parts (weights kept in
 // LDS), then each thread sums its output columns over the parts, loads independent of one another.
@@ -932,6 +993,16 @@ static void launch_decode(const bt_attention_args &a, unsigned blocks, int tiles
   else launch_decode_hd<128>(a, blocks, tiles, parts, scratch, s);
 }
 template <int HD>
+static void launch_decode1_hd(const bt_attention_args &a, unsigned blocks, int tiles, int parts, float *scratch,
+                              hipStream_t s) {
+  const bool wide = a.k_sr % HD == 0 && a.k_sh % HD == 0 && a.k_exps % (HD / 16) == 0;
+  if (a.kv_fmt == BT_BFP8 && wide) attention_decode1_kernel<HD, BT_BFP8, true><<<blocks, 64, 0, s>>>(a, tiles, parts, scratch);
+  else if (a.kv_fmt == BT_BFP8) attention_decode1_kernel<HD, BT_BFP8, false><<<blocks, 64, 0, s>>>(a, tiles, parts, scratch);
+  else if (a.kv_fmt == BT_BFP4 && wide) attention_decode1_kernel<HD, BT_BFP4, true><<<blocks, 64, 0, s>>>(a, tiles, parts, scratch);
+  else if (a.kv_fmt == BT_BFP4) attention_decode1_kernel<HD, BT_BFP4, false><<<blocks, 64, 0, s>>>(a, tiles, parts, scratch);
+  else attention_decode1_kernel<HD, BT_BF16, false><<<blocks, 64, 0, s>>>(a, tiles, parts, scratch);
+}
+template <int HD>
 static void launch_prefill_hd(const bt_attention_args &a, unsigned blocks, int rblocks, int kvh, hipStream_t s) {
   if (a.kv_fmt == BT_BFP8) attention_prefill_kernel<HD, BT_BFP8><<<blocks, 512, 0, s>>>(a, rblocks, kvh);
   else if (a.kv_fmt == BT_BFP4) attention_prefill_kernel<HD, BT_BFP4><<<blocks, 512, 0, s>>>(a, rblocks, kvh);
@@ -944,6 +1015,7 @@ static void launch_prefill(const bt_attention_args &a, unsigned blocks, int rblo
 
 struct AttnPlan {
   bool decode;
+  bool one;  // decode parts of one block of keys each, a wave a part (attention_decode1_kernel)
   int tiles, parts, kpp;
   uint64_t scratch_bytes;
 };
@@ -972,7 +1044,7 @@ static int plan_attention(const bt_attention_args *a, AttnPlan *p) {
   const int kvh = a->heads / a->rep, np = a->rep * a->rows;
   p->tiles = (np + 15) / 16;
   p->decode = p->tiles <= 4;  // few query rows for each key head: split the keys instead
-  p->parts = 1, p->kpp = 0, p->scratch_bytes = 0;
+  p->parts = 1, p->kpp = 0, p->scratch_bytes = 0, p->one = false;
   if (p->decode) {
     const int nblk = (a->keys + KB - 1) / KB;
     int parts = a->parts;
@@ -981,10 +1053,16 @@ static int plan_attention(const bt_attention_args *a, AttnPlan *p) {
     // shorter-lived blocks at 1-32 batch entries and 4096-16384 keys. A part's keys are a chain of dependent loads,
     // so up to 32 blocks of 64 keys, parts of two blocks (and the combine's launch) beat longer ones; beyond, four;
     // up to 4 blocks, one part (no combine) is the fastest.
-    const int target = a->kv_fmt == BT_BF16 ? 256 : 512;
+    // 5 to 16 blocks of keys over at most 512 blocks of the grid: a part a block of keys, a wave a part, joined by the
+    // combine alone (B=1 at 512 keys 7.55 -> 6.79 us, at 1024 7.99 -> 7.70; B=8 at 512 the same, at 1024 slower)
+    const int target = a->kv_fmt == BT_BF16 ? 256 : 512, units = kvh * p->tiles;
     const int per_part = nblk <= 4 ? nblk : nblk <= 32 ? 2 : 4;
-    if (parts == 0) parts = std::min((target + kvh * p->tiles / 2) / (kvh * p->tiles), std::max(1, nblk / per_part));
+    if (parts == 0) {
+      if (nblk > 4 && nblk <= 16 && units * nblk <= 512) parts = nblk;
+      else parts = std::min((target + units / 2) / units, std::max(1, nblk / per_part));
+    }
     p->parts = std::max(1, std::min(std::min(parts, nblk), MAX_PARTS));
+    p->one = p->parts > 1 && p->parts >= nblk;
     const int pf = 32 + 16 * a->head_dim;
     if (p->parts > 1) p->scratch_bytes = (uint64_t)kvh * p->tiles * p->parts * pf * 4;
   }
@@ -1014,7 +1092,12 @@ static int run_attention(Runtime *r, const bt_attention_args *a, const AttnPlan 
   const int kvh = a->heads / a->rep;
   if (p.decode) {
     const unsigned blocks = (unsigned)(kvh * p.tiles * p.parts);
-    launch_decode(*a, blocks, p.tiles, p.parts, scratch, r->stream);
+    if (p.one) {
+      if (a->head_dim == 64) launch_decode1_hd<64>(*a, blocks, p.tiles, p.parts, scratch, r->stream);
+      else launch_decode1_hd<128>(*a, blocks, p.tiles, p.parts, scratch, r->stream);
+    } else {
+      launch_decode(*a, blocks, p.tiles, p.parts, scratch, r->stream);
+    }
     BT_LAUNCHED("attention");
     if (p.parts > 1) {
       const unsigned cb = (unsigned)(kvh * p.tiles);

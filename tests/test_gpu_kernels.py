@@ -489,7 +489,8 @@ ATTENTION_CASES = [(4, 8, 64, 96, 2, 0, 0), (2, 40, 128, 200, 1, 50, 0), (8, 1, 
                    (32, 1, 128, 4096, 4, 0, 0), (9, 32, 64, 160, 3, 0, 0), (9, 1, 64, 160, 3, 0, 0),
                    (8, 1, 128, 1000, 4, 0, 7), (8, 2, 64, 700, 4, 100, 0), (8, 256, 128, 300, 4, 0, 0),
                    (6, 130, 64, 130, 3, 17, 0), (32, 1, 128, 16384, 4, 0, 0), (16, 600, 128, 600, 4, 0, 0),
-                   (6, 333, 64, 400, 3, 0, 0)]
+                   (6, 333, 64, 400, 3, 0, 0), (8, 1, 128, 512, 4, 0, 8), (8, 2, 64, 300, 4, 30, 5),
+                   (16, 1, 64, 640, 4, 0, 16)]
 
 
 @pytest.mark.parametrize("case", ATTENTION_CASES, ids=lambda c: "e{}r{}d{}k{}rep{}w{}p{}".format(*c))
