@@ -2321,8 +2321,7 @@ static void launch_lds_n(const MatmulArgs &args, unsigned blocks, hipStream_t s)
 }
 template <int FMT, int DT>
 static void launch_lds(const MatmulArgs &args, unsigned blocks, hipStream_t s) {
-  if (args.m > 16) launch_lds_n<FMT, DT, 2, 1>(args, blocks, s);
-  else launch_lds_n<FMT, DT, 1, 1>(args, blocks, s);
+  launch_lds_n<FMT, DT, 1, 1>(args, blocks, s);
 }
 
 template <int FMT, int DT, int ROWS>
@@ -2388,9 +2387,11 @@ static void launch_dt(const MatmulArgs &args, unsigned blocks, hipStream_t s, bo
     }
   } else if (FMT != BT_BF16 && vec && fits && args.batch == 1 && args.m <= 256 && args.chunks <= 12 &&
              ((int64_t)(args.m - 1) * args.a.sr + args.k) * 2 < (1ll << 31) && (args.n_inst || plain_out(args))) {
-    // A staged in LDS once a block (32 rows a block, the blocks of a run side by side in y), a run a wave (more runs
-    // a wave measured slower: fewer waves in flight). From 33 rows up each run's weights are decoded once for every
-    // 2 row tiles, where the one-tile skinny kernel decodes them once a tile: C1's 128 rows 10.1 -> 9.85 us.
+    // A staged in LDS once a block (16 rows a block, the blocks of a run side by side in y), a run a wave (more runs
+    // a wave measured slower: fewer waves in flight). Two row tiles a wave, each run's weights decoded once for both,
+    // measured 9.85 us for C1's 128 rows against 10.1 for the one-tile skinny kernel while the epilogue ran through the
+    // program evaluator; with one-operation epilogues run straight, one tile a wave (twice the waves, half the chain
+    // after the last byte) is 4.75 us against 6.41.
     const unsigned blocks = (unsigned)((args.nruns + 3) / 4);
     launch_lds<FMT, DT>(args, blocks, s);
   } else if (vec && fits && ((int64_t)31 * args.a.sr + 2 * (int64_t)args.k + 1024) * 2 < (1ll << 32)) {
