@@ -213,8 +213,9 @@ def test_fused_relu_epilogue_config1(rt):
   assert np.all(np.abs(fused - np.maximum(ops.matmul(xw, wq), 0)) <= ops.matmul_bound(xw, wq))
 
 
+@pytest.mark.parametrize("out", ["bf16", "fp32"])
 @pytest.mark.parametrize("m", [1, 4, 16, 128, 600])
-def test_one_operation_epilogues_equal_the_evaluator(rt, m):
+def test_one_operation_epilogues_equal_the_evaluator(rt, m, out):
   # An epilogue of one operation on the product with no inputs (relu, silu, exp, neg, x * x, x + x) runs as that
   # operation straight on the tile; the same program behind a mov runs
   # through the evaluator. Bit for bit the same, in every kernel the row counts reach (the GEMV, the A-staging kernel,
@@ -224,20 +225,23 @@ def test_one_operation_epilogues_equal_the_evaluator(rt, m):
   x, w = rng.normal(0, 1, (m, 576)), rng.normal(0, 0.02, (576, 1536)).astype(np.float32)
   exps, vals = pack(rt, w, "bfp8")
   cols = columns(rt, exps, vals, "bfp8", 1, 576, 1536)
-  plain = matmul(rt, x, cols, "bfp8", 1, 1536)[0]
+  plain = matmul(rt, x, cols, "bfp8", 1, 1536, out=out)[0]
   for name in ("relu", "silu", "exp", "neg", "mul", "add"):
-    p, q = Program("bf16", epilogue=True), Program("bf16", epilogue=True)
+    p, q = Program(out, epilogue=True), Program(out, epilogue=True)
     if name in ("mul", "add"):
       fast = p.build(p.op(name, p.value(), p.value()))
       slow = q.build(q.op(name, q.op("mov", q.value()), q.value()))
     else:
       fast, slow = p.build(p.op(name, p.value())), q.build(q.op(name, q.op("mov", q.value())))
     assert fast.n_inst == 1 and slow.n_inst == 2
-    got, want = matmul(rt, x, cols, "bfp8", 1, 1536, prog=fast)[0], matmul(rt, x, cols, "bfp8", 1, 1536, prog=slow)[0]
+    got = matmul(rt, x, cols, "bfp8", 1, 1536, out=out, prog=fast)[0]
+    want = matmul(rt, x, cols, "bfp8", 1, 1536, out=out, prog=slow)[0]
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), name
-  relu = matmul(rt, x, cols, "bfp8", 1, 1536, prog=(lambda p: p.build(p.op("relu", p.value())))(Program("bf16", epilogue=True)))[0]
+  relu = matmul(rt, x, cols, "bfp8", 1, 1536, out=out,
+                prog=(lambda p: p.build(p.op("relu", p.value())))(Program(out, epilogue=True)))[0]
   assert np.array_equal(relu, np.maximum(plain, 0))
-  neg = matmul(rt, x, cols, "bfp8", 1, 1536, prog=(lambda p: p.build(p.op("neg", p.value())))(Program("bf16", epilogue=True)))[0]
+  neg = matmul(rt, x, cols, "bfp8", 1, 1536, out=out,
+               prog=(lambda p: p.build(p.op("neg", p.value())))(Program(out, epilogue=True)))[0]
   assert np.array_equal(neg, -plain)
 
 

@@ -467,9 +467,11 @@ def test_block_float_cache_long_decode(rt):
 
 
 @pytest.mark.parametrize("fmt", ["bfp8", "bfp4"])
-def test_block_float_cache_split_decode(rt, fmt):
-  # 480 cached rows (8 blocks of 64 keys: parts of two blocks, then their combine), 128-wide heads, two query rows:
-  # the cache read in place gives bit for bit what its values give in bf16
+@pytest.mark.parametrize("parts", [None, 4])
+def test_block_float_cache_split_decode(rt, fmt, parts):
+  # 480 cached rows (8 blocks of 64 keys: by default a part a block, one-wave parts; with 4 parts, parts of two blocks
+  # on 4-wave blocks; then their combine), 128-wide heads, two query rows: the cache read in place gives bit for bit
+  # what its values give in bf16
   rng = np.random.default_rng(22)
   x = B.bf16(rng.normal(0, 1, (4, 480, 128)))
   cache = Tensor.of(rt, np.zeros((4, 480, 128), np.float32)).cast(fmt).realize()
@@ -477,8 +479,8 @@ def test_block_float_cache_split_decode(rt, fmt):
   same = Tensor.of(rt, value(cache).reshape(4, 480, 128).astype(np.float32))
   q = Tensor.of(rt, B.bf16(rng.normal(0, 1, (8, 2, 128)) / 11).astype(np.float32))
   pl = Tensor.of(rt, [[[470], [479]]], "int32")
-  got = q.attend(cache[0:2, :, :].repeat_interleave(4), cache[2:4, :, :].repeat_interleave(4), pl)
-  want = q.attend(same[0:2, :, :].repeat_interleave(4), same[2:4, :, :].repeat_interleave(4), pl)
+  got = q.attend(cache[0:2, :, :].repeat_interleave(4), cache[2:4, :, :].repeat_interleave(4), pl, parts=parts)
+  want = q.attend(same[0:2, :, :].repeat_interleave(4), same[2:4, :, :].repeat_interleave(4), pl, parts=parts)
   assert got.tobytes() == want.tobytes()
 
 
