@@ -5,6 +5,8 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdarg>
+#include <mutex>
+#include <unordered_map>
 #include <vector>
 #include "../../include/baretile_amd.h"
 
@@ -65,6 +67,19 @@ struct Runtime {
   void *scratch = nullptr;
   size_t scratch_bytes = 0;
   std::vector<void *> retired;
+  // Every block bt_alloc handed out (bytes: a multiple of 256; plain: made by hipMalloc inside a capture, else taken
+  // from the device's stream-ordered pool), and the freed ones kept by size for the next allocation of that size.
+  // Every launch of the runtime goes to its one stream, so a block freed after the launches that use it can serve a
+  // later allocation at once, in stream order, as the pool would, without the pool's cost on every call (about 10 us
+  // a free, which made a one-token decode step bound by its host code).
+  struct Block {
+    uint64_t bytes;
+    bool plain, kept;
+  };
+  std::mutex blocks_lock;  // ctypes lets go of Python's lock for each call, and a tensor may be freed on any thread
+  std::unordered_map<void *, Block> blocks;
+  std::unordered_map<uint64_t, std::vector<void *>> kept;
+  uint64_t kept_bytes = 0;
 };
 
 // The runtime's scratch of at least `bytes`, or null: inside a capture when it would have to grow (the caller then

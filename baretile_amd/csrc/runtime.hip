@@ -75,6 +75,27 @@ __global__ void sleep_kernel(uint64_t ticks, uint32_t *out) {
   if (out && now == start) out[0] = 1;  // never taken once ticks > 0; keeps the loop observable
 }
 
+// At most this much memory is kept for reuse, in blocks of at most KEEP_BLOCK; larger blocks go back to the pool.
+constexpr uint64_t KEEP_BLOCK = 256ull << 20, KEEP_TOTAL = 4ull << 30;
+
+// Gives every kept block back: the pool's in stream order, the plain ones once the stream has drained. Not inside a
+// capture, where a free would be recorded into the graph. The caller holds blocks_lock.
+int release_kept(Runtime *r) {
+  std::vector<void *> plain;
+  for (auto &size : r->kept)
+    for (void *p : size.second) {
+      auto b = r->blocks.find(p);
+      if (b->second.plain) plain.push_back(p);
+      else BT_HIP(hipFreeAsync(p, r->stream));
+      r->blocks.erase(b);
+    }
+  r->kept.clear();
+  r->kept_bytes = 0;
+  if (!plain.empty()) BT_HIP(hipStreamSynchronize(r->stream));
+  for (void *p : plain) BT_HIP(hipFree(p));
+  return BT_OK;
+}
+
 }  // namespace bt
 
 using namespace bt;
@@ -147,6 +168,10 @@ int bt_close(bt_runtime *rt) {
   if (r->closed) return BT_OK;
   BT_HIP(hipSetDevice(r->device));
   if (r->capture_origin) return fail(BT_ESTATE, "close a runtime after ending its graph capture");
+  {
+    std::lock_guard<std::mutex> hold(r->blocks_lock);
+    if (int s = release_kept(r)) return s;
+  }
   BT_HIP(hipStreamSynchronize(r->stream));
   BT_HIP(hipStreamDestroy(r->stream));
   for (void *p : r->retired) (void)hipFree(p);
@@ -180,13 +205,29 @@ int bt_alloc(bt_runtime *rt, uint64_t bytes, uint64_t *addr) {
   Runtime *r;
   if (int s = enter(rt, &r)) return s;
   if (!addr) return fail(BT_EINVAL, "no result pointer");
+  const uint64_t n = bytes ? (bytes + 255) / 256 * 256 : 256;
+  std::lock_guard<std::mutex> hold(r->blocks_lock);
+  auto k = r->kept.find(n);
+  if (k != r->kept.end() && !k->second.empty()) {  // a freed block of this size, reused in stream order
+    void *p = k->second.back();
+    k->second.pop_back();
+    r->blocks[p].kept = false;
+    *addr = (uint64_t)(uintptr_t)p;
+    r->kept_bytes -= n;
+    return BT_OK;
+  }
+  // Outside a capture, stream-ordered from the device's pool. Inside a capture, a plain allocation that outlives the
+  // graph: the graph keeps using it on every replay.
   void *p = nullptr;
-  uint64_t n = bytes ? (bytes + 255) / 256 * 256 : 256;
-  // Outside a capture, stream-ordered from the device's pool, so a free only waits for the launches queued before it.
-  // Inside a capture, a plain allocation that outlives the graph: the graph keeps using it on every replay.
   hipError_t e = r->capture_origin ? hipMalloc(&p, n) : hipMallocAsync(&p, n, r->stream);
+  if (e == hipErrorOutOfMemory && !r->capture_origin && r->kept_bytes) {  // give the kept blocks back and try again
+    (void)hipGetLastError();
+    if (int s = release_kept(r)) return s;
+    e = hipMallocAsync(&p, n, r->stream);
+  }
   if (e == hipErrorOutOfMemory) return fail(BT_ENOMEM, "out of device memory allocating %llu bytes", (unsigned long long)n);
   if (e != hipSuccess) return fail(BT_ESTATE, "allocating %llu bytes: %s", (unsigned long long)n, hipGetErrorString(e));
+  r->blocks[p] = {n, r->capture_origin != nullptr, false};
   *addr = (uint64_t)(uintptr_t)p;
   return BT_OK;
 }
@@ -195,11 +236,26 @@ int bt_free(bt_runtime *rt, uint64_t addr, int captured) {
   Runtime *r;
   if (int s = enter(rt, &r)) return s;
   if (!addr) return BT_OK;
+  void *p = (void *)(uintptr_t)addr;
+  std::lock_guard<std::mutex> hold(r->blocks_lock);
+  auto b = r->blocks.find(p);
+  if (b != r->blocks.end()) {
+    const uint64_t n = b->second.bytes;
+    if (b->second.kept) return fail(BT_EINVAL, "address %#llx freed twice", (unsigned long long)addr);
+    if (n <= KEEP_BLOCK && r->kept_bytes + n <= KEEP_TOTAL) {  // kept for the next allocation of its size
+      r->kept[n].push_back(p);
+      r->kept_bytes += n;
+      b->second.kept = true;
+      return BT_OK;
+    }
+    captured = b->second.plain;
+    r->blocks.erase(b);
+  }
   if (captured) {  // made while capturing: freed only once the stream has drained
     BT_HIP(hipStreamSynchronize(r->stream));
-    BT_HIP(hipFree((void *)(uintptr_t)addr));
+    BT_HIP(hipFree(p));
   } else {
-    BT_HIP(hipFreeAsync((void *)(uintptr_t)addr, r->stream));
+    BT_HIP(hipFreeAsync(p, r->stream));
   }
   return BT_OK;
 }

@@ -138,6 +138,29 @@ def test_wait_times_out_and_the_stream_drains(rt):
   with pytest.raises(ValueError): rt.sleep(11)
 
 
+def test_freed_blocks_are_reused_in_stream_order(rt):
+  # runtime.py:814-820's stream-ordered free, with the runtime keeping freed blocks for its next allocations of their
+  # size: the block comes back at once, a second free of it is refused, and a tensor whose block is handed out again
+  # while a launch that reads it is still queued (behind a two-tenths-of-a-second sleep) still gives that launch its
+  # old values
+  p = rt.dram_alloc(1000)
+  rt.dram_free(p)
+  assert rt.dram_alloc(1000) == p  # 1000 bytes round to 1024: the same block
+  q = rt.dram_alloc(5000)
+  assert q != p
+  rt.dram_free(q)
+  rt.dram_free(p)
+  with pytest.raises(ValueError, match="twice"): rt.dram_free(p)
+  rt.dram_alloc(1024), rt.dram_alloc(5120)  # both kept blocks taken again
+  vals = np.arange(-32, 32, dtype=np.float32).reshape(1, 64)
+  x = Tensor.of(rt, vals.tolist(), "fp32")
+  rt.sleep(0.2)
+  y = x.relu().realize()
+  del x
+  z = Tensor.of(rt, np.full((1, 64), 7.0).tolist(), "fp32")
+  assert np.array_equal(value(y)[0], np.maximum(vals, 0)) and np.array_equal(value(z)[0], np.full((1, 64), 7.0))
+
+
 def test_open_device(chip):
   # test_device.py:69 and docs/api.md:43-45: while a Chip holds the GPU, a second opener gets RuntimeError, so two live
   # runtimes never share one device (nor the device's static working memory); a GPU that isn't there is a ValueError.
