@@ -212,9 +212,10 @@ __global__ void __launch_bounds__(256) put_kernel(uint8_t *dst, int64_t dst_rows
   }
 }
 
-// One block per row i of x, for all batch entries at once. A later duplicate place wins (tensor.py:223-241): the block
-// first looks for a j > i with the same place, and writes nothing if there is one. Rows move in 16-byte pieces when
-// both sides allow it. For n up to PUT_SCAN rows; the scan is O(n) a block.
+// Blocks (i, y) for row i of x, for all batch entries at once, the y blocks of a row taking its pieces in turn (as
+// many as make 512 pieces a block, so a wide row is not left to one block). A later duplicate place wins
+// (tensor.py:223-241): each block first looks for a j > i with the same place, and writes nothing if there is one.
+// Rows move in 16-byte pieces when both sides allow it. For n up to PUT_SCAN rows; the scan is O(n) a block.
 constexpr int64_t PUT_SCAN = 8192;
 __global__ void __launch_bounds__(256) put_rows_kernel(uint8_t *dst, int64_t dst_rows, int64_t row_bytes,
                                                        int64_t dst_sb, int64_t dst_sr, const int32_t *ids, int64_t n,
@@ -231,15 +232,16 @@ __global__ void __launch_bounds__(256) put_rows_kernel(uint8_t *dst, int64_t dst
   if (found) later = 1;
   __syncthreads();
   if (later) return;
+  const int64_t first = (int64_t)blockIdx.y * blockDim.x + threadIdx.x, step = (int64_t)gridDim.y * blockDim.x;
   if (wide) {
     const int64_t pieces = row_bytes / 16;
-    for (int64_t e = threadIdx.x; e < batch * pieces; e += blockDim.x) {
+    for (int64_t e = first; e < batch * pieces; e += step) {
       const int64_t b = e / pieces, at = e % pieces * 16;
       *(uint4 *)(dst + b * dst_sb + p * dst_sr + at) = *(const uint4 *)(x + b * x_sb + i * x_sr + at);
     }
   } else {
     const int64_t halves = row_bytes / 2;
-    for (int64_t e = threadIdx.x; e < batch * halves; e += blockDim.x) {
+    for (int64_t e = first; e < batch * halves; e += step) {
       const int64_t b = e / halves, at = e % halves * 2;
       *(uint16_t *)(dst + b * dst_sb + p * dst_sr + at) = *(const uint16_t *)(x + b * x_sb + i * x_sr + at);
     }
@@ -410,9 +412,11 @@ int bt_put(bt_runtime *rt, int dtype, uint64_t dst, int64_t batch, int64_t dst_r
   if (n <= PUT_SCAN) {
     const int wide = row_bytes % 16 == 0 && dst % 16 == 0 && x % 16 == 0 && (dst_sb * size) % 16 == 0 &&
                      (dst_sr * size) % 16 == 0 && (x_sb * size) % 16 == 0 && (x_sr * size) % 16 == 0;
-    put_rows_kernel<<<(unsigned)n, 256, 0, r->stream>>>((uint8_t *)dst, dst_rows, row_bytes, dst_sb * size,
-                                                        dst_sr * size, (const int32_t *)ids, n, (const uint8_t *)x,
-                                                        x_sb * size, x_sr * size, batch, wide);
+    const int64_t units = batch * (wide ? row_bytes / 16 : row_bytes / 2);
+    const dim3 grid((unsigned)n, (unsigned)std::min<int64_t>((units + 511) / 512, 65535));
+    put_rows_kernel<<<grid, 256, 0, r->stream>>>((uint8_t *)dst, dst_rows, row_bytes, dst_sb * size, dst_sr * size,
+                                                 (const int32_t *)ids, n, (const uint8_t *)x, x_sb * size, x_sr * size,
+                                                 batch, wide);
   } else {
     int64_t pieces = (row_bytes / 2 + 255) / 256;
     put_kernel<<<(unsigned)(batch * pieces), 256, 0, r->stream>>>((uint8_t *)dst, dst_rows, row_bytes, dst_sb * size,

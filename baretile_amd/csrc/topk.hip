@@ -7,7 +7,9 @@
 // (LDS atomics), narrowing to the byte prefix that holds the k-th largest. Then every value above that key is taken,
 // and of the values equal to it the first in column order, as many as are still needed: a pass in column order,
 // 256 columns at a time, ranks the equal ones with a block-wide count. One wavefront sorts the k picks (bitonic, 64
-// lanes) by value, then column, and writes the values and their columns, or their labels when given.
+// lanes) by value, then column, and writes the values and their columns, or their labels when given. For k = 1 the
+// largest is found without the select: each thread's best of its columns, then the wave's by lane swaps, then the
+// block's.
 #include "common.h"
 
 namespace bt {
@@ -44,6 +46,32 @@ __global__ void __launch_bounds__(256) topk_kernel(const uint8_t *x, int64_t sb,
   const int part = (int)(unit % parts);
   const int64_t rr = unit / parts, r = rr % rows, b = rr / rows;
   const uint8_t *row = x + (b * sb + r * sr) * SZ + (int64_t)part * width * SZ;
+
+  if (k == 1) {  // the largest key, the first in column order: each thread's columns, then the wave's, then the block's
+    uint32_t bk = 0;
+    int32_t bc = 0x7FFFFFFF;
+    for (int c = tid; c < width; c += 256) {
+      const uint32_t key = order_key(value_bits<DT>(row, c));
+      if (before(key, c, bk, bc)) bk = key, bc = c;
+    }
+    for (int stride = 32; stride > 0; stride >>= 1) {
+      const uint32_t ok = __shfl_xor(bk, stride, 64);
+      const int32_t oc = __shfl_xor(bc, stride, 64);
+      if (before(ok, oc, bk, bc)) bk = ok, bc = oc;
+    }
+    if (lane == 0) cand_key[wib] = bk, cand_col[wib] = bc;
+    __syncthreads();
+    if (tid == 0) {
+      for (int w = 1; w < 4; w++)
+        if (before(cand_key[w], cand_col[w], bk, bc)) bk = cand_key[w], bc = cand_col[w];
+      const int64_t o = rr * (int64_t)parts + part;
+      if (DT == BT_BF16) ((uint16_t *)values)[o] = ((const uint16_t *)row)[bc];
+      else ((uint32_t *)values)[o] = ((const uint32_t *)row)[bc];
+      const int64_t c = (int64_t)part * width + bc;
+      ids[o] = labels ? labels[b * lsb + r * lsr + c] : (int32_t)c;
+    }
+    return;
+  }
 
   // radix select of the k-th largest key
   uint32_t prefix = 0, mask = 0, need = (uint32_t)k;

@@ -426,23 +426,65 @@ def argmax(logits):
 
 
 def generate(w, c, prompt, steps, size, feed=None, clock=None, replay=True):
-  """Greedy decode: prefill the prompt, then `steps` tokens, each step one replay of the recorded forward (jit).
-  With feed, step i is fed feed[i] instead of its own pick (the reference's NumPy-fed protocol, gpt2.py:147-161).
-  With clock (a list), the time.perf_counter() at which each pick is known is appended to it. replay=False runs every
-  step eagerly, one launch per kernel, as the first call of a jit does.
-  Returns (picks, per-step logits as float32 arrays)."""
+  """Greedy decode: prefill the prompt, then `steps` tokens. Each step after the first replays the recorded forward
+  (jit); on its own (no feed, replay), a step also picks its token on the device and feeds it, with the next place, to
+  the next step (greedy_steps), so the steps follow each other with no trip to the host, and the picks and logits are
+  read back once at the end. With feed, step i is fed feed[i] instead of its own pick (the reference's NumPy-fed
+  protocol, gpt2.py:147-161), and each step's logits come back to the host before the next. With clock (a list), the
+  time.perf_counter() at which each pick is known on the host is appended to it (on the device path, every pick after
+  the prompt's at the end). replay=False runs every step eagerly, one launch per kernel, as the first call of a jit
+  does. Returns (picks, per-step logits as float32 arrays)."""
   import time
   rt = w["norm"].rt
   caches = kv_cache(rt, c, size)
   logits = prefill(prompt, w, c, caches, len(prompt))
+  row = np.frombuffer(logits.tobytes(), np.float32).copy()
+  picks, outs = [int(np.argmax(row))], [row]
+  if clock is not None: clock.append(time.perf_counter())
+  if steps > 1 and feed is None and replay:
+    more, rows = greedy_steps(w, c, caches, picks[0], len(prompt), steps - 1)
+    if clock is not None: clock.extend([time.perf_counter()] * (steps - 1))
+    return picks + more, outs + rows
   step = (jit if replay else lambda f: f)(lambda i, p: forward(i, p, w, c, caches))
-  picks, outs = [], []
-  for s in range(steps):
+  for s in range(steps - 1):
+    tok = picks[-1] if feed is None else feed[s]
+    logits = step(Tensor.of(rt, [[tok]], "int32"), Tensor.of(rt, [[len(prompt) + s]], "int32"))
     row = np.frombuffer(logits.tobytes(), np.float32).copy()
     outs.append(row)
     picks.append(int(np.argmax(row)))
     if clock is not None: clock.append(time.perf_counter())
-    if s + 1 == steps: break
-    tok = picks[-1] if feed is None else feed[s]
-    logits = step(Tensor.of(rt, [[tok]], "int32"), Tensor.of(rt, [[len(prompt) + s]], "int32"))
   return picks, outs
+
+
+def greedy_steps(w, c, caches, pick, place, n):
+  """n greedy one-token steps after `pick` at `place`, chained on the device: each step's forward, the argmax of its
+  logits (topk over equal parts of the row, then over the parts' winners, which keeps the first of equal values, as
+  numpy's argmax does), and the writes of its pick and logits into rows kept by place and of the next step's token
+  and place into the step's own inputs, all as launches. The first step runs eagerly, the second is recorded into a
+  graph, and the rest replay it (as jit's calls do); nothing comes back to the host until the last step is done.
+  Returns (the n picks, their logits as float32 arrays)."""
+  from baretile_amd.tensor import Recording
+  rt, vocab = w["norm"].rt, w["embed.T"].cols
+  end = place + n
+  if end > caches[0].rows: raise ValueError(f"{n} steps from place {place} run past the cache's {caches[0].rows} rows")
+  ids, at = Tensor.of(rt, [[pick]], "int32"), Tensor.of(rt, [[place]], "int32")
+  picks, rows = Tensor(rt, end, 1, dtype="int32"), Tensor(rt, end, vocab, dtype="fp32")
+  parts = next(p for p in (192, 128, 96, 64, 48, 32, 16, 8, 4, 2, 1) if vocab % p == 0 and vocab // p >= 1)
+
+  def step():
+    logits = forward(ids, at, w, c, caches).reshape(1, vocab)
+    best, i = logits.topk(1, parts=parts)
+    if parts > 1: i = best.topk(1, labels=i)[1]
+    rows.put(at, logits)
+    picks.put(at, i)
+    ids.assign(i)
+    at.assign(at + 1)
+
+  step()
+  if n > 1:
+    rec = Recording(rt)
+    with rec: step()
+    for _ in range(n - 1): rec.send()
+  got = np.frombuffer(rt.download(picks[place:end, :].addr, 4 * n), np.int32)
+  out = np.frombuffer(rt.download(rows[place:end, :].addr, 4 * n * vocab), np.float32).reshape(n, vocab)
+  return [int(t) for t in got], list(out)  # the rows are views of one array read back once

@@ -179,8 +179,9 @@ def decode_leg(tokens=128, prompt_len=32, check=True, replay=True):
   vocab 49152) with random weights (linears N(0, 0.02), norms N(1, 0.1), embedding N(0, 1), seed 0), bfp8 linears
   and tied output layer, bf16 norms, embedding and KV cache, a 32-token uniform prompt and 128 new tokens.
 
-  The device runs the stream twice: autonomously (its own picks fed back; timed) and NumPy-fed (the oracle's picks fed,
-  gpt2.py:147-161). The oracle (oracle/llama_ref.py) runs the same decode on the host; its per-token time is the CPU
+  The device runs the stream twice: autonomously (timed: each step picks its token on the device and feeds it to the
+  next, llama.greedy_steps; tok/s counts the tokens after the prompt's pick over their time, and the steady rate is
+  the time that the second half of the tokens adds to a stream of the first half) and NumPy-fed (the oracle's picks fed, gpt2.py:147-161). The oracle (oracle/llama_ref.py) runs the same decode on the host; its per-token time is the CPU
   baseline. Returns a dict of tok/s, token identity and per-step logit error against the oracle."""
   from oracle import llama_ref as L
   from baretile_amd.models import llama
@@ -199,23 +200,26 @@ def decode_leg(tokens=128, prompt_len=32, check=True, replay=True):
     dw = llama.upload(rt, host, dc, places=size)
     rt.wait()
     llama.generate(dw, dc, prompt, 4, size, replay=replay)  # loads the code objects
-    clock = []
-    start = time.perf_counter()
-    toks, logits = llama.generate(dw, dc, prompt, tokens, size, clock=clock, replay=replay)
-    first = clock[0] - start  # prefill of the prompt and the first pick
-    steady = (clock[-1] - clock[2]) / (len(clock) - 3)  # replays of the recorded step (the 2nd step records)
+    def stream(n):  # n tokens: (picks, logits, prefill and first pick in s, the other n - 1 tokens in s)
+      clock = []
+      start = time.perf_counter()
+      toks, logits = llama.generate(dw, dc, prompt, n, size, clock=clock, replay=replay)
+      return toks, logits, clock[0] - start, clock[-1] - clock[0]
+    toks, logits, first, span = stream(tokens)
+    half = tokens // 2
+    steady = (span - stream(half)[3]) / (tokens - half)  # a token more in a longer stream: one replayed step
     # bytes a token reads: every bfp8 linear and the tied head, the norms, one embedding row, and the keys and values of
     # the positions it attends to (the cache holds prompt_len + step rows at step)
     wb = 30 * (576 * 960 + 576 * 576 + 576 * 3072 + 1536 * 576) * 1088 // 1024 + 576 * 49152 * 1088 // 1024
     ctx = prompt_len + (tokens - 1) / 2
     per_token = wb + 61 * 576 * 2 + 576 * 2 + int(30 * 2 * 3 * 64 * 2 * ctx)
-    out = {"tok/s": round((len(clock) - 1) / (clock[-1] - clock[0]), 1), "steady_tok/s": round(1 / steady, 1),
+    out = {"tok/s": round((tokens - 1) / span, 1), "steady_tok/s": round(1 / steady, 1),
            "roofline": {"bound": "hbm", "bytes_per_token": per_token, "unit": "GB/s",
                         "achieved": round(per_token / steady / 1e9, 1), "peak": PEAK_GBS,
                         "frac": round(per_token / steady / 1e9 / PEAK_GBS, 4),
                         "note": "the weights fit the 256 MB Infinity Cache, so this bound is loose: the step is "
                                 "launch- and latency-bound"},
-           "ms_per_token": round(1000 * (clock[-1] - clock[0]) / (len(clock) - 1), 4),
+           "ms_per_token": round(1000 * span / (tokens - 1), 4),
            "prefill_ms": round(1000 * first, 3), "tokens": tokens, "prompt": prompt_len, "graph_replay": replay,
            "kernels_per_token": None}
     caches = llama.kv_cache(rt, dc, size)

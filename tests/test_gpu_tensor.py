@@ -224,7 +224,7 @@ def test_errors(rt):
 def test_topk(rt):
   # test_kernels.py:2029-2062: the k largest of each row in the order of numpy's stable argsort of -x (the first of
   # equals first, -0 equal to 0); bf16 rows of several widths and a batch; fp32 rows in parts, then the best of the
-  # parts by their labels
+  # parts by their labels (k = 1 too: a greedy pick over a 49152-token vocabulary in 192 parts)
   rng = np.random.default_rng(37)
   for batch, rows, cols, k in ((1, 1, 128, 8), (1, 3, 16, 4), (1, 40, 40, 1), (2, 33, 256, 32), (1, 2, 49152, 64)):
     x = rng.normal(0, 2, (batch, rows, cols))
@@ -237,7 +237,7 @@ def test_topk(rt):
     got_values = np.array(values.tolist()).reshape(batch, rows, k)
     assert np.array_equal(got_ids, want), (batch, rows, cols, k)
     assert np.array_equal(got_values, np.take_along_axis(x, want, -1)), (batch, rows, cols, k)
-  for rows, cols, parts, k in ((5, 2560, 4, 64), (40, 1024, 2, 32)):
+  for rows, cols, parts, k in ((5, 2560, 4, 64), (5, 2560, 4, 1), (1, 49152, 192, 1), (40, 1024, 2, 32)):
     x = rng.normal(0, 3, (rows, cols)).astype(np.float32)
     x[0, 100] = x[0, cols // 2 + 3] = x[0].max() + 1  # a tie across parts
     values, ids = Tensor.of(rt, x, "fp32").topk(k, parts)
