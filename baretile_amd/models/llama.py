@@ -13,8 +13,10 @@ The numbers follow the reference's device path (llama.py:88-183):
 Llama-family only: Qwen's DeltaNet and experts, gpt-oss sinks and sliding windows other than the plain causal one
 are outside this backend's scope.
 """
+import collections.abc
 import json
 import math
+import operator
 import os
 from types import SimpleNamespace
 import numpy as np
@@ -427,13 +429,14 @@ def argmax(logits):
 
 def generate(w, c, prompt, steps, size, feed=None, clock=None, replay=True):
   """Greedy decode: prefill the prompt, then `steps` tokens. Each step after the first replays the recorded forward
-  (jit); on its own (no feed, replay), a step also picks its token on the device and feeds it, with the next place, to
-  the next step (greedy_steps), so the steps follow each other with no trip to the host, and the picks and logits are
-  read back once at the end. With feed, step i is fed feed[i] instead of its own pick (the reference's NumPy-fed
-  protocol, gpt2.py:147-161), and each step's logits come back to the host before the next. With clock (a list), the
-  time.perf_counter() at which each pick is known on the host is appended to it (on the device path, every pick after
-  the prompt's at the end). replay=False runs every step eagerly, one launch per kernel, as the first call of a jit
-  does. Returns (picks, per-step logits as float32 arrays)."""
+  (jit); on its own (no feed, replay), a step also picks its token on the device and feeds it, with the next place,
+  to the next step (greedy_steps), so the steps follow each other with no trip to the host; the picks come back once
+  at the end, and those steps' logits stay on the device until one of them is asked for (Logits). With feed, step i
+  is fed feed[i] instead of its own pick (the reference's NumPy-fed protocol, gpt2.py:147-161), and each step's
+  logits come back to the host before the next. With clock (a list), the time.perf_counter() at which each pick is
+  known on the host is appended to it (on the device path, every pick after the prompt's at the end). replay=False
+  runs every step eagerly, one launch per kernel, as the first call of a jit does. Returns (picks, per-step logits as
+  float32 arrays, in a list or a Logits sequence)."""
   import time
   rt = w["norm"].rt
   caches = kv_cache(rt, c, size)
@@ -444,7 +447,7 @@ def generate(w, c, prompt, steps, size, feed=None, clock=None, replay=True):
   if steps > 1 and feed is None and replay:
     more, rows = greedy_steps(w, c, caches, picks[0], len(prompt), steps - 1)
     if clock is not None: clock.extend([time.perf_counter()] * (steps - 1))
-    return picks + more, outs + rows
+    return picks + more, Logits(outs, rows)
   step = (jit if replay else lambda f: f)(lambda i, p: forward(i, p, w, c, caches))
   for s in range(steps - 1):
     tok = picks[-1] if feed is None else feed[s]
@@ -460,9 +463,11 @@ def greedy_steps(w, c, caches, pick, place, n):
   """n greedy one-token steps after `pick` at `place`, chained on the device: each step's forward, the argmax of its
   logits (topk over equal parts of the row, then over the parts' winners, which keeps the first of equal values, as
   numpy's argmax does), and the writes of its pick and logits into rows kept by place and of the next step's token
-  and place into the step's own inputs, all as launches. The first step runs eagerly, the second is recorded into a
-  graph, and the rest replay it (as jit's calls do); nothing comes back to the host until the last step is done.
-  Returns (the n picks, their logits as float32 arrays)."""
+  and place into the step's own inputs, all as launches. On the fused row kernels (row_fits), which keep nothing made
+  on first use, the step is recorded into a graph at once and every step is a replay of it; otherwise, or should the
+  capture refuse something the step makes the first time (an upload), the first step runs eagerly, as jit's first
+  call does, and the recording follows it. Nothing comes back to the host until the last step is done.
+  Returns (the n picks, their logits: an (n, vocab) fp32 view of a device tensor)."""
   from baretile_amd.tensor import Recording
   rt, vocab = w["norm"].rt, w["embed.T"].cols
   end = place + n
@@ -480,11 +485,38 @@ def greedy_steps(w, c, caches, pick, place, n):
     ids.assign(i)
     at.assign(at + 1)
 
-  step()
-  if n > 1:
-    rec = Recording(rt)
+  ran = 0
+  if not w.setdefault("row_fits", row_fits(w, c)):  # other kernels keep a block-float B's tiles from a first call
+    step()
+    ran = 1
+  rec = Recording(rt)
+  try:
     with rec: step()
-    for _ in range(n - 1): rec.send()
+  except RuntimeError:  # the step makes something the first time that a capture can't (an upload): run it first
+    if ran: raise
+    step()
+    rec, ran = Recording(rt), 1
+    with rec: step()
+  for _ in range(n - ran): rec.send()
   got = np.frombuffer(rt.download(picks[place:end, :].addr, 4 * n), np.int32)
-  out = np.frombuffer(rt.download(rows[place:end, :].addr, 4 * n * vocab), np.float32).reshape(n, vocab)
-  return [int(t) for t in got], list(out)  # the rows are views of one array read back once
+  return [int(t) for t in got], rows[place:end, :]
+
+
+class Logits(collections.abc.Sequence):
+  """Per-step logits as float32 arrays: those made on the host, then the rows of an fp32 device tensor (greedy_steps'
+  logits, kept on the device), read back whole the first time one is asked for (so the runtime must still be open)."""
+  def __init__(self, host, rows):
+    self.host, self.rows, self.read = list(host), rows, None
+
+  def __len__(self): return len(self.host) + self.rows.rows
+
+  def __getitem__(self, i):
+    if isinstance(i, slice): return [self[j] for j in range(*i.indices(len(self)))]
+    i = operator.index(i)
+    if i < 0: i += len(self)
+    if not 0 <= i < len(self): raise IndexError(f"step {i} of {len(self)}")
+    if i < len(self.host): return self.host[i]
+    if self.read is None:
+      t = self.rows
+      self.read = np.frombuffer(t.rt.download(t.addr, 4 * t.rows * t.cols), np.float32).reshape(t.rows, t.cols)
+    return self.read[i - len(self.host)]

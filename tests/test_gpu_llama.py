@@ -77,13 +77,18 @@ def test_smollm_config3_autonomous_decode_matches_numpy(rt):
   # own picks (gpt2.py:147-161's autonomous protocol; the device's steps are replays of the recorded step). The
   # device's stream equals the oracle's up to the first step whose NumPy top-2 margin is within twice the device's
   # largest logit error (on this seed no step is that close, so all 128), and under the NumPy-fed protocol every
-  # step's logits are within 3% of the largest (test_models.py:849)
+  # step's logits are within 3% of the largest (test_models.py:849). The autonomous steps pick their tokens on the
+  # device: where they picked what the oracle fed, their logits (kept on the device, read back when asked for) are
+  # the fed run's bit for bit, as both run the same kernels on the same inputs
   size = 160
   c, ref, dc, dw = setup(rt, 30, 49152, "bfp8", places=size, seed=0)
   prompt = [int(i) for i in np.random.default_rng(1).integers(0, 49152, 32)]
   want_toks, want_logits = L.greedy(prompt, 128, ref, c, size)
-  got_toks, _ = llama.generate(dw, dc, prompt, 128, size)
+  got_toks, got_logits = llama.generate(dw, dc, prompt, 128, size)
   _, fed_logits = llama.generate(dw, dc, prompt, 128, size, feed=want_toks)
+  assert len(got_logits) == 128 and len(got_logits[-3:]) == 3
+  same = next((s for s in range(128) if got_toks[s] != want_toks[s]), 128)
+  assert all(np.array_equal(got_logits[s], fed_logits[s]) for s in range(same)), same
   errs = [np.abs(g - w).max() for g, w in zip(fed_logits, want_logits)]
   assert all(e <= 0.03 * np.abs(w).max() for e, w in zip(errs, want_logits)), max(errs)
   close = [s for s, w in enumerate(want_logits) if np.diff(np.sort(w)[-2:])[0] <= 2 * max(errs)]
