@@ -1,6 +1,7 @@
 """llama.config / llama.load (llama.py:400-462) on checkpoints written here in the safetensors format: names,
 layouts (linear layers transposed for x @ w, q/k/v and gate/up fused, vectors as one-row matrices), the tied or
-separate output layer, BF16 kept bit for bit and F32 rounded to nearest even, shards. CPU only."""
+separate output layer, BF16 kept bit for bit and F32 rounded to nearest even, shards; and llama.Logits, generate's
+per-step logits read back from the device on first use. CPU only."""
 import json
 import os
 import struct
@@ -123,3 +124,29 @@ def test_load_takes_llama3_rope_scaling(tmp_path, style):
   assert all(np.array_equal(g, w) for g, w in zip(got, want))
   plain = llama.model(**{**vars(c), "rope": None})
   assert not np.array_equal(llama.frequencies(plain), llama.frequencies(c))
+
+
+def test_logits_read_the_device_rows_once_on_first_use():
+  # generate's per-step logits on the device path: the host-made rows first, then the device tensor's rows, read back
+  # in one transfer the first time any of them is asked for; indexing as a list's (negative, slices, IndexError)
+  data = np.arange(12, dtype=np.float32).reshape(3, 4)
+  reads = []
+
+  class Runtime:
+    def download(self, addr, nbytes):
+      reads.append((addr, nbytes))
+      return bytearray(data.tobytes())
+
+  class Rows:  # a (3, 4) fp32 view of a device tensor, as greedy_steps returns it
+    rt, addr, rows, cols = Runtime(), 4096, 3, 4
+
+  first = np.full(4, -1.0, np.float32)
+  got = llama.Logits([first], Rows())
+  assert len(got) == 4 and reads == []
+  assert got[0] is first and reads == []
+  assert np.array_equal(got[1], data[0]) and np.array_equal(got[-1], data[2])
+  assert [r.tolist() for r in got[1:3]] == data[:2].tolist()
+  assert reads == [(4096, 48)]
+  with pytest.raises(IndexError): got[4]
+  with pytest.raises(IndexError): got[-5]
+  assert len(list(got)) == 4
