@@ -85,6 +85,7 @@ int release_kept(Runtime *r) {
   for (auto &size : r->kept)
     for (void *p : size.second) {
       auto b = r->blocks.find(p);
+      if (b == r->blocks.end()) continue;  // every kept block is listed in blocks; this only guards the lookup
       if (b->second.plain) plain.push_back(p);
       else BT_HIP(hipFreeAsync(p, r->stream));
       r->blocks.erase(b);

@@ -209,7 +209,8 @@ def upload(rt, w, c, places=None):
   """Weights (NumPy float arrays, or Weights from load: their bf16 bits go up as they are) laid out for x @ w with
   q/k/v and gate/up fused, to the device (llama.py:479-495), one at a time. Matrices go to their precision's format
   and into the matmul's tiles once; norms and the embedding stay bf16; the tied output layer is embed.T in the head's
-  format. Adds the RoPE tables for `places` positions."""
+  format. Adds the RoPE tables for `places` positions: cos and sin are the two halves of the rows of one table,
+  cos_sin."""
   prec = c.precision
   out = {}
   for name, a in w.items():
@@ -229,7 +230,9 @@ def upload(rt, w, c, places=None):
     weight_format("embed.T", prec) if weight_format("embed.T", prec) != "bf16" else "bf16").columns()
   if places:
     cos, sin, turn = rotary(c, places)
-    out["cos"], out["sin"], out["turn"] = Tensor.of(rt, cos), Tensor.of(rt, sin), Tensor.of(rt, turn).columns()
+    both = Tensor.of(rt, np.concatenate([cos, sin], 1))  # a place's cos row, then its sin row: one gather for both
+    out["cos_sin"], out["cos"], out["sin"] = both, both[:, :cos.shape[1]], both[:, cos.shape[1]:]
+    out["turn"] = Tensor.of(rt, turn).columns()
   return out
 
 
@@ -389,7 +392,12 @@ def forward(ids, places, w, c, caches, every=False, slots=None):
   region's first row."""
   n = ids.cols
   x = w["embed"].gather(ids).float()
-  rot = (w["cos"].gather(places), w["sin"].gather(places), w["turn"])
+  row = n == 1 and not slots and w.setdefault("row_fits", row_fits(w, c))  # one token: the fused row kernels
+  if row and "cos_sin" in w:  # both tables' rows in one launch
+    both = w["cos_sin"].gather(places).reshape(2, w["cos"].cols)
+    rot = (both[0:1, :], both[1:2, :], w["turn"])
+  else:
+    rot = (w["cos"].gather(places), w["sin"].gather(places), w["turn"])
   firsts = None
   if not slots:
     rows, column = places, places.reshape(1, n, 1)
@@ -402,7 +410,7 @@ def forward(ids, places, w, c, caches, every=False, slots=None):
     column = (first + places * (places < part - 1)).realize().reshape(1, n, 1)  # a free slot's token: its first row
     firsts = first.reshape(1, n, 1)
   blocks = [block(w, l) for l in range(c.layers)]
-  if n == 1 and not slots and w.setdefault("row_fits", row_fits(w, c)):  # one token: the fused row kernels
+  if row:
     x = x.reshape(1, c.dim)
     for l in range(c.layers): x = row_layer(x, blocks[l], c, rot, column, caches[l], rows)
     return x.matmul_row(w["embed.T"], "fp32", norm=w["norm"], eps=c.eps).reshape(1, 1, w["embed.T"].cols)
@@ -459,30 +467,35 @@ def generate(w, c, prompt, steps, size, feed=None, clock=None, replay=True):
   return picks, outs
 
 
-def greedy_steps(w, c, caches, pick, place, n):
+def greedy_steps(w, c, caches, pick, place, n, stats=None):
   """n greedy one-token steps after `pick` at `place`, chained on the device: each step's forward, the argmax of its
   logits (topk over equal parts of the row, then over the parts' winners, which keeps the first of equal values, as
-  numpy's argmax does), and the writes of its pick and logits into rows kept by place and of the next step's token
-  and place into the step's own inputs, all as launches. On the fused row kernels (row_fits), which keep nothing made
-  on first use, the step is recorded into a graph at once and every step is a replay of it; otherwise, or should the
-  capture refuse something the step makes the first time (an upload), the first step runs eagerly, as jit's first
-  call does, and the recording follows it. Nothing comes back to the host until the last step is done.
-  Returns (the n picks, their logits: an (n, vocab) fp32 view of a device tensor)."""
+  numpy's argmax does) written as the next step's token, the logits into rows kept by place, and the next place, all
+  as launches; the picks are made again from the kept rows at the end, in one pass, by the same kernels. On the
+  fused row kernels (row_fits), which keep nothing made on first use, the step is recorded into a graph at once and
+  every step is a replay of it; otherwise, or should the capture refuse something the step makes the first time (an
+  upload), the first step runs eagerly, as jit's first call does, and the recording follows it. Nothing comes back
+  to the host until the last step is done.
+  Returns (the n picks, their logits: an (n, vocab) fp32 view of a device tensor); stats (a dict), if given, gets
+  the recorded step's kernel count as "kernels"."""
   from baretile_amd.tensor import Recording
   rt, vocab = w["norm"].rt, w["embed.T"].cols
   end = place + n
+  if n < 1 or place < 0: raise ValueError(f"greedy_steps takes at least one step from a place of 0 or more: {n}, {place}")
   if end > caches[0].rows: raise ValueError(f"{n} steps from place {place} run past the cache's {caches[0].rows} rows")
   ids, at = Tensor.of(rt, [[pick]], "int32"), Tensor.of(rt, [[place]], "int32")
-  picks, rows = Tensor(rt, end, 1, dtype="int32"), Tensor(rt, end, vocab, dtype="fp32")
+  best, rows = Tensor(rt, 1, 1, dtype="fp32"), Tensor(rt, end, vocab, dtype="fp32")
   parts = next(p for p in (192, 128, 96, 64, 48, 32, 16, 8, 4, 2, 1) if vocab % p == 0 and vocab // p >= 1)
 
-  def step():
+  def argmax(x, out=None):  # the first largest of each row, as x.rows x 1 (values, ids)
+    if parts == 1: return x.topk(1, out=out)
+    top, i = x.topk(1, parts=parts)
+    return top.topk(1, labels=i, out=out)
+
+  def step():  # the pick goes straight into the next step's token
     logits = forward(ids, at, w, c, caches).reshape(1, vocab)
-    best, i = logits.topk(1, parts=parts)
-    if parts > 1: i = best.topk(1, labels=i)[1]
+    argmax(logits, out=(best, ids))
     rows.put(at, logits)
-    picks.put(at, i)
-    ids.assign(i)
     at.assign(at + 1)
 
   ran = 0
@@ -498,8 +511,10 @@ def greedy_steps(w, c, caches, pick, place, n):
     rec, ran = Recording(rt), 1
     with rec: step()
   for _ in range(n - ran): rec.send()
-  got = np.frombuffer(rt.download(picks[place:end, :].addr, 4 * n), np.int32)
-  return [int(t) for t in got], rows[place:end, :]
+  if stats is not None: stats["kernels"] = rec.kernels
+  kept = rows[place:end, :]
+  got = np.frombuffer(argmax(kept)[1].tobytes(), np.int32)  # the same picks, made again from the kept logits at once
+  return [int(t) for t in got], kept
 
 
 class Logits(collections.abc.Sequence):

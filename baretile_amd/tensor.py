@@ -903,11 +903,12 @@ class Tensor:
     if not places._contiguous(): places = places.contiguous()
     return q, k, v, places, k.rep
 
-  def topk(self, k, parts=1, labels=None):
+  def topk(self, k, parts=1, labels=None, out=None):
     """(values, int32 indices) of the k largest entries of each row, descending, in one kernel (tensor.py:685-706):
     equal values keep column order (numpy's stable argsort of -x) and -0 equals 0; bf16 or fp32, k up to 64. With
     parts, each of that many equal parts of a row gives its k, labelled by original column; topk again with those
-    labels combines the parts."""
+    labels combines the parts. out: (values, indices) to write into, realized contiguous tensors of the result's
+    shape (self's dtype, then int32), which come back."""
     k, parts = operator.index(k), operator.index(parts)
     if k <= 0 or parts <= 0: raise ValueError("topk needs positive k and parts")
     if labels is not None and labels.rt is not self.rt: raise ValueError("topk's labels must use the same runtime")
@@ -923,9 +924,19 @@ class Tensor:
     if labels is not None:
       lab = labels.realize()
       if lab.sc != 1 or lab.rep != 1 or lab.cyc: lab = lab.contiguous()
-    values = Tensor(self.rt, x.rows, parts * k, batch=x.batch, dtype=x.dtype)
-    ids = Tensor(self.rt, x.rows, parts * k, batch=x.batch, dtype="int32")
-    values.lead = ids.lead = self.lead
+    if out is None:
+      values = Tensor(self.rt, x.rows, parts * k, batch=x.batch, dtype=x.dtype)
+      ids = Tensor(self.rt, x.rows, parts * k, batch=x.batch, dtype="int32")
+      values.lead = ids.lead = self.lead
+    else:
+      values, ids = out
+      fits = lambda t, dt: (isinstance(t, Tensor) and t.rt is self.rt and t.op is None and t._contiguous() and
+                            (t.batch, t.rows, t.cols, t.dtype) == (x.batch, x.rows, parts * k, dt))
+      if not (fits(values, x.dtype) and fits(ids, "int32")):
+        raise ValueError(f"topk's out must be realized contiguous ({x.batch}, {x.rows}, {parts * k}) tensors, "
+                         f"{x.dtype} and int32")
+      _written(values.storage)
+      _written(ids.storage)
     self.rt.run("topk", "topk", _lib.DTYPES[x.dtype], x.addr, x.batch, x.rows, x.cols, x.sb if x.batch > 1 else 0, x.sr,
                 parts, k, lab.addr if lab is not None else 0, (lab.sb if lab.batch > 1 else 0) if lab is not None else 0,
                 lab.sr if lab is not None else 0, values.addr, ids.addr, reads=_bytes(x, lab))
@@ -1311,6 +1322,7 @@ class Recording:
   def __init__(self, rt):
     self.rt, self.graph, self.storages, self.held, self.active = rt, None, [], [], False
     self.unchecked = set()  # ids of block-float storages laid out as a matmul's B with no exponent check
+    self.kernels = 0  # launches captured
 
   def __enter__(self):
     if self.rt.recording is not None: raise RuntimeError("cannot nest recordings on the same runtime")
@@ -1318,10 +1330,12 @@ class Recording:
     self.rt.recording = self
     self.active = True
     _lib.call("graph_begin", self.rt.handle)
+    self.kernels = -self.rt.launches
     return self
 
   def __exit__(self, kind, *_):
     g = ctypes.c_void_p()
+    self.kernels += self.rt.launches
     try: _lib.call("graph_end", self.rt.handle, ctypes.byref(g))
     finally:
       # memory let go during the capture may still be read by the graph: it is freed with the graph

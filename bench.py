@@ -221,10 +221,9 @@ def decode_leg(tokens=128, prompt_len=32, check=True, replay=True):
            "ms_per_token": round(1000 * span / (tokens - 1), 4),
            "prefill_ms": round(1000 * first, 3), "tokens": tokens, "prompt": prompt_len, "graph_replay": replay,
            "kernels_per_token": None}
-    caches = llama.kv_cache(rt, dc, size)
-    base = rt.launches
-    llama.greedy_steps(dw, dc, caches, prompt[0], 0, 1)
-    out["kernels_per_token"] = rt.launches - base - 1  # the recorded step's launches (its one replay counts one more)
+    caches, stats = llama.kv_cache(rt, dc, size), {}
+    llama.greedy_steps(dw, dc, caches, prompt[0], 0, 1, stats)
+    out["kernels_per_token"] = stats["kernels"]  # what a replayed step holds
     del caches
     if not check: return out, None
     t0 = time.perf_counter()

@@ -251,6 +251,15 @@ def test_topk(rt):
     assert np.array_equal(np.array(values.tolist(), np.float32), np.take_along_axis(x, want, -1))
   with pytest.raises(ValueError): Tensor.of(rt, x, "fp32").topk(65)
   with pytest.raises(ValueError): Tensor.of(rt, x, "fp32").topk(4, parts=3)
+  # out: the same results written into given tensors, which come back; a wrong shape or dtype is refused
+  t = Tensor.of(rt, x, "fp32")
+  values, ids = t.topk(3, parts=2)
+  out = (Tensor.zeros(rt, x.shape[0], 6, dtype="fp32"), Tensor.zeros(rt, x.shape[0], 6, dtype="int32"))
+  got = t.topk(3, parts=2, out=out)
+  assert got[0] is out[0] and got[1] is out[1]
+  assert out[0].tolist() == values.tolist() and out[1].tolist() == ids.tolist()
+  with pytest.raises(ValueError, match="out"): t.topk(3, parts=2, out=(out[1], out[0]))
+  with pytest.raises(ValueError, match="out"): t.topk(2, parts=2, out=out)
 
 
 def _weights(rt, k, n, fmt, seed):
