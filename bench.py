@@ -181,8 +181,9 @@ def decode_leg(tokens=128, prompt_len=32, check=True, replay=True):
 
   The device runs the stream twice: autonomously (timed: each step picks its token on the device and feeds it to the
   next, llama.greedy_steps; tok/s counts the tokens after the prompt's pick over their time, and the steady rate is
-  the time that the second half of the tokens adds to a stream of the first half) and NumPy-fed (the oracle's picks fed, gpt2.py:147-161). The oracle (oracle/llama_ref.py) runs the same decode on the host; its per-token time is the CPU
-  baseline. Returns a dict of tok/s, token identity and per-step logit error against the oracle."""
+  the time that the second half of the tokens adds to a stream of the first half) and NumPy-fed (the oracle's picks
+  fed, gpt2.py:147-161). The oracle (oracle/llama_ref.py) runs the same decode on the host; its per-token time is the
+  CPU baseline. Returns a dict of tok/s, token identity and per-step logit error against the oracle."""
   from oracle import llama_ref as L
   from baretile_amd.models import llama
   from baretile_amd.runtime import Runtime
@@ -222,8 +223,14 @@ def decode_leg(tokens=128, prompt_len=32, check=True, replay=True):
            "prefill_ms": round(1000 * first, 3), "tokens": tokens, "prompt": prompt_len, "graph_replay": replay,
            "kernels_per_token": None}
     caches, stats = llama.kv_cache(rt, dc, size), {}
-    llama.greedy_steps(dw, dc, caches, prompt[0], 0, 1, stats)
-    out["kernels_per_token"] = stats["kernels"]  # what a replayed step holds
+    if replay:  # what a replayed step holds
+      llama.greedy_steps(dw, dc, caches, prompt[0], 0, 1, stats)
+      out["kernels_per_token"] = stats["kernels"]
+    else:  # the launches of one eager forward (no graph, as under a kernel trace)
+      from baretile_amd.tensor import Tensor
+      base = rt.launches
+      llama.forward(Tensor.of(rt, [[prompt[0]]], "int32"), Tensor.of(rt, [[0]], "int32"), dw, dc, caches).realize()
+      out["kernels_per_token"] = rt.launches - base
     del caches
     if not check: return out, None
     t0 = time.perf_counter()
