@@ -42,7 +42,7 @@ int bt_close(bt_runtime *rt);
  * launches queued before the free are done (runtime.py:814-820). `captured` marks memory allocated while a graph
  * capture was open. The runtime keeps freed blocks of up to 256 MB, 4 GB in all, for its next allocations of the
  * same size (one stream, so reuse is in stream order), and gives them back when it closes or when an allocation
- * outside a capture runs out of memory. */
+ * outside a capture runs out of memory. Freeing a kept block again returns BT_EINVAL. */
 int bt_alloc(bt_runtime *rt, uint64_t bytes, uint64_t *addr);
 int bt_free(bt_runtime *rt, uint64_t addr, int captured);
 /* Tensor.frombytes / tobytes transfers (tensor.py:113-204, kernels.py:1374-1453 upload/readback_kernel). Both
