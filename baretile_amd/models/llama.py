@@ -306,6 +306,16 @@ def block(w, l):
   return {k[len(pre):]: v for k, v in w.items() if k.startswith(pre)}
 
 
+def blocks(w, layers):
+  """block(w, l) for every l < layers, from one pass over the weights (not one a layer)."""
+  out = [{} for _ in range(layers)]
+  for k, v in w.items():
+    if k.startswith("layers."):
+      l, _, name = k[7:].partition(".")
+      if l.isdigit() and int(l) < layers: out[int(l)][name] = v
+  return out
+
+
 def layer(x, p, c, rot, places, cache, rows, firsts=None):
   """Attention, then the MLP, each after an RMSNorm and added onto the fp32 stream in its own kernel (llama.py:106-130)."""
   x = (x + attention(rms(x, p["input_layernorm"], c), p, c, rot, places, cache, rows, firsts)).realize()
@@ -409,12 +419,12 @@ def forward(ids, places, w, c, caches, every=False, slots=None):
     rows = (places + first).realize()  # each token's cache row
     column = (first + places * (places < part - 1)).realize().reshape(1, n, 1)  # a free slot's token: its first row
     firsts = first.reshape(1, n, 1)
-  blocks = [block(w, l) for l in range(c.layers)]
+  ps = blocks(w, c.layers)
   if row:
     x = x.reshape(1, c.dim)
-    for l in range(c.layers): x = row_layer(x, blocks[l], c, rot, column, caches[l], rows)
+    for l in range(c.layers): x = row_layer(x, ps[l], c, rot, column, caches[l], rows)
     return x.matmul_row(w["embed.T"], "fp32", norm=w["norm"], eps=c.eps).reshape(1, 1, w["embed.T"].cols)
-  for l in range(c.layers): x = layer(x, blocks[l], c, rot, column, caches[l], rows, firsts)
+  for l in range(c.layers): x = layer(x, ps[l], c, rot, column, caches[l], rows, firsts)
   h = rms(x, w["norm"], c)
   if not (every or slots) and n > 1: h = h[:, n - 1:n, :]  # the last token's row
   return h.matmul(w["embed.T"], "fp32")

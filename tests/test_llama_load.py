@@ -150,3 +150,11 @@ def test_logits_read_the_device_rows_once_on_first_use():
   with pytest.raises(IndexError): got[4]
   with pytest.raises(IndexError): got[-5]
   assert len(list(got)) == 4
+
+
+def test_blocks_split_the_weights_as_block_does():
+  # forward's one pass over the weights gives each layer what block(w, l) gives it (layers past the count left out)
+  w = {f"layers.{l}.{n}": (l, n) for l in range(12) for n in ("qkv_proj", "input_layernorm")}
+  w.update({"embed": 0, "norm": 1, "layers.x.odd": 2, "layers.12.extra": 3})
+  got = llama.blocks(w, 12)
+  assert len(got) == 12 and all(got[l] == llama.block(w, l) for l in range(12))
