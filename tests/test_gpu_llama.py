@@ -117,8 +117,12 @@ def test_chunked_prefill_matches_numpy(rt, mode):
   assert np.abs(got - want).max() < 0.03 * np.abs(want).max(), np.abs(got - want).max()
 
 
-def test_jit_decode_matches_eager(rt):
+@pytest.mark.parametrize("row", [True, False])
+def test_jit_decode_matches_eager(rt, row):
+  # generate's steps, picked on the device and replayed from a graph, against a host loop of eager forwards; also
+  # with the fused row kernels turned off (the per-operation kernels, a first step run eagerly before the recording)
   c, ref, dc, dw = setup(rt, 2, 256, "bfp8", places=64)
+  dw["row_fits"] = row
   prompt = [3, 1, 4, 1, 5, 9, 2, 6]
   a, _ = llama.generate(dw, dc, prompt, 6, 64)
   caches = llama.kv_cache(rt, dc, 64)
