@@ -477,10 +477,15 @@ def generate(w, c, prompt, steps, size, feed=None, clock=None, replay=True):
   return picks, outs
 
 
+def argmax_parts(vocab):
+  """The equal parts an on-device argmax splits a row of logits into: a block each, then one over their winners."""
+  return max(p for p in range(1, 257) if vocab % p == 0)
+
+
 def greedy_steps(w, c, caches, pick, place, n, stats=None):
   """n greedy one-token steps after `pick` at `place`, chained on the device: each step's forward, the argmax of its
-  logits (topk over equal parts of the row, then over the parts' winners, which keeps the first of equal values, as
-  numpy's argmax does) written as the next step's token, the logits into rows kept by place, and the next place, all
+  logits (topk over up to 256 equal parts of the row, then over the parts' winners, which keeps the first of equal
+  values, as numpy's argmax does) written as the next step's token, the logits into rows kept by place, and the next place, all
   as launches; the picks are made again from the kept rows at the end, in one pass, by the same kernels. On the
   fused row kernels (row_fits), which keep nothing made on first use, the step is recorded into a graph at once and
   every step is a replay of it; otherwise, or should the capture refuse something the step makes the first time (an
@@ -495,7 +500,7 @@ def greedy_steps(w, c, caches, pick, place, n, stats=None):
   if end > caches[0].rows: raise ValueError(f"{n} steps from place {place} run past the cache's {caches[0].rows} rows")
   ids, at = Tensor.of(rt, [[pick]], "int32"), Tensor.of(rt, [[place]], "int32")
   best, rows = Tensor(rt, 1, 1, dtype="fp32"), Tensor(rt, end, vocab, dtype="fp32")
-  parts = next(p for p in (192, 128, 96, 64, 48, 32, 16, 8, 4, 2, 1) if vocab % p == 0 and vocab // p >= 1)
+  parts = argmax_parts(vocab)
 
   def argmax(x, out=None):  # the first largest of each row, as x.rows x 1 (values, ids)
     if parts == 1: return x.topk(1, out=out)
